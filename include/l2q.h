@@ -1,0 +1,202 @@
+/* l2q.h - C ABI of the MI355X batch-1 quantized Llama-2 decode path.
+ *
+ * Two layers of entry points, all plain C types (no torch, no HIP types):
+ *
+ *   Engine ABI - what the host runner calls once per position.  It replaces
+ *   the reference's single seam, `float* forward(Transformer*, int token,
+ *   int pos)` (v1-int8-vnni/runq.c:320), together with its GPU counterparts
+ *   `forward_step` (v3-cuda-kvcache/run.cu:422) and `run_token`
+ *   (v5-cuda-fused/run.cu:682-695).
+ *
+ *   Op ABI - one GPU op per call, device pointers in, device pointers out,
+ *   enqueued on a caller-supplied HIP stream (passed as `void*`; NULL is the
+ *   null stream).  These replace the reference's kernel launchers
+ *   (`launch_matmul` v5-cuda-fused/run.cu:584, `launch_rmsnorm_quant` :590,
+ *   `launch_quant` v3-cuda-kvcache/run.cu:403) and are what the parity and
+ *   microbenchmark harnesses drive.
+ *
+ * Every function returns L2Q_OK (0) or a negative status; l2q_last_error()
+ * then returns a human-readable message (thread-local).  The library never
+ * calls exit(); the runner maps a failure to the reference's fail-fast exit
+ * (runq.c:258-275, v5-cuda-fused/run.cu:50-52).
+ *
+ * Quantization conventions shared by every entry point:
+ *   - a "group" is G consecutive elements of one row (G = 32 for reference
+ *     files, 64 for the Llama-2-7B configurations);
+ *   - activations are Q8: int8 q in [-127,127] plus one fp32 scale per group,
+ *     s = amax/127 (1e-8 if amax == 0), q = round-half-even(x/s)
+ *     (runq.c:117-139);
+ *   - INT8 weights are signed int8 (the on-disk +128 bias removed),
+ *     row-major [rows][cols], scales [rows][cols/G];
+ *   - INT4 weights are packed two per byte, low nibble = even column,
+ *     two's complement, [rows][cols/2], scales [rows][cols/G]
+ *     (tools/quantize_int4.py:38-51).
+ */
+#ifndef L2Q_H
+#define L2Q_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define L2Q_OK              0
+#define L2Q_ERR_ARG        -1   /* bad argument or unsupported shape        */
+#define L2Q_ERR_HIP        -2   /* a HIP runtime call failed                */
+#define L2Q_ERR_FORMAT     -3   /* weights image too short / inconsistent   */
+#define L2Q_ERR_NOMEM      -4   /* device allocation failed                 */
+#define L2Q_ERR_STATE      -5   /* engine used out of order (pos > max)     */
+
+/* Model hyper-parameters, byte-identical to the 7 x int32 header of the
+ * reference checkpoints (runq.c:33-41, v5-cuda-fused/run.cu:57-59).
+ * vocab_size is passed positive; the checkpoint's sign convention (negative
+ * = unshared classifier) is resolved by the reader. */
+typedef struct {
+    int dim;
+    int hidden_dim;
+    int n_layers;
+    int n_heads;
+    int n_kv_heads;
+    int vocab_size;
+    int seq_len;
+} l2q_config;
+
+/* ------------------------------------------------------------------------
+ * Errors / device
+ * ---------------------------------------------------------------------- */
+
+/* Message for the last failing call on this thread ("" if none). */
+const char* l2q_last_error(void);
+
+/* Number of visible HIP devices (0 when none); never fails. */
+int l2q_device_count(void);
+
+/* ------------------------------------------------------------------------
+ * Engine ABI
+ * ---------------------------------------------------------------------- */
+
+typedef struct l2q_engine l2q_engine;
+
+/* Build an engine from a checkpoint's tensor section.
+ *
+ * `weights` points at the first byte after the file header (the token
+ * embedding table) of a QLL8 (wbits = 8) or QLL4 (wbits = 4) checkpoint,
+ * usually inside the caller's mmap; `weights_bytes` is how many bytes are
+ * readable there.  Tensor order and sizes follow runq.c:230-253 /
+ * v5-cuda-fused/run.cu:534-551 with `group` elements per scale.  The engine
+ * copies everything it needs to the current device (one allocation, laid out
+ * for the kernels), so the caller may unmap afterwards.
+ *
+ * `max_steps` sizes the KV cache (positions 0..max_steps-1), as the GPU
+ * reference runners do (v5-cuda-fused/run.cu:1147-1150); it is clamped to
+ * cfg->seq_len.  Replaces read_checkpoint/memory_map_weights/
+ * malloc_run_state (runq.c:190-283) and load_weights/alloc_state/build_graph
+ * (v5-cuda-fused/run.cu:534-582, 671-679). */
+int l2q_engine_create(const l2q_config* cfg, const void* weights,
+                      size_t weights_bytes, int wbits, int group,
+                      int max_steps, l2q_engine** out);
+
+/* One decode step: embed `token`, run every layer at position `pos`
+ * (appending its K/V), final norm and classifier.  If `logits` is not NULL
+ * the vocab_size fp32 logits are copied into it (host memory).  Synchronous.
+ * Positions must be fed in order 0,1,2,... as in the reference loops
+ * (runq.c:697-711); pos >= max_steps is L2Q_ERR_STATE.
+ * Replaces forward() (runq.c:320-421) and run_token() (v5:682-695). */
+int l2q_engine_forward(l2q_engine* e, int token, int pos, float* logits);
+
+/* Same step, but the greedy choice (first index of the maximum logit,
+ * sample_argmax runq.c:578-585) is made on the device and only the index
+ * crosses to the host. */
+int l2q_engine_forward_argmax(l2q_engine* e, int token, int pos, int* next);
+
+/* Diagnostic step that runs the same kernels one launch at a time (no
+ * graph) and copies the residual stream after the embedding and after every
+ * layer into `x_layers` ([n_layers + 1][dim] fp32, host) and, if not NULL,
+ * the logits.  Used for per-layer parity checks. */
+int l2q_engine_forward_debug(l2q_engine* e, int token, int pos,
+                             float* x_layers, float* logits);
+
+/* Replay the captured step `n_steps` times at positions pos0 .. pos0+n-1
+ * with token ids `tokens` (host array, length n_steps), without copying
+ * logits back, and report the elapsed device time in milliseconds measured
+ * with HIP events on the engine's stream.  Benchmark entry point. */
+int l2q_engine_time_steps(l2q_engine* e, const int* tokens, int pos0,
+                          int n_steps, double* elapsed_ms);
+
+/* Device bytes held by the engine (weights + KV cache + activations). */
+size_t l2q_engine_device_bytes(const l2q_engine* e);
+
+void l2q_engine_destroy(l2q_engine* e);
+
+/* ------------------------------------------------------------------------
+ * Op ABI (device pointers, asynchronous on `stream`)
+ * ---------------------------------------------------------------------- */
+
+/* Q8 activation quantize of x[n] into xq[n], xs[n/group].
+ * runq.c:117-139 (quantize_act), v3-cuda-kvcache/run.cu:104-129. */
+int l2q_quantize_act(const float* x, int n, int group,
+                     int8_t* xq, float* xs, void* stream);
+
+/* INT8 GEMV: out[r] = sum_b ws[r,b] * xs[b] * dot_b(r), where
+ * dot_b(r) = sum_{j<group} w[r, b*group+j] * xq[b*group+j] (exact int32).
+ * If `dots` is not NULL the int32 group dots are written to
+ * dots[r*(cols/group) + b].  w is signed int8 [rows][cols].
+ * runq.c:142-159 (matmul_q8), v3-cuda-kvcache/run.cu:177-202. */
+int l2q_gemv_q8(float* out, const int8_t* xq, const float* xs,
+                const int8_t* w, const float* ws, int rows, int cols,
+                int group, int32_t* dots, void* stream);
+
+/* INT4 GEMV, same contract with w packed [rows][cols/2] (low nibble = even
+ * column, two's complement).  v5-cuda-fused/run.cu:252-330 with the dequant
+ * of tools/quantize_int4.py:38-51. */
+int l2q_gemv_q4(float* out, const int8_t* xq, const float* xs,
+                const uint8_t* w, const float* ws, int rows, int cols,
+                int group, int32_t* dots, void* stream);
+
+/* Remove the +128 bias of on-disk QLL8 weights (u8 -> s8), n bytes.
+ * v3-cuda-kvcache/run.cu:167-175. `dst` may equal `src`. */
+int l2q_unbias_q8(const uint8_t* src, int8_t* dst, size_t n, void* stream);
+
+/* Fused residual-add + RMSNorm + Q8 quantize of one vector of n floats:
+ *   v = x + (resid ? resid : 0);  if (xout) xout = v;
+ *   o = w * (inv * v), inv = 1/sqrtf(sum(v^2)/n + 1e-5f);  quantize(o).
+ * runq.c:294-305 (rmsnorm) + :117-139, v5-cuda-fused/run.cu:120-175. */
+int l2q_rmsnorm_quant(const float* x, const float* resid, float* xout,
+                      const float* w, int n, int group,
+                      int8_t* xq, float* xs, void* stream);
+
+/* SwiGLU + Q8 quantize: g = hb * (1/(1+expf(-hb))) * hb2 over n elements.
+ * runq.c:404-412, v5-cuda-fused/run.cu:180-200.  If `gout` is not NULL the
+ * fp32 product is stored there as well. */
+int l2q_swiglu_quant(const float* hb, const float* hb2, int n, int group,
+                     int8_t* xq, float* xs, float* gout, void* stream);
+
+/* RoPE on q (all heads) and k, then append k and v at position `pos` of
+ * one layer's cache.  `rope` is the [max_t][head_size/2][2] (cos, sin)
+ * table from l2q_rope_table (device copy).  q is rotated in place.
+ * Cache layout: [n_kv_heads][max_t][head_size] fp32 for K and for V.
+ * runq.c:340-365, v5-cuda-fused/run.cu:332-345, 413-439. */
+int l2q_rope_kv_append(float* q, const float* k, const float* v,
+                       float* kcache, float* vcache, const float* rope,
+                       int pos, int n_heads, int n_kv_heads, int head_size,
+                       int max_t, void* stream);
+
+/* Single-query multi-head attention over positions 0..pos of one layer's
+ * cache (layout as above): out[h*hs + i] = sum_t softmax_t(q_h.k_t /
+ * sqrtf(hs)) v_t[i], kv head = h / (n_heads/n_kv_heads).
+ * runq.c:367-391 + softmax :307-318, v5-cuda-fused/run.cu:441-499. */
+int l2q_attention(const float* q, const float* kcache, const float* vcache,
+                  float* out, int pos, int n_heads, int n_kv_heads,
+                  int head_size, int max_t, void* stream);
+
+/* Host helper: fill the RoPE (cos, sin) table for positions 0..max_t-1 with
+ * the reference's float expressions (runq.c:351-356), so that device and
+ * CPU rotations are bit-identical.  `table` has max_t*head_size floats. */
+void l2q_rope_table(float* table, int max_t, int head_size);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* L2Q_H */

@@ -1,0 +1,127 @@
+// device.h - gfx950 device helpers shared by the decode kernels.
+//
+// Wave64 reductions, the Q8 group quantizer (runq.c:117-139 semantics, in
+// registers), int8/int4 group dot products on v_dot4_i32_i8, and the
+// per-group accumulation formula of runq.c:150-156.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#define L2Q_WAVE 64
+
+namespace l2q {
+
+// Launch-shape limits shared by the kernels and their host launchers.
+constexpr int kNormThreads = 1024;   // fused RMSNorm: one workgroup
+constexpr int kNormMaxPer = 8;       // elements per thread -> n <= 8192
+constexpr int kAttnThreads = 256;    // attention workgroup
+constexpr int kAttnTile = 64;        // positions per LDS-staged K tile
+constexpr int kAttnMaxHs = 256;      // largest head size
+
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+
+// 128-bit streaming load (non-temporal: weights are read once per step).
+__device__ __forceinline__ uint4 load_stream(const void* p) {
+    u32x4 v = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
+    return make_uint4(v.x, v.y, v.z, v.w);
+}
+
+// ---------------------------------------------------------------------------
+// Wave64 reductions (xor butterflies: every lane ends with the result).
+
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, L2Q_WAVE);
+    return v;
+}
+
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, L2Q_WAVE));
+    return v;
+}
+
+// Reduction over aligned groups of `W` consecutive lanes (W a power of two
+// <= 64): every lane gets the result of its own group.
+template <int W>
+__device__ __forceinline__ float group_max(float v) {
+#pragma unroll
+    for (int o = W / 2; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, L2Q_WAVE));
+    return v;
+}
+
+template <int W>
+__device__ __forceinline__ float group_sum(float v) {
+#pragma unroll
+    for (int o = W / 2; o > 0; o >>= 1) v += __shfl_xor(v, o, L2Q_WAVE);
+    return v;
+}
+
+template <int W>
+__device__ __forceinline__ int group_isum(int v) {
+#pragma unroll
+    for (int o = W / 2; o > 0; o >>= 1) v += __shfl_xor(v, o, L2Q_WAVE);
+    return v;
+}
+
+// ---------------------------------------------------------------------------
+// Q8 activation quantization of one value given its group's amax:
+// s = amax/127 (1e-8 if 0), q = clamp(rint(x/s), +-127).  Division is the
+// correctly rounded IEEE one (HIP default; never built with fast-math) and
+// rintf is round-half-even, as lrintf in the reference.
+
+__device__ __forceinline__ float q8_scale(float amax) {
+    float s = amax / 127.0f;
+    return s == 0.0f ? 1e-8f : s;
+}
+
+__device__ __forceinline__ int q8_value(float x, float s) {
+    float r = rintf(x / s);
+    r = fminf(fmaxf(r, -127.0f), 127.0f);
+    return (int)r;
+}
+
+// runq.c:137: xt = s * 128 * sum(q), the bias-correction term of the
+// unsigned-weight dot product.
+__device__ __forceinline__ float q8_bias_term(float s, int sumq) {
+    return s * 128.0f * (float)sumq;
+}
+
+// runq.c:155 for one group, as GCC -O3 -march=native compiles it (two FMAs):
+//   sum += ws * (xs * d_u8 - xt),   d_u8 = d + 128*sum(q)
+// d_u8 is the dot the reference's VPDPBUSD produces on +128-biased weights;
+// with it every per-group term is bit-identical to the reference's.
+__device__ __forceinline__ float group_accumulate(float acc, float ws, float xs, float xt,
+                                                 int d, int sumq) {
+    int du8 = d + 128 * sumq;
+    return __builtin_fmaf(ws, __builtin_fmaf(xs, (float)du8, -xt), acc);
+}
+
+// ---------------------------------------------------------------------------
+// Dot products on v_dot4_i32_i8.
+
+__device__ __forceinline__ int dot4(int a, int b, int c) {
+    return __builtin_amdgcn_sdot4(a, b, c, false);
+}
+
+// Split the activation bytes of one packed-int4 dword's columns into the
+// even columns (x0,x2,x4,x6) and odd columns (x1,x3,x5,x7).  a = x0..x3,
+// b = x4..x7 (little-endian bytes).  v_perm_b32 selects bytes of {b:a}.
+__device__ __forceinline__ int even_bytes(int a, int b) {
+    return (int)__builtin_amdgcn_perm((unsigned)b, (unsigned)a, 0x06040200u);
+}
+__device__ __forceinline__ int odd_bytes(int a, int b) {
+    return (int)__builtin_amdgcn_perm((unsigned)b, (unsigned)a, 0x07050301u);
+}
+
+// Eight packed int4 weights (w) against eight activations given as their
+// even/odd byte splits: the nibbles are moved into the high half of each
+// byte, where they read as signed int8 values 16*q, and the dot is exact
+// 16x the true one (|16*q*x| sums stay far below 2^31).
+__device__ __forceinline__ int dot8_q4_x16(unsigned w, int xe, int xo, int c) {
+    int hi = (int)(w & 0xF0F0F0F0u);          // 16 * odd columns
+    int lo = (int)((w << 4) & 0xF0F0F0F0u);   // 16 * even columns
+    return dot4(hi, xo, dot4(lo, xe, c));
+}
+
+}  // namespace l2q

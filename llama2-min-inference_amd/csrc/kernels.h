@@ -1,0 +1,316 @@
+// kernels.h - the non-GEMV decode kernels: Q8 quantize, fused residual +
+// RMSNorm + quantize, SwiGLU + quantize, RoPE + KV append, split-context
+// single-query attention and the device argmax.
+//
+// Positions: kernels used inside the captured decode graph read the token
+// and position from device memory (`meta` = {token, pos}), so one graph
+// serves every step; the op ABI passes them by value (meta == NULL).
+#pragma once
+#include "device.h"
+
+namespace l2q {
+
+__device__ __forceinline__ int meta_pos(const int* meta, int pos) { return meta ? meta[1] : pos; }
+
+// ---------------------------------------------------------------------------
+// Q8 quantize (runq.c:117-139).  One thread per element, groups of G
+// consecutive lanes (G divides 64, so a group never straddles a wave).
+template <int G>
+__global__ __launch_bounds__(256) void k_quantize(const float* __restrict__ x, int n,
+                                                  int8_t* __restrict__ xq, float* __restrict__ xs) {
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    const bool in = i < n;
+    const float v = in ? x[i] : 0.0f;
+    const float s = q8_scale(group_max<G>(fabsf(v)));
+    if (in) {
+        xq[i] = (int8_t)q8_value(v, s);
+        if ((i % G) == 0) xs[i / G] = s;
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Residual add + RMSNorm + Q8 quantize of one vector (runq.c:294-305 then
+// :117-139; the residual fold of v5-cuda-fused/run.cu:120-175).  One
+// workgroup of 1024 threads; element i is owned by thread i % 1024, so each
+// wave holds 64 consecutive elements and groups stay inside a wave.
+// If `emb` is set, x is the embedding row of the token in meta[0].
+
+template <int G>
+__global__ __launch_bounds__(kNormThreads) void k_rmsnorm_quant(
+    const float* __restrict__ x, const float* __restrict__ emb, const int* __restrict__ meta,
+    const float* __restrict__ resid, float* __restrict__ xout, const float* __restrict__ w, int n,
+    int8_t* __restrict__ xq, float* __restrict__ xs) {
+    __shared__ float red[kNormThreads / L2Q_WAVE];
+    const int tid = threadIdx.x;
+    const float* src = emb ? emb + (size_t)meta[0] * n : x;
+    float v[kNormMaxPer];
+    float ss = 0.0f;
+#pragma unroll
+    for (int k = 0; k < kNormMaxPer; k++) {
+        const int i = tid + k * kNormThreads;
+        float t = 0.0f;
+        if (i < n) {
+            t = src[i];
+            if (resid) t += resid[i];
+        }
+        v[k] = t;
+        ss = __builtin_fmaf(t, t, ss);
+    }
+    ss = wave_sum(ss);
+    if ((tid & (L2Q_WAVE - 1)) == 0) red[tid / L2Q_WAVE] = ss;
+    __syncthreads();
+    float tot = 0.0f;
+#pragma unroll
+    for (int k = 0; k < kNormThreads / L2Q_WAVE; k++) tot += red[k];
+    const float inv = 1.0f / sqrtf(tot / (float)n + 1e-5f);
+#pragma unroll
+    for (int k = 0; k < kNormMaxPer; k++) {
+        const int i = tid + k * kNormThreads;
+        if (k * kNormThreads >= n) break;   // uniform across the workgroup
+        const bool in = i < n;
+        const float o = in ? w[i] * (inv * v[k]) : 0.0f;
+        const float s = q8_scale(group_max<G>(fabsf(o)));
+        if (in) {
+            if (xout) xout[i] = v[k];
+            xq[i] = (int8_t)q8_value(o, s);
+            if ((i % G) == 0) xs[i / G] = s;
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// SwiGLU + Q8 quantize (runq.c:404-412):  g = (h * (1/(1+expf(-h)))) * h2.
+template <int G>
+__global__ __launch_bounds__(256) void k_swiglu_quant(const float* __restrict__ hb,
+                                                      const float* __restrict__ hb2, int n,
+                                                      int8_t* __restrict__ xq, float* __restrict__ xs,
+                                                      float* __restrict__ gout) {
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    const bool in = i < n;
+    float g = 0.0f;
+    if (in) {
+        float h = hb[i];
+        h *= (1.0f / (1.0f + expf(-h)));
+        g = h * hb2[i];
+    }
+    const float s = q8_scale(group_max<G>(fabsf(g)));
+    if (in) {
+        xq[i] = (int8_t)q8_value(g, s);
+        if ((i % G) == 0) xs[i / G] = s;
+        if (gout) gout[i] = g;
+    }
+}
+
+// ---------------------------------------------------------------------------
+// RoPE + KV append (runq.c:340-365).  One thread per (even, odd) pair of
+// the query; pairs inside kv_dim also rotate k and store k, v at `pos`.
+// The (cos, sin) come from the host-built table (bit-identical to libm).
+// Rotation as a GCC -O3 -march=native build of the reference evaluates it:
+//   v0' = fma(v0, c, -(v1*s)),  v1' = fma(v0, s, v1*c).
+// Cache layout [n_kv_heads][max_t][head_size].
+__global__ __launch_bounds__(256) void k_rope_kv_append(
+    float* __restrict__ q, const float* __restrict__ k, const float* __restrict__ v,
+    float* __restrict__ kcache, float* __restrict__ vcache, const float* __restrict__ rope,
+    const int* __restrict__ meta, int pos_arg, int dim, int kv_dim, int hs, int max_t) {
+    const int p = blockIdx.x * blockDim.x + threadIdx.x;
+    const int i = 2 * p;
+    if (i >= dim) return;
+    const int pos = meta_pos(meta, pos_arg);
+    const int hd = i % hs;
+    const float c = rope[(size_t)pos * hs + hd];
+    const float s = rope[(size_t)pos * hs + hd + 1];
+    {
+        const float v0 = q[i], v1 = q[i + 1];
+        q[i] = __builtin_fmaf(v0, c, -(v1 * s));
+        q[i + 1] = __builtin_fmaf(v0, s, v1 * c);
+    }
+    if (i < kv_dim) {
+        const int h = i / hs;
+        const size_t off = ((size_t)h * max_t + pos) * hs + hd;
+        const float k0 = k[i], k1 = k[i + 1];
+        kcache[off] = __builtin_fmaf(k0, c, -(k1 * s));
+        kcache[off + 1] = __builtin_fmaf(k0, s, k1 * c);
+        vcache[off] = v[i];
+        vcache[off + 1] = v[i + 1];
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Single-query attention, split over the context (runq.c:367-391 +
+// softmax :307-318).  Workgroup (head h, split s) covers positions
+// [s*C, min((s+1)*C, pos+1)) with C = ceil((pos+1)/S); it streams K in
+// LDS-staged tiles of 64 positions (coalesced 128-bit loads, padded rows),
+// scores one position per lane, keeps an online (max, sum) and accumulates
+// p*V with V read coalesced straight from the cache.  It leaves the
+// partial (m, l, o[hs]); k_attn_combine merges the S partials of a head.
+
+__global__ __launch_bounds__(kAttnThreads) void k_attn_partial(
+    const float* __restrict__ q, const float* __restrict__ kcache, const float* __restrict__ vcache,
+    float* __restrict__ part_o, float* __restrict__ part_ml, const int* __restrict__ meta, int pos_arg,
+    int n_heads, int kv_mul, int hs, int max_t) {
+    extern __shared__ float smem[];
+    const int hsp = hs + 4;                         // padded K row (keeps 16 B alignment)
+    float* kt = smem;                               // [kAttnTile][hsp]
+    float* qs = kt + kAttnTile * hsp;               // [hs]
+    float* sc = qs + hs;                            // [4][kAttnTile] partial scores
+    float* pt = sc + 4 * kAttnTile;                 // [kAttnTile] tile probabilities
+    float* ov = pt + kAttnTile;                     // [kAttnThreads] V partials
+    float* st = ov + kAttnThreads;                  // [4]: m, l, alpha
+    const int h = blockIdx.x, s = blockIdx.y, S = gridDim.y;
+    const int tid = threadIdx.x, lane = tid & (L2Q_WAVE - 1), wv = tid / L2Q_WAVE;
+    const int pos = meta_pos(meta, pos_arg);
+    const int n = pos + 1;
+    const int C = (n + S - 1) / S;
+    const int t0 = s * C, t1 = min(n, t0 + C);
+    float* po = part_o + ((size_t)h * S + s) * hs;
+    float* pml = part_ml + ((size_t)h * S + s) * 2;
+    if (t0 >= t1) {   // empty split (uniform across the workgroup)
+        for (int d = tid; d < hs; d += kAttnThreads) po[d] = 0.0f;
+        if (tid == 0) { pml[0] = -INFINITY; pml[1] = 0.0f; }
+        return;
+    }
+    const int kvh = h / kv_mul;
+    const float* kbase = kcache + (size_t)kvh * max_t * hs;
+    const float* vbase = vcache + (size_t)kvh * max_t * hs;
+    for (int d = tid; d < hs; d += kAttnThreads) qs[d] = q[(size_t)h * hs + d];
+    if (tid == 0) { st[0] = -INFINITY; st[1] = 0.0f; }
+
+    const float rs = sqrtf((float)hs);
+    const int dslice = hs / 4;                      // dims per wave in the score pass
+    const int nsl = kAttnThreads / hs;              // position slices in the V pass
+    const int vd = tid % hs, vsl = tid / hs;
+    const int f4 = hs / 4;
+    float o = 0.0f;
+
+    for (int tb = t0; tb < t1; tb += kAttnTile) {
+        const int nt = min(kAttnTile, t1 - tb);
+        __syncthreads();   // previous tile consumed; qs / st visible
+        // stage K[tb .. tb+nt) with 128-bit coalesced loads
+        for (int f = tid; f < nt * f4; f += kAttnThreads) {
+            const int r = f / f4, c4 = f - r * f4;
+            const float4 kv4 = *reinterpret_cast<const float4*>(kbase + (size_t)(tb + r) * hs + 4 * c4);
+            *reinterpret_cast<float4*>(kt + r * hsp + 4 * c4) = kv4;
+        }
+        __syncthreads();
+        // partial scores: lane = position, wave wv sums dims [wv*dslice, (wv+1)*dslice)
+        {
+            float acc = 0.0f;
+            if (lane < nt) {
+                const float* kr = kt + lane * hsp + wv * dslice;
+                const float* qq = qs + wv * dslice;
+                for (int d = 0; d < dslice; d++) acc = __builtin_fmaf(qq[d], kr[d], acc);
+            }
+            sc[wv * kAttnTile + lane] = acc;
+        }
+        __syncthreads();
+        // wave 0: scores, tile max, probabilities, running (m, l)
+        if (wv == 0) {
+            const bool in = lane < nt;
+            const float sj = in ? (sc[lane] + sc[kAttnTile + lane] + sc[2 * kAttnTile + lane] +
+                                   sc[3 * kAttnTile + lane]) / rs
+                                : -INFINITY;
+            const float m_old = st[0];
+            const float mn = fmaxf(m_old, wave_max(sj));
+            const float pj = in ? expf(sj - mn) : 0.0f;
+            pt[lane] = pj;
+            const float psum = wave_sum(pj);
+            if (lane == 0) {
+                const float alpha = expf(m_old - mn);   // 0 on the first tile
+                st[0] = mn;
+                st[1] = st[1] * alpha + psum;
+                st[2] = alpha;
+            }
+        }
+        __syncthreads();
+        o *= st[2];
+        if (vsl < nsl) {
+            for (int j = vsl; j < nt; j += nsl) o = __builtin_fmaf(pt[j], vbase[(size_t)(tb + j) * hs + vd], o);
+        }
+    }
+    // reduce the position slices of the V accumulator
+    ov[tid] = o;
+    __syncthreads();
+    if (tid < hs) {
+        float t = 0.0f;
+        for (int k = 0; k < nsl; k++) t += ov[k * hs + tid];
+        po[tid] = t;
+    }
+    if (tid == 0) { pml[0] = st[0]; pml[1] = st[1]; }
+}
+
+// LDS bytes of k_attn_partial for a head size.
+__host__ __device__ constexpr size_t attn_lds_bytes(int hs) {
+    return (size_t)(kAttnTile * (hs + 4) + hs + 4 * kAttnTile + kAttnTile + kAttnThreads + 4) * sizeof(float);
+}
+
+// Merge the S partials of each head: out = sum_s e^(m_s-M) o_s / sum_s e^(m_s-M) l_s.
+__global__ __launch_bounds__(256) void k_attn_combine(const float* __restrict__ part_o,
+                                                      const float* __restrict__ part_ml,
+                                                      float* __restrict__ out, int S, int hs) {
+    const int h = blockIdx.x;
+    float M = -INFINITY;
+    for (int s = 0; s < S; s++) M = fmaxf(M, part_ml[((size_t)h * S + s) * 2]);
+    float L = 0.0f;
+    for (int s = 0; s < S; s++) {
+        const float ms = part_ml[((size_t)h * S + s) * 2];
+        if (ms != -INFINITY) L += expf(ms - M) * part_ml[((size_t)h * S + s) * 2 + 1];
+    }
+    for (int d = threadIdx.x; d < hs; d += blockDim.x) {
+        float acc = 0.0f;
+        for (int s = 0; s < S; s++) {
+            const float ms = part_ml[((size_t)h * S + s) * 2];
+            if (ms != -INFINITY) acc += expf(ms - M) * part_o[((size_t)h * S + s) * hs + d];
+        }
+        out[(size_t)h * hs + d] = acc / L;
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Greedy argmax (runq.c:578-585: first index of the maximum).
+__global__ __launch_bounds__(1024) void k_argmax(const float* __restrict__ v, int n, int* __restrict__ out) {
+    __shared__ float bv[1024 / L2Q_WAVE];
+    __shared__ int bi[1024 / L2Q_WAVE];
+    float best = -INFINITY;
+    int idx = n;   // sentinel larger than every index
+    for (int i = threadIdx.x; i < n; i += blockDim.x) {
+        const float x = v[i];
+        if (x > best) { best = x; idx = i; }   // ascending i: first max kept
+    }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+        const float ob = __shfl_xor(best, o, L2Q_WAVE);
+        const int oi = __shfl_xor(idx, o, L2Q_WAVE);
+        if (ob > best || (ob == best && oi < idx)) { best = ob; idx = oi; }
+    }
+    const int w = threadIdx.x / L2Q_WAVE;
+    if ((threadIdx.x & (L2Q_WAVE - 1)) == 0) { bv[w] = best; bi[w] = idx; }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        float b = bv[0];
+        int ix = bi[0];
+        for (int k = 1; k < (int)(blockDim.x / L2Q_WAVE); k++)
+            if (bv[k] > b || (bv[k] == b && bi[k] < ix)) { b = bv[k]; ix = bi[k]; }
+        out[0] = ix < n ? ix : 0;
+    }
+}
+
+// Embedding row gather (runq.c:332-333) for the diagnostic path.
+__global__ void k_embed(const float* __restrict__ emb, const int* __restrict__ meta, float* __restrict__ x,
+                        int dim) {
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < dim) x[i] = emb[(size_t)meta[0] * dim + i];
+}
+
+// One-time un-bias of QLL8 weights (u8 = q + 128 -> s8), 16 bytes a thread.
+__global__ void k_unbias(const uint8_t* __restrict__ src, int8_t* __restrict__ dst, size_t n) {
+    const size_t i = ((size_t)blockIdx.x * blockDim.x + threadIdx.x) * 16;
+    if (i + 16 <= n) {
+        uint4 u = *reinterpret_cast<const uint4*>(src + i);
+        u.x ^= 0x80808080u; u.y ^= 0x80808080u; u.z ^= 0x80808080u; u.w ^= 0x80808080u;
+        *reinterpret_cast<uint4*>(dst + i) = u;
+    } else {
+        for (size_t j = i; j < n; j++) dst[j] = (int8_t)(src[j] ^ 0x80u);
+    }
+}
+
+}  // namespace l2q

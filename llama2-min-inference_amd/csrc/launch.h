@@ -1,0 +1,48 @@
+// launch.h - host-side launchers of the decode kernels (C++), shared by the
+// op ABI (ops.hip) and the engine (engine.hip).  Each returns L2Q_OK or a
+// negative status after recording a message with set_error().
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+#include "gemv.h"
+#include "l2q.h"
+
+namespace l2q {
+
+void set_error(const char* fmt, ...) __attribute__((format(printf, 1, 2)));
+int hip_fail(hipError_t e, const char* what);   // records and returns L2Q_ERR_HIP
+int check_launch(const char* what);             // hipGetLastError after a launch
+
+// GEMV: bits 4/8, group 32/64.  Validates shape and 16-byte alignment.
+int launch_gemv(int bits, int group, const GemvArgs& a, hipStream_t st);
+
+int launch_quantize(const float* x, int n, int group, int8_t* xq, float* xs, hipStream_t st);
+
+// emb/meta: layer-0 form (x = emb[meta[0]]); otherwise x.
+int launch_rmsnorm_quant(const float* x, const float* emb, const int* meta, const float* resid,
+                         float* xout, const float* w, int n, int group, int8_t* xq, float* xs,
+                         hipStream_t st);
+
+int launch_swiglu_quant(const float* hb, const float* hb2, int n, int group, int8_t* xq, float* xs,
+                        float* gout, hipStream_t st);
+
+int launch_rope_kv_append(float* q, const float* k, const float* v, float* kcache, float* vcache,
+                          const float* rope, const int* meta, int pos, int dim, int kv_dim, int hs,
+                          int max_t, hipStream_t st);
+
+// Split-context attention: S splits per head, partial buffers of
+// n_heads*S*hs and n_heads*S*2 floats.
+int launch_attention(const float* q, const float* kcache, const float* vcache, float* out,
+                     float* part_o, float* part_ml, int S, const int* meta, int pos, int n_heads,
+                     int n_kv_heads, int hs, int max_t, hipStream_t st);
+
+int launch_argmax(const float* v, int n, int* out, hipStream_t st);
+int launch_unbias(const uint8_t* src, int8_t* dst, size_t n, hipStream_t st);
+
+// Shape checks shared by the op ABI and the engine.
+bool gemv_shape_ok(int bits, int group, int rows, int cols);
+bool attention_shape_ok(int n_heads, int n_kv_heads, int hs);
+
+}  // namespace l2q

@@ -1,0 +1,283 @@
+// ops.hip - launchers and the op-level C ABI (see include/l2q.h).
+#include <hip/hip_runtime.h>
+#include <math.h>
+#include <stdarg.h>
+#include <stdio.h>
+#include <string.h>
+
+#include "kernels.h"
+#include "launch.h"
+
+namespace l2q {
+
+static thread_local char g_err[512];
+
+void set_error(const char* fmt, ...) {
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(g_err, sizeof g_err, fmt, ap);
+    va_end(ap);
+}
+
+int hip_fail(hipError_t e, const char* what) {
+    set_error("%s: %s", what, hipGetErrorString(e));
+    return L2Q_ERR_HIP;
+}
+
+int check_launch(const char* what) {
+    hipError_t e = hipGetLastError();
+    return e == hipSuccess ? L2Q_OK : hip_fail(e, what);
+}
+
+static bool aligned16(const void* p) { return ((uintptr_t)p & 15) == 0; }
+
+// ---------------------------------------------------------------------------
+// GEMV dispatch.  T = groups per lane = ceil((cols/G)/64); R = rows per wave
+// chosen so a wave keeps a few KB of weights in flight without spilling.
+constexpr int kMaxT = 8;
+
+bool gemv_shape_ok(int bits, int group, int rows, int cols) {
+    if (bits != 4 && bits != 8) return false;
+    if (group != 32 && group != 64) return false;
+    if (rows <= 0 || cols <= 0 || cols % group) return false;
+    const int T = (cols / group + L2Q_WAVE - 1) / L2Q_WAVE;
+    return T <= kMaxT;
+}
+
+template <int BITS, int G, int T, int R>
+static int go_gemv(const GemvArgs& a, hipStream_t st) {
+    const int waves = (a.rows + R - 1) / R;
+    const int blocks = (waves + 3) / 4;
+    hipLaunchKernelGGL((k_gemv<BITS, G, T, R>), dim3(blocks), dim3(256), 0, st, a);
+    return check_launch("gemv");
+}
+
+template <int BITS, int G>
+static int gemv_by_t(const GemvArgs& a, hipStream_t st) {
+    const int T = (a.cols / G + L2Q_WAVE - 1) / L2Q_WAVE;
+    switch (T) {
+        case 1: return go_gemv<BITS, G, 1, 4>(a, st);
+        case 2: return go_gemv<BITS, G, 2, 4>(a, st);
+        case 3: return go_gemv<BITS, G, 3, 2>(a, st);
+        case 4: return go_gemv<BITS, G, 4, 2>(a, st);
+        case 5: return go_gemv<BITS, G, 5, 1>(a, st);
+        case 6: return go_gemv<BITS, G, 6, 1>(a, st);
+        case 7: return go_gemv<BITS, G, 7, 1>(a, st);
+        case 8: return go_gemv<BITS, G, 8, 1>(a, st);
+    }
+    set_error("gemv: cols/group = %d groups exceeds %d per lane", a.cols / G, kMaxT * L2Q_WAVE);
+    return L2Q_ERR_ARG;
+}
+
+int launch_gemv(int bits, int group, const GemvArgs& a, hipStream_t st) {
+    if (!gemv_shape_ok(bits, group, a.rows, a.cols)) {
+        set_error("gemv: unsupported shape bits=%d group=%d rows=%d cols=%d", bits, group, a.rows, a.cols);
+        return L2Q_ERR_ARG;
+    }
+    if (!a.out || !a.xq || !a.xs || !a.w || !a.ws) { set_error("gemv: null pointer"); return L2Q_ERR_ARG; }
+    if (!aligned16(a.w) || !aligned16(a.xq)) { set_error("gemv: weights and activations must be 16-byte aligned"); return L2Q_ERR_ARG; }
+    if (bits == 4) return group == 32 ? gemv_by_t<4, 32>(a, st) : gemv_by_t<4, 64>(a, st);
+    return group == 32 ? gemv_by_t<8, 32>(a, st) : gemv_by_t<8, 64>(a, st);
+}
+
+// ---------------------------------------------------------------------------
+
+int launch_quantize(const float* x, int n, int group, int8_t* xq, float* xs, hipStream_t st) {
+    if (n <= 0 || (group != 32 && group != 64) || n % group) { set_error("quantize: bad n=%d group=%d", n, group); return L2Q_ERR_ARG; }
+    const int blocks = (n + 255) / 256;
+    if (group == 32) hipLaunchKernelGGL(k_quantize<32>, dim3(blocks), dim3(256), 0, st, x, n, xq, xs);
+    else hipLaunchKernelGGL(k_quantize<64>, dim3(blocks), dim3(256), 0, st, x, n, xq, xs);
+    return check_launch("quantize");
+}
+
+int launch_rmsnorm_quant(const float* x, const float* emb, const int* meta, const float* resid, float* xout,
+                         const float* w, int n, int group, int8_t* xq, float* xs, hipStream_t st) {
+    if (n <= 0 || n > kNormThreads * kNormMaxPer || (group != 32 && group != 64) || n % group) {
+        set_error("rmsnorm_quant: bad n=%d group=%d", n, group);
+        return L2Q_ERR_ARG;
+    }
+    if (group == 32)
+        hipLaunchKernelGGL(k_rmsnorm_quant<32>, dim3(1), dim3(kNormThreads), 0, st, x, emb, meta, resid, xout, w, n, xq, xs);
+    else
+        hipLaunchKernelGGL(k_rmsnorm_quant<64>, dim3(1), dim3(kNormThreads), 0, st, x, emb, meta, resid, xout, w, n, xq, xs);
+    return check_launch("rmsnorm_quant");
+}
+
+int launch_swiglu_quant(const float* hb, const float* hb2, int n, int group, int8_t* xq, float* xs, float* gout,
+                        hipStream_t st) {
+    if (n <= 0 || (group != 32 && group != 64) || n % group) { set_error("swiglu_quant: bad n=%d group=%d", n, group); return L2Q_ERR_ARG; }
+    const int blocks = (n + 255) / 256;
+    if (group == 32) hipLaunchKernelGGL(k_swiglu_quant<32>, dim3(blocks), dim3(256), 0, st, hb, hb2, n, xq, xs, gout);
+    else hipLaunchKernelGGL(k_swiglu_quant<64>, dim3(blocks), dim3(256), 0, st, hb, hb2, n, xq, xs, gout);
+    return check_launch("swiglu_quant");
+}
+
+int launch_rope_kv_append(float* q, const float* k, const float* v, float* kcache, float* vcache, const float* rope,
+                          const int* meta, int pos, int dim, int kv_dim, int hs, int max_t, hipStream_t st) {
+    if (hs <= 0 || hs % 2 || dim % hs || kv_dim % hs || kv_dim > dim || max_t <= 0 || (!meta && (pos < 0 || pos >= max_t))) {
+        set_error("rope_kv_append: bad shape dim=%d kv_dim=%d hs=%d pos=%d max_t=%d", dim, kv_dim, hs, pos, max_t);
+        return L2Q_ERR_ARG;
+    }
+    const int pairs = dim / 2;
+    hipLaunchKernelGGL(k_rope_kv_append, dim3((pairs + 255) / 256), dim3(256), 0, st, q, k, v, kcache, vcache, rope,
+                       meta, pos, dim, kv_dim, hs, max_t);
+    return check_launch("rope_kv_append");
+}
+
+bool attention_shape_ok(int n_heads, int n_kv_heads, int hs) {
+    return n_heads > 0 && n_kv_heads > 0 && n_heads % n_kv_heads == 0 && hs > 0 && hs % 4 == 0 &&
+           hs <= kAttnMaxHs;
+}
+
+int launch_attention(const float* q, const float* kcache, const float* vcache, float* out, float* part_o,
+                     float* part_ml, int S, const int* meta, int pos, int n_heads, int n_kv_heads, int hs, int max_t,
+                     hipStream_t st) {
+    if (!attention_shape_ok(n_heads, n_kv_heads, hs) || S <= 0 || max_t <= 0 ||
+        (!meta && (pos < 0 || pos >= max_t))) {
+        set_error("attention: bad shape heads=%d kv_heads=%d hs=%d S=%d pos=%d max_t=%d", n_heads, n_kv_heads, hs, S,
+                  pos, max_t);
+        return L2Q_ERR_ARG;
+    }
+    hipLaunchKernelGGL(k_attn_partial, dim3(n_heads, S), dim3(kAttnThreads), attn_lds_bytes(hs), st, q, kcache, vcache,
+                       part_o, part_ml, meta, pos, n_heads, n_heads / n_kv_heads, hs, max_t);
+    int rc = check_launch("attention_partial");
+    if (rc) return rc;
+    hipLaunchKernelGGL(k_attn_combine, dim3(n_heads), dim3(hs < 256 ? hs : 256), 0, st, part_o, part_ml, out, S, hs);
+    return check_launch("attention_combine");
+}
+
+int launch_argmax(const float* v, int n, int* out, hipStream_t st) {
+    if (n <= 0) { set_error("argmax: n=%d", n); return L2Q_ERR_ARG; }
+    hipLaunchKernelGGL(k_argmax, dim3(1), dim3(1024), 0, st, v, n, out);
+    return check_launch("argmax");
+}
+
+int launch_unbias(const uint8_t* src, int8_t* dst, size_t n, hipStream_t st) {
+    if (n == 0) return L2Q_OK;
+    const size_t threads = (n + 15) / 16;
+    hipLaunchKernelGGL(k_unbias, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, st, src, dst, n);
+    return check_launch("unbias");
+}
+
+// Split count for a one-off attention call: ~32 positions per workgroup,
+// at most 128 splits per head.
+static int attention_splits(int pos) {
+    int S = (pos + 1 + 31) / 32;
+    return S < 1 ? 1 : (S > 128 ? 128 : S);
+}
+
+// Per-device scratch for the partials of l2q_attention (grown on demand).
+struct AttnScratch {
+    float* buf = nullptr;
+    size_t floats = 0;
+};
+static AttnScratch g_attn_scratch[64];
+
+static int attn_scratch(size_t floats, float** out) {
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return hip_fail(e, "hipGetDevice");
+    if (dev < 0 || dev >= 64) { set_error("attention: device %d out of range", dev); return L2Q_ERR_ARG; }
+    AttnScratch& s = g_attn_scratch[dev];
+    if (s.floats < floats) {
+        if (s.buf) {
+            e = hipDeviceSynchronize();
+            if (e != hipSuccess) return hip_fail(e, "hipDeviceSynchronize");
+            (void)hipFree(s.buf);
+            s.buf = nullptr;
+            s.floats = 0;
+        }
+        e = hipMalloc(&s.buf, floats * sizeof(float));
+        if (e != hipSuccess) { s.buf = nullptr; return hip_fail(e, "hipMalloc(attention scratch)"); }
+        s.floats = floats;
+    }
+    *out = s.buf;
+    return L2Q_OK;
+}
+
+}  // namespace l2q
+
+using namespace l2q;
+
+// ---------------------------------------------------------------------------
+// C ABI
+
+extern "C" {
+
+const char* l2q_last_error(void) { return g_err; }
+
+int l2q_device_count(void) {
+    int n = 0;
+    if (hipGetDeviceCount(&n) != hipSuccess) {
+        (void)hipGetLastError();
+        return 0;
+    }
+    return n;
+}
+
+int l2q_quantize_act(const float* x, int n, int group, int8_t* xq, float* xs, void* stream) {
+    return launch_quantize(x, n, group, xq, xs, (hipStream_t)stream);
+}
+
+int l2q_gemv_q8(float* out, const int8_t* xq, const float* xs, const int8_t* w, const float* ws, int rows, int cols,
+                int group, int32_t* dots, void* stream) {
+    GemvArgs a{out, xq, xs, w, ws, rows, cols, dots};
+    return launch_gemv(8, group, a, (hipStream_t)stream);
+}
+
+int l2q_gemv_q4(float* out, const int8_t* xq, const float* xs, const uint8_t* w, const float* ws, int rows, int cols,
+                int group, int32_t* dots, void* stream) {
+    GemvArgs a{out, xq, xs, w, ws, rows, cols, dots};
+    return launch_gemv(4, group, a, (hipStream_t)stream);
+}
+
+int l2q_unbias_q8(const uint8_t* src, int8_t* dst, size_t n, void* stream) {
+    return launch_unbias(src, dst, n, (hipStream_t)stream);
+}
+
+int l2q_rmsnorm_quant(const float* x, const float* resid, float* xout, const float* w, int n, int group, int8_t* xq,
+                      float* xs, void* stream) {
+    return launch_rmsnorm_quant(x, nullptr, nullptr, resid, xout, w, n, group, xq, xs, (hipStream_t)stream);
+}
+
+int l2q_swiglu_quant(const float* hb, const float* hb2, int n, int group, int8_t* xq, float* xs, float* gout,
+                     void* stream) {
+    return launch_swiglu_quant(hb, hb2, n, group, xq, xs, gout, (hipStream_t)stream);
+}
+
+int l2q_rope_kv_append(float* q, const float* k, const float* v, float* kcache, float* vcache, const float* rope,
+                       int pos, int n_heads, int n_kv_heads, int head_size, int max_t, void* stream) {
+    if (n_heads <= 0 || n_kv_heads <= 0 || n_heads % n_kv_heads) {
+        set_error("rope_kv_append: bad heads %d/%d", n_heads, n_kv_heads);
+        return L2Q_ERR_ARG;
+    }
+    return launch_rope_kv_append(q, k, v, kcache, vcache, rope, nullptr, pos, n_heads * head_size,
+                                 n_kv_heads * head_size, head_size, max_t, (hipStream_t)stream);
+}
+
+int l2q_attention(const float* q, const float* kcache, const float* vcache, float* out, int pos, int n_heads,
+                  int n_kv_heads, int head_size, int max_t, void* stream) {
+    if (!attention_shape_ok(n_heads, n_kv_heads, head_size) || pos < 0 || pos >= max_t) {
+        set_error("attention: bad shape heads=%d kv_heads=%d hs=%d pos=%d max_t=%d", n_heads, n_kv_heads, head_size,
+                  pos, max_t);
+        return L2Q_ERR_ARG;
+    }
+    const int S = attention_splits(pos);
+    float* scratch = nullptr;
+    int rc = attn_scratch((size_t)n_heads * S * (head_size + 2), &scratch);
+    if (rc) return rc;
+    return launch_attention(q, kcache, vcache, out, scratch, scratch + (size_t)n_heads * S * head_size, S, nullptr, pos,
+                            n_heads, n_kv_heads, head_size, max_t, (hipStream_t)stream);
+}
+
+void l2q_rope_table(float* table, int max_t, int head_size) {
+    for (int pos = 0; pos < max_t; pos++)
+        for (int hd = 0; hd < head_size; hd += 2) {
+            float freq = 1.0f / powf(10000.0f, hd / (float)head_size);
+            float val = pos * freq;
+            table[(size_t)pos * head_size + hd] = cosf(val);
+            table[(size_t)pos * head_size + hd + 1] = sinf(val);
+        }
+}
+
+}  // extern "C"

@@ -1,0 +1,86 @@
+"""Engine wrapper: the decode step of a QLL8/QLL4 checkpoint on one GPU.
+
+Mirrors the reference seam ``forward(transformer, token, pos) -> logits``
+(runq.c:320) and the greedy loop of runq.c:681-718, through the C ABI.
+"""
+import ctypes as C
+
+import numpy as np
+
+from . import abi
+from .host import Checkpoint
+
+
+class Engine:
+    def __init__(self, ckpt: Checkpoint, max_steps: int = 0):
+        if ckpt.header.shared_weights:
+            raise ValueError("shared weights not supported")   # runq.c:247-251
+        self.cfg = ckpt.cfg
+        self.vocab = self.cfg.vocab_size
+        w = ckpt.weights
+        h = C.c_void_p()
+        abi.call("l2q_engine_create", C.byref(self.cfg), w.ctypes.data, w.nbytes, ckpt.wbits, ckpt.group,
+                 max_steps, C.byref(h))
+        self._h = h
+        self.max_steps = max_steps if 0 < max_steps <= self.cfg.seq_len else self.cfg.seq_len
+        self._logits = np.empty(self.vocab, dtype=np.float32)
+
+    def forward(self, token: int, pos: int) -> np.ndarray:
+        """Logits after one step (a copy owned by the caller)."""
+        abi.call("l2q_engine_forward", self._h, token, pos, self._logits.ctypes.data)
+        return self._logits.copy()
+
+    def step(self, token: int, pos: int) -> None:
+        """One step without fetching logits (prompt forcing)."""
+        abi.call("l2q_engine_forward", self._h, token, pos, None)
+
+    def forward_argmax(self, token: int, pos: int) -> int:
+        out = C.c_int()
+        abi.call("l2q_engine_forward_argmax", self._h, token, pos, C.byref(out))
+        return out.value
+
+    def forward_debug(self, token: int, pos: int):
+        """(x after embedding and after every layer [L+1, dim], logits)."""
+        xl = np.empty((self.cfg.n_layers + 1, self.cfg.dim), dtype=np.float32)
+        lg = np.empty(self.vocab, dtype=np.float32)
+        abi.call("l2q_engine_forward_debug", self._h, token, pos, xl.ctypes.data, lg.ctypes.data)
+        return xl, lg
+
+    def time_steps(self, tokens, pos0: int) -> float:
+        """Device milliseconds for len(tokens) graph replays (no logits copy)."""
+        t = np.ascontiguousarray(tokens, dtype=np.int32)
+        ms = C.c_double()
+        abi.call("l2q_engine_time_steps", self._h, t.ctypes.data, pos0, len(t), C.byref(ms))
+        return ms.value
+
+    def greedy(self, prompt, n_steps: int, device_argmax: bool = True):
+        """Force `prompt`, then pick argmax until n_steps positions have run.
+        Returns the id chosen after every position (no BOS stop)."""
+        ids = []
+        token = prompt[0]
+        for pos in range(n_steps):
+            if pos < len(prompt) - 1:
+                self.step(token, pos)
+                nxt = prompt[pos + 1]
+            elif device_argmax:
+                nxt = self.forward_argmax(token, pos)
+            else:
+                nxt = int(np.argmax(self.forward(token, pos)))
+            ids.append(int(nxt))
+            token = nxt
+        return ids
+
+    @property
+    def device_bytes(self) -> int:
+        return abi.lib().l2q_engine_device_bytes(self._h)
+
+    def close(self):
+        if getattr(self, "_h", None) and self._h.value:
+            abi.lib().l2q_engine_destroy(self._h)
+            self._h = C.c_void_p()
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass

@@ -1,0 +1,246 @@
+"""ctypes binding of the oracle (TEST INFRASTRUCTURE ONLY).
+
+Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg import
+this module; the product never does.
+
+* ``Oracle`` binds liboracle.so, the plain-C restatement of the reference
+  decode path (oracle.c, each function citing the runq.c lines it follows).
+* ``RefRunq`` binds _ref/libref_runq.so, the reference CPU runner
+  (v1-int8-vnni/runq.c) compiled unmodified from the reference checkout.
+"""
+import ctypes as C
+import os
+
+import numpy as np
+
+ORACLE_DIR = os.path.dirname(os.path.abspath(__file__))
+ORACLE_LIB = os.path.join(ORACLE_DIR, "liboracle.so")
+REF_LIB = os.path.join(ORACLE_DIR, "_ref", "libref_runq.so")
+REF_BIN = os.path.join(ORACLE_DIR, "_ref", "runq")
+
+P = C.c_void_p
+I = C.c_int
+
+
+def _p(a):
+    return None if a is None else a.ctypes.data
+
+
+_olib = None
+
+
+def olib():
+    global _olib
+    if _olib is None:
+        L = C.CDLL(ORACLE_LIB)
+        sig = {
+            "orc_quantize_act": (None, [P, I, I, P, P, P]),
+            "orc_matmul_q8": (None, [P, P, P, P, P, P, I, I, I, P]),
+            "orc_matmul_q4": (None, [P, P, P, P, P, P, I, I, I, P]),
+            "orc_rmsnorm": (None, [P, P, P, I]),
+            "orc_softmax": (None, [P, I]),
+            "orc_model_create": (P, [P, P, C.c_size_t, I, I, I]),
+            "orc_model_free": (None, [P]),
+            "orc_forward": (C.POINTER(C.c_float), [P, I, I, P]),
+            "orc_greedy": (None, [P, P, I, I, P]),
+            "orc_argmax": (I, [P, I]),
+            "orc_rope_table": (None, [P, I, I]),
+            "orc_rope": (None, [P, P, I, I, I, I]),
+            "orc_attention": (None, [P, P, P, P, I, I, I, I, C.c_size_t, C.c_size_t, P, I]),
+            "orc_swiglu": (None, [P, P, P, I]),
+        }
+        for n, (r, a) in sig.items():
+            f = getattr(L, n)
+            f.restype = r
+            f.argtypes = a
+        _olib = L
+    return _olib
+
+
+def quantize_act(x: np.ndarray, group: int):
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    n = x.size
+    xq = np.empty(n, dtype=np.int8)
+    xs = np.empty(n // group, dtype=np.float32)
+    xt = np.empty(n // group, dtype=np.float32)
+    olib().orc_quantize_act(_p(x), n, group, _p(xq), _p(xs), _p(xt))
+    return xq, xs, xt
+
+
+def matmul(bits: int, xq, xs, xt, w, ws, rows: int, cols: int, group: int, want_dots: bool = True):
+    """out[rows] (+ int32 group dots) of the oracle GEMV; w as stored in the
+    file (INT8: biased u8 [rows][cols]; INT4: packed [rows][cols/2])."""
+    out = np.empty(rows, dtype=np.float32)
+    dots = np.empty((rows, cols // group), dtype=np.int32) if want_dots else None
+    f = olib().orc_matmul_q4 if bits == 4 else olib().orc_matmul_q8
+    f(_p(out), _p(xq), _p(xs), _p(xt), _p(np.ascontiguousarray(w)), _p(np.ascontiguousarray(ws)),
+      rows, cols, group, _p(dots))
+    return out, dots
+
+
+def rmsnorm(x: np.ndarray, w: np.ndarray) -> np.ndarray:
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    o = np.empty_like(x)
+    olib().orc_rmsnorm(_p(o), _p(x), _p(np.ascontiguousarray(w, dtype=np.float32)), x.size)
+    return o
+
+
+def softmax(x: np.ndarray) -> np.ndarray:
+    y = np.ascontiguousarray(x, dtype=np.float32).copy()
+    olib().orc_softmax(_p(y), y.size)
+    return y
+
+
+def rope_table(max_t: int, head_size: int) -> np.ndarray:
+    t = np.empty(max_t * head_size, dtype=np.float32)
+    olib().orc_rope_table(_p(t), max_t, head_size)
+    return t
+
+
+def rope(q: np.ndarray, k: np.ndarray, pos: int, head_size: int):
+    """Rotated copies of q [dim] and k [kv_dim] (runq.c:351-365)."""
+    q = np.ascontiguousarray(q, dtype=np.float32).copy()
+    k = np.ascontiguousarray(k, dtype=np.float32).copy()
+    olib().orc_rope(_p(q), _p(k), pos, q.size, k.size, head_size)
+    return q, k
+
+
+def attention(q: np.ndarray, kcache: np.ndarray, vcache: np.ndarray, pos: int, n_heads: int,
+              n_kv_heads: int, head_size: int) -> np.ndarray:
+    """runq.c:367-391 over caches laid out [n_kv_heads][max_t][head_size]."""
+    q = np.ascontiguousarray(q, dtype=np.float32)
+    kc = np.ascontiguousarray(kcache, dtype=np.float32)
+    vc = np.ascontiguousarray(vcache, dtype=np.float32)
+    max_t = kc.shape[1]
+    out = np.empty(n_heads * head_size, dtype=np.float32)
+    att = np.empty(n_heads * (pos + 1), dtype=np.float32)
+    olib().orc_attention(_p(q), _p(kc), _p(vc), _p(out), pos, n_heads, n_kv_heads, head_size,
+                         head_size, max_t * head_size, _p(att), pos + 1)
+    return out
+
+
+def swiglu(h: np.ndarray, h2: np.ndarray) -> np.ndarray:
+    h = np.ascontiguousarray(h, dtype=np.float32)
+    out = np.empty_like(h)
+    olib().orc_swiglu(_p(out), _p(h), _p(np.ascontiguousarray(h2, dtype=np.float32)), h.size)
+    return out
+
+
+class Oracle:
+    """CPU restatement of forward() over a checkpoint image (host memory)."""
+
+    def __init__(self, cfg_list, weights: np.ndarray, wbits: int, group: int, max_t: int = 0):
+        self.cfg = list(cfg_list)
+        self.dim, self.n_layers, self.vocab = self.cfg[0], self.cfg[2], self.cfg[5]
+        self._w = weights   # keep the buffer alive
+        arr = (C.c_int * 7)(*self.cfg)
+        self._m = olib().orc_model_create(arr, _p(weights), weights.nbytes, wbits, group, max_t)
+        if not self._m:
+            raise ValueError("oracle: weights image too short for the config")
+
+    def forward(self, token: int, pos: int, layers: bool = False):
+        xl = np.empty((self.n_layers + 1, self.dim), dtype=np.float32) if layers else None
+        ptr = olib().orc_forward(self._m, token, pos, _p(xl))
+        logits = np.ctypeslib.as_array(ptr, shape=(self.vocab,)).copy()
+        return (xl, logits) if layers else logits
+
+    def greedy(self, prompt, n_steps: int):
+        pr = np.ascontiguousarray(prompt, dtype=np.int32)
+        out = np.empty(n_steps, dtype=np.int32)
+        olib().orc_greedy(self._m, _p(pr), len(pr), n_steps, _p(out))
+        return [int(v) for v in out]
+
+    def close(self):
+        if self._m:
+            olib().orc_model_free(self._m)
+            self._m = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+# ---------------------------------------------------------------------------
+# the reference runner compiled from its own source
+
+
+def ref_available() -> bool:
+    return os.path.exists(REF_LIB)
+
+
+_rlib = None
+
+
+def rlib():
+    global _rlib
+    if _rlib is None:
+        L = C.CDLL(REF_LIB)
+        sig = {
+            "ref_open": (I, [C.c_char_p]),
+            "ref_config": (None, [P]),
+            "ref_forward": (C.POINTER(C.c_float), [I, I]),
+            "ref_close": (None, []),
+            "ref_quantize_act": (None, [P, I, P, P, P]),
+            "ref_matmul_q8": (None, [P, P, P, P, P, P, I, I]),
+            "ref_rmsnorm": (None, [P, P, P, I]),
+            "ref_softmax": (None, [P, I]),
+            "ref_sample_argmax": (I, [P, I]),
+        }
+        for n, (r, a) in sig.items():
+            f = getattr(L, n)
+            f.restype = r
+            f.argtypes = a
+        _rlib = L
+    return _rlib
+
+
+class RefRunq:
+    """runq.c's Transformer on a QLL8 (version 1, group 32) file."""
+
+    def __init__(self, path: str):
+        self.vocab = rlib().ref_open(path.encode())
+        cfg = np.empty(7, dtype=np.int32)
+        rlib().ref_config(_p(cfg))
+        self.cfg = [int(v) for v in cfg]
+
+    def forward(self, token: int, pos: int) -> np.ndarray:
+        ptr = rlib().ref_forward(token, pos)
+        return np.ctypeslib.as_array(ptr, shape=(self.vocab,)).copy()
+
+    def greedy(self, prompt, n_steps: int):
+        ids, token = [], prompt[0]
+        for pos in range(n_steps):
+            lg = self.forward(token, pos)
+            nxt = prompt[pos + 1] if pos < len(prompt) - 1 else int(np.argmax(lg))
+            ids.append(int(nxt))
+            token = nxt
+        return ids
+
+    def close(self):
+        rlib().ref_close()
+
+
+def ref_quantize_act(x: np.ndarray):
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    n = x.size
+    xq = np.empty(n, dtype=np.int8)
+    xs = np.empty(n // 32, dtype=np.float32)
+    xt = np.empty(n // 32, dtype=np.float32)
+    rlib().ref_quantize_act(_p(x), n, _p(xq), _p(xs), _p(xt))
+    return xq, xs, xt
+
+
+def ref_matmul_q8(xq, xs, xt, w_u8, ws, rows: int, cols: int) -> np.ndarray:
+    out = np.empty(rows, dtype=np.float32)
+    rlib().ref_matmul_q8(_p(out), _p(xq), _p(xs), _p(xt), _p(np.ascontiguousarray(w_u8)),
+                         _p(np.ascontiguousarray(ws)), rows, cols)
+    return out
+
+
+def ref_rmsnorm(x: np.ndarray, w: np.ndarray) -> np.ndarray:
+    x = np.ascontiguousarray(x, dtype=np.float32).copy()
+    o = np.empty_like(x)
+    rlib().ref_rmsnorm(_p(o), _p(x), _p(np.ascontiguousarray(w, dtype=np.float32).copy()), x.size)
+    return o

@@ -1,0 +1,120 @@
+"""End-to-end parity of the GPU decode engine (C ABI) against the oracle.
+
+c1: stories15M-shaped INT8 model (group 32, the reference's own format),
+16 random prompt ids then 240 greedy steps: ids identical to the oracle
+and to the reference runq.c golden ids; residual stream within 1e-4
+relative after every layer.  INT4 models: the same bars at group 32 and
+group 64 (the 7B shape with fewer layers, and the full 32 layers).
+"""
+import json
+import os
+
+import numpy as np
+import pytest
+
+from conftest import GOLDEN, assert_close, rel_err
+from llama2q import host
+from llama2q.model import Engine
+import oracle_py as O
+
+pytestmark = pytest.mark.gpu
+
+
+def c1_prompt(seed=1234, n=16):
+    return [int(v) for v in host.uniform_ints(n, seed, 100, 3, 32000)]
+
+
+@pytest.fixture(scope="module")
+def c1_q8():
+    return host.synth_checkpoint(host.config_15m(), 8, 32, seed=1234)
+
+
+def test_c1_q8_greedy_256(gpu_lib, c1_q8):
+    ck = c1_q8
+    prompt = c1_prompt()
+    eng = Engine(ck, max_steps=256)
+    ids_gpu = eng.greedy(prompt, 256)
+    orc = O.Oracle(ck.cfg.as_list(), ck.weights, 8, 32, max_t=256)
+    ids_orc = orc.greedy(prompt, 256)
+    assert ids_gpu == ids_orc
+    with open(os.path.join(GOLDEN, "c1_q8_greedy.json")) as f:
+        gold = json.load(f)
+    assert gold["prompt"] == prompt
+    assert ids_gpu == gold["ids"]
+    eng.close()
+
+
+def test_c1_q8_layers_and_logits(gpu_lib, c1_q8):
+    ck = c1_q8
+    prompt = c1_prompt()
+    eng = Engine(ck, max_steps=64)
+    orc = O.Oracle(ck.cfg.as_list(), ck.weights, 8, 32, max_t=64)
+    token = prompt[0]
+    for pos in range(40):
+        xl_g, lg_g = eng.forward_debug(token, pos)
+        xl_o, lg_o = orc.forward(token, pos, layers=True)
+        for l in range(xl_o.shape[0]):
+            assert rel_err(xl_g[l], xl_o[l]) < 1e-4, (pos, l)
+        assert rel_err(lg_g, lg_o) < 1e-4
+        token = prompt[pos + 1] if pos < len(prompt) - 1 else int(np.argmax(lg_o))
+    eng.close()
+
+
+def test_c1_graph_matches_eager(gpu_lib, c1_q8):
+    """The captured graph and the eager launch sequence give identical logits,
+    and the device argmax equals the host argmax."""
+    ck = c1_q8
+    prompt = c1_prompt()
+    a = Engine(ck, max_steps=32)
+    b = Engine(ck, max_steps=32)
+    for pos in range(20):
+        tok = prompt[pos % len(prompt)]
+        lg_graph = a.forward(tok, pos)
+        _, lg_eager = b.forward_debug(tok, pos)
+        np.testing.assert_array_equal(lg_graph, lg_eager)
+    am = a.forward_argmax(prompt[3], 20)
+    lg = b.forward(prompt[3], 20)
+    assert am == int(np.argmax(lg))
+    a.close()
+    b.close()
+
+
+def int4_case(cfg, group, n_prompt, n_steps, seed=99):
+    ck = host.synth_checkpoint(cfg, 4, group, seed=seed, q4_divisor=7.0)
+    prompt = [int(v) for v in host.uniform_ints(n_prompt, seed, 100, 3, cfg.vocab_size)]
+    eng = Engine(ck, max_steps=n_steps)
+    ids_gpu = eng.greedy(prompt, n_steps)
+    # per-layer check at the last position
+    orc = O.Oracle(ck.cfg.as_list(), ck.weights, 4, group, max_t=n_steps)
+    ids_orc = orc.greedy(prompt, n_steps)
+    eng.close()
+    return ids_gpu, ids_orc
+
+
+def test_int4_g32_c1_shape(gpu_lib):
+    ids_gpu, ids_orc = int4_case(host.config_15m(), 32, 16, 256)
+    assert ids_gpu == ids_orc
+
+
+def test_int4_g64_7b_shape_2_layers(gpu_lib):
+    cfg = host.config_7b(seq_len=4096)
+    cfg.n_layers = 2
+    ids_gpu, ids_orc = int4_case(cfg, 64, 128, 160)
+    assert ids_gpu == ids_orc
+
+
+def test_int4_g64_7b_layers_debug(gpu_lib):
+    cfg = host.config_7b(seq_len=4096)
+    cfg.n_layers = 2
+    ck = host.synth_checkpoint(cfg, 4, 64, seed=3, q4_divisor=7.0)
+    eng = Engine(ck, max_steps=16)
+    orc = O.Oracle(ck.cfg.as_list(), ck.weights, 4, 64, max_t=16)
+    token = 17
+    for pos in range(8):
+        xl_g, lg_g = eng.forward_debug(token, pos)
+        xl_o, lg_o = orc.forward(token, pos, layers=True)
+        for l in range(xl_o.shape[0]):
+            assert rel_err(xl_g[l], xl_o[l]) < 1e-4, (pos, l)
+        assert rel_err(lg_g, lg_o) < 1e-4
+        token = int(np.argmax(lg_o))
+    eng.close()

@@ -1,0 +1,228 @@
+"""Op-level parity on the GPU: every HIP op through the C ABI against the
+CPU oracle on the same seeded inputs.
+
+Bars: int32 group dots and Q8 activations bit-exact; GEMV fp32 outputs
+within 1e-5 relative (absolute floor: the RMS of the reference vector);
+RoPE/KV append bit-exact (host-built libm table, same FMA form); attention
+within 1e-5 relative.
+"""
+import numpy as np
+import pytest
+
+from conftest import assert_close, rel_err
+from llama2q import abi, host
+import oracle_py as O
+
+pytestmark = pytest.mark.gpu
+
+GEMV_SHAPES = [(4096, 4096), (11008, 4096), (4096, 11008), (32000, 4096)]   # c2 / c3
+SMALL_SHAPES = [(288, 288), (768, 288), (288, 768), (130, 4224), (3, 64), (1, 11008)]
+
+
+def dev(torch, a):
+    return torch.from_numpy(np.ascontiguousarray(a)).cuda()
+
+
+def stream(torch):
+    return torch.cuda.current_stream().cuda_stream
+
+
+def make_weights(rows, cols, bits, group, seed, divisor=7.0):
+    w = host.gauss(rows * cols, seed, 7, 0.02).reshape(rows, cols)
+    if bits == 8:
+        q, s = host.quantize_q8(w, group)
+    else:
+        q, s = host.quantize_q4(w, group, divisor)
+    return q, s
+
+
+def run_gemv(torch, bits, group, q, s, xq, xs, rows, cols):
+    wq = q.view(np.int8) ^ np.int8(-128) if bits == 8 else q      # un-biased signed int8
+    d_w, d_s = dev(torch, wq), dev(torch, s)
+    d_xq, d_xs = dev(torch, xq), dev(torch, xs)
+    out = torch.empty(rows, dtype=torch.float32, device="cuda")
+    dots = torch.empty(rows * (cols // group), dtype=torch.int32, device="cuda")
+    name = "l2q_gemv_q8" if bits == 8 else "l2q_gemv_q4"
+    abi.call(name, out.data_ptr(), d_xq.data_ptr(), d_xs.data_ptr(), d_w.data_ptr(), d_s.data_ptr(),
+             rows, cols, group, dots.data_ptr(), stream(torch))
+    torch.cuda.synchronize()
+    return out.cpu().numpy(), dots.cpu().numpy().reshape(rows, cols // group)
+
+
+@pytest.mark.parametrize("bits", [8, 4])
+@pytest.mark.parametrize("group", [32, 64])
+@pytest.mark.parametrize("shape", GEMV_SHAPES + SMALL_SHAPES)
+def test_gemv_matches_oracle(gpu_lib, torch_cuda, bits, group, shape):
+    rows, cols = shape
+    if cols % group:
+        pytest.skip("group does not divide cols")
+    print(f"gemv bits={bits} group={group} shape={shape}", flush=True)
+    seed = 1000 * bits + group + rows
+    q, s = make_weights(rows, cols, bits, group, seed)
+    x = host.gauss(cols, seed, 9, 1.0)
+    xq, xs, xt = O.quantize_act(x, group)
+    ref, ref_dots = O.matmul(bits, xq, xs, xt, q, s, rows, cols, group)
+    out, dots = run_gemv(torch_cuda, bits, group, q, s, xq, xs, rows, cols)
+    np.testing.assert_array_equal(dots, ref_dots)
+    assert_close(out, ref, 1e-5, what=f"gemv{bits} g{group} {shape}")
+
+
+def test_gemv_int4_extremes(gpu_lib, torch_cuda):
+    """Nibbles 0x8 (-8) and 0x7 (+7) against activations +-127."""
+    rows, cols, group = 64, 4096, 64
+    rng = np.random.default_rng(5)
+    q = rng.choice(np.array([0x88, 0x77, 0x87, 0x78, 0x00, 0xF1], dtype=np.uint8), size=(rows, cols // 2))
+    s = np.full((rows, cols // group), 0.01, dtype=np.float32)
+    xq = rng.choice(np.array([127, -127, 0, 1, -1], dtype=np.int8), size=cols)
+    xs = np.full(cols // group, 0.02, dtype=np.float32)
+    xt = (xs * 128.0 * xq.reshape(-1, group).sum(1).astype(np.float32)).astype(np.float32)
+    ref, ref_dots = O.matmul(4, xq, xs, xt, q, s, rows, cols, group)
+    out, dots = run_gemv(torch_cuda, 4, group, q, s, xq, xs, rows, cols)
+    np.testing.assert_array_equal(dots, ref_dots)
+    assert_close(out, ref, 1e-5, what="int4 extremes")
+
+
+@pytest.mark.parametrize("group", [32, 64])
+@pytest.mark.parametrize("n", [288, 768, 4096, 11008])
+def test_quantize_act_bit_exact(gpu_lib, torch_cuda, group, n):
+    if n % group:
+        pytest.skip("group does not divide n")
+    x = host.gauss(n, 77, n, 1.0)
+    x[:group] = 0.0                      # an all-zero group -> scale 1e-8
+    x[group] = 0.5                       # exact ties for the rounding checks
+    xq_ref, xs_ref, _ = O.quantize_act(x, group)
+    d_x = dev(torch_cuda, x)
+    xq = torch_cuda.empty(n, dtype=torch_cuda.int8, device="cuda")
+    xs = torch_cuda.empty(n // group, dtype=torch_cuda.float32, device="cuda")
+    abi.call("l2q_quantize_act", d_x.data_ptr(), n, group, xq.data_ptr(), xs.data_ptr(), stream(torch_cuda))
+    torch_cuda.cuda.synchronize()
+    np.testing.assert_array_equal(xq.cpu().numpy(), xq_ref)
+    np.testing.assert_array_equal(xs.cpu().numpy(), xs_ref)
+
+
+@pytest.mark.parametrize("group", [32, 64])
+@pytest.mark.parametrize("n", [288, 4096])
+def test_rmsnorm_quant(gpu_lib, torch_cuda, group, n):
+    if n % group:
+        pytest.skip("group does not divide n")
+    x = host.gauss(n, 5, 1, 1.0)
+    r = host.gauss(n, 5, 2, 0.5)
+    w = 1.0 + host.gauss(n, 5, 3, 0.1)
+    v = (x + r).astype(np.float32)
+    o_ref = O.rmsnorm(v, w)
+    xq_ref, xs_ref, _ = O.quantize_act(o_ref, group)
+    t = torch_cuda
+    d_x, d_r, d_w = dev(t, x), dev(t, r), dev(t, w)
+    xout = t.empty(n, dtype=t.float32, device="cuda")
+    xq = t.empty(n, dtype=t.int8, device="cuda")
+    xs = t.empty(n // group, dtype=t.float32, device="cuda")
+    abi.call("l2q_rmsnorm_quant", d_x.data_ptr(), d_r.data_ptr(), xout.data_ptr(), d_w.data_ptr(), n, group,
+             xq.data_ptr(), xs.data_ptr(), stream(t))
+    t.cuda.synchronize()
+    np.testing.assert_array_equal(xout.cpu().numpy(), v)          # the residual add is one rounding
+    gq, gs = xq.cpu().numpy(), xs.cpu().numpy()
+    # the sum of squares is reduced in a different order than runq's 16-lane
+    # FMA tree, so scales agree to ~1 ulp and a value sitting on a rounding
+    # boundary may move by one step
+    assert rel_err(gs, xs_ref) < 1e-6
+    diff = np.abs(gq.astype(int) - xq_ref.astype(int))
+    assert diff.max() <= 1 and (diff > 0).mean() < 1e-3
+    deq = gq.reshape(-1, group) * gs[:, None]
+    assert_close(deq.ravel(), o_ref, 1e-2, what="dequantized norm output")
+
+
+@pytest.mark.parametrize("group", [32, 64])
+@pytest.mark.parametrize("n", [768, 11008])
+def test_swiglu_quant(gpu_lib, torch_cuda, group, n):
+    if n % group:
+        pytest.skip("group does not divide n")
+    h = host.gauss(n, 8, 1, 2.0)
+    h2 = host.gauss(n, 8, 2, 2.0)
+    g_ref = O.swiglu(h, h2)
+    xq_ref, xs_ref, _ = O.quantize_act(g_ref, group)
+    t = torch_cuda
+    d_h, d_h2 = dev(t, h), dev(t, h2)
+    gout = t.empty(n, dtype=t.float32, device="cuda")
+    xq = t.empty(n, dtype=t.int8, device="cuda")
+    xs = t.empty(n // group, dtype=t.float32, device="cuda")
+    abi.call("l2q_swiglu_quant", d_h.data_ptr(), d_h2.data_ptr(), n, group, xq.data_ptr(), xs.data_ptr(),
+             gout.data_ptr(), stream(t))
+    t.cuda.synchronize()
+    # device expf vs glibc expf: within a few ulp
+    assert_close(gout.cpu().numpy(), g_ref, 1e-6, what="swiglu")
+    diff = np.abs(xq.cpu().numpy().astype(int) - xq_ref.astype(int))
+    assert diff.max() <= 1 and (diff > 0).mean() < 1e-3
+    assert rel_err(xs.cpu().numpy(), xs_ref) < 1e-6
+
+
+def attention_case(t, n_heads, n_kv, hs, max_t, pos, seed):
+    """Fill caches for positions < pos, then RoPE + append at pos and attend."""
+    kv_dim = n_kv * hs
+    kc = host.gauss(n_kv * max_t * hs, seed, 1, 1.0).reshape(n_kv, max_t, hs)
+    vc = host.gauss(n_kv * max_t * hs, seed, 2, 1.0).reshape(n_kv, max_t, hs)
+    q = host.gauss(n_heads * hs, seed, 3, 1.0)
+    k = host.gauss(kv_dim, seed, 4, 1.0)
+    v = host.gauss(kv_dim, seed, 5, 1.0)
+    # oracle: rope then append then attend
+    qr, kr = O.rope(q, k, pos, hs)
+    kc_ref, vc_ref = kc.copy(), vc.copy()
+    kc_ref[:, pos, :] = kr.reshape(n_kv, hs)
+    vc_ref[:, pos, :] = v.reshape(n_kv, hs)
+    out_ref = O.attention(qr, kc_ref, vc_ref, pos, n_heads, n_kv, hs)
+    # GPU
+    rope = np.empty(max_t * hs, dtype=np.float32)
+    abi.lib().l2q_rope_table(rope.ctypes.data, max_t, hs)
+    d_q, d_k, d_v = dev(t, q), dev(t, k), dev(t, v)
+    d_kc, d_vc, d_rope = dev(t, kc), dev(t, vc), dev(t, rope)
+    out = t.empty(n_heads * hs, dtype=t.float32, device="cuda")
+    abi.call("l2q_rope_kv_append", d_q.data_ptr(), d_k.data_ptr(), d_v.data_ptr(), d_kc.data_ptr(),
+             d_vc.data_ptr(), d_rope.data_ptr(), pos, n_heads, n_kv, hs, max_t, stream(t))
+    abi.call("l2q_attention", d_q.data_ptr(), d_kc.data_ptr(), d_vc.data_ptr(), out.data_ptr(), pos, n_heads, n_kv,
+             hs, max_t, stream(t))
+    t.cuda.synchronize()
+    return (qr, kc_ref, vc_ref, out_ref), (d_q.cpu().numpy(), d_kc.cpu().numpy(), d_vc.cpu().numpy(),
+                                           out.cpu().numpy())
+
+
+@pytest.mark.parametrize("ctx", [1, 2, 63, 64, 65, 256, 1024, 2048, 4096])
+def test_rope_append_attention_c4(gpu_lib, torch_cuda, ctx):
+    """c4: 32 heads x 128, fp32 cache of 4096 positions, RoPE theta 1e4."""
+    print(f"attention ctx={ctx}", flush=True)
+    ref, got = attention_case(torch_cuda, 32, 32, 128, 4096, ctx - 1, 40 + ctx)
+    np.testing.assert_array_equal(got[0], ref[0])     # rotated q
+    np.testing.assert_array_equal(got[1], ref[1])     # K cache incl. the appended row
+    np.testing.assert_array_equal(got[2], ref[2])     # V cache
+    assert_close(got[3], ref[3], 1e-5, what=f"attention ctx={ctx}")
+
+
+@pytest.mark.parametrize("n_heads,n_kv,hs,max_t,pos", [
+    (6, 6, 48, 256, 0), (6, 6, 48, 256, 100), (6, 6, 48, 256, 255),   # c1 heads
+    (8, 2, 64, 512, 300),                                              # grouped-query heads
+])
+def test_attention_other_heads(gpu_lib, torch_cuda, n_heads, n_kv, hs, max_t, pos):
+    ref, got = attention_case(torch_cuda, n_heads, n_kv, hs, max_t, pos, 7)
+    np.testing.assert_array_equal(got[0], ref[0])
+    np.testing.assert_array_equal(got[1], ref[1])
+    assert_close(got[3], ref[3], 1e-5, what="attention")
+
+
+def test_unbias(gpu_lib, torch_cuda):
+    t = torch_cuda
+    src = np.arange(1000, dtype=np.int64).astype(np.uint8)
+    d_src = dev(t, src)
+    dst = t.empty(1000, dtype=t.int8, device="cuda")
+    abi.call("l2q_unbias_q8", d_src.data_ptr(), dst.data_ptr(), 1000, stream(t))
+    t.cuda.synchronize()
+    np.testing.assert_array_equal(dst.cpu().numpy(), (src.astype(np.int16) - 128).astype(np.int8))
+
+
+def test_bad_shapes_raise(gpu_lib, torch_cuda):
+    t = torch_cuda
+    buf = t.zeros(1 << 16, dtype=t.uint8, device="cuda")
+    p = buf.data_ptr()
+    with pytest.raises(abi.L2QError):
+        abi.call("l2q_gemv_q4", p, p, p, p, p, 16, 100, 64, None, None)       # cols % group
+    with pytest.raises(abi.L2QError):
+        abi.call("l2q_gemv_q8", p, p + 1, p, p, p, 16, 4096, 64, None, None)  # misaligned activations
+    with pytest.raises(abi.L2QError):
+        abi.call("l2q_attention", p, p, p, p, 10, 4, 4, 128, 8, None)         # pos >= max_t
