@@ -139,18 +139,23 @@ void l2q_engine_destroy(l2q_engine* e);
 int l2q_quantize_act(const float* x, int n, int group,
                      int8_t* xq, float* xs, void* stream);
 
-/* INT8 GEMV: out[r] = sum_b ws[r,b] * xs[b] * dot_b(r), where
- * dot_b(r) = sum_{j<group} w[r, b*group+j] * xq[b*group+j] (exact int32).
- * If `dots` is not NULL the int32 group dots are written to
- * dots[r*(cols/group) + b].  w is signed int8 [rows][cols].
- * runq.c:142-159 (matmul_q8), v3-cuda-kvcache/run.cu:177-202. */
+/* INT8 GEMV: out[r] = sum_b ws[r,b] * (xs[b]*(d_b(r) + 128*sum_b(xq)) - xt[b])
+ * with d_b(r) = sum_{j<group} w[r, b*group+j] * xq[b*group+j] the exact
+ * int32 group dot and xt[b] = xs[b]*128*sum_b(xq): the reference's formula
+ * for its +128-biased weights, folded over b in order with FMAs, so out is
+ * bit-identical to runq.c:142-159 (matmul_q8; v3-cuda-kvcache/run.cu:177-202
+ * is the GPU counterpart).  If `dots` is not NULL the int32 group dots are
+ * written to dots[r*(cols/group) + b].  w is signed int8 [rows][cols];
+ * cols <= 448*group. */
 int l2q_gemv_q8(float* out, const int8_t* xq, const float* xs,
                 const int8_t* w, const float* ws, int rows, int cols,
                 int group, int32_t* dots, void* stream);
 
 /* INT4 GEMV, same contract with w packed [rows][cols/2] (low nibble = even
- * column, two's complement).  v5-cuda-fused/run.cu:252-330 with the dequant
- * of tools/quantize_int4.py:38-51. */
+ * column, two's complement): the dequant of tools/quantize_int4.py:38-51
+ * through the formula above (the result equals runq's on the model with
+ * every int4 value stored as int8).  v5-cuda-fused/run.cu:252-330 is the
+ * GPU counterpart. */
 int l2q_gemv_q4(float* out, const int8_t* xq, const float* xs,
                 const uint8_t* w, const float* ws, int rows, int cols,
                 int group, int32_t* dots, void* stream);
@@ -185,11 +190,27 @@ int l2q_rope_kv_append(float* q, const float* k, const float* v,
 
 /* Single-query multi-head attention over positions 0..pos of one layer's
  * cache (layout as above): out[h*hs + i] = sum_t softmax_t(q_h.k_t /
- * sqrtf(hs)) v_t[i], kv head = h / (n_heads/n_kv_heads).
- * runq.c:367-391 + softmax :307-318, v5-cuda-fused/run.cu:441-499. */
+ * sqrtf(hs)) v_t[i], kv head = h / (n_heads/n_kv_heads).  Evaluated in the
+ * reference's order (serial dot per position, expf identical to the host
+ * C library's, serial softmax sum, serial p*V accumulation per element), so
+ * the output is bit-identical to runq.c:367-391 (+ softmax :307-318).
+ * max_t <= 8184 (the probabilities of a head are staged in LDS). */
 int l2q_attention(const float* q, const float* kcache, const float* vcache,
                   float* out, int pos, int n_heads, int n_kv_heads,
                   int head_size, int max_t, void* stream);
+
+/* The same attention split over the context (flash-decoding: per-split
+ * online softmax, then a merge), for throughput; float results agree with
+ * l2q_attention to ~1e-6 relative, not bit for bit.
+ * v5-cuda-fused/run.cu:441-499 semantics. */
+int l2q_attention_split(const float* q, const float* kcache, const float* vcache,
+                        float* out, int pos, int n_heads, int n_kv_heads,
+                        int head_size, int max_t, void* stream);
+
+/* expf exactly as the host C library computes it (the exp used by the
+ * attention softmax and SwiGLU above), elementwise over n floats.  Exposed
+ * so its identity with the host's expf can be checked on every input. */
+int l2q_expf(const float* x, float* y, size_t n, void* stream);
 
 /* Host helper: fill the RoPE (cos, sin) table for positions 0..max_t-1 with
  * the reference's float expressions (runq.c:351-356), so that device and

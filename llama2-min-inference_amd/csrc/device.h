@@ -88,13 +88,12 @@ __device__ __forceinline__ float q8_bias_term(float s, int sumq) {
 }
 
 // runq.c:155 for one group, as GCC -O3 -march=native compiles it (two FMAs):
-//   sum += ws * (xs * d_u8 - xt),   d_u8 = d + 128*sum(q)
+//   sum = fma(ws, t, sum),  t = fma(xs, (float)d_u8, -xt),  d_u8 = d + 128*sum(q)
 // d_u8 is the dot the reference's VPDPBUSD produces on +128-biased weights;
 // with it every per-group term is bit-identical to the reference's.
-__device__ __forceinline__ float group_accumulate(float acc, float ws, float xs, float xt,
-                                                 int d, int sumq) {
-    int du8 = d + 128 * sumq;
-    return __builtin_fmaf(ws, __builtin_fmaf(xs, (float)du8, -xt), acc);
+__device__ __forceinline__ float group_term(float xs, float xt, int d, int sumq) {
+    const int du8 = d + 128 * sumq;
+    return __builtin_fmaf(xs, (float)du8, -xt);
 }
 
 // ---------------------------------------------------------------------------

@@ -47,7 +47,7 @@ struct l2q_engine {
     float *x, *qkv, *att, *wo_out, *h13, *ffn_out, *logits;
     int8_t* xq;
     float* xs;
-    float *kcache, *vcache, *rope, *part_o, *part_ml;
+    float *kcache, *vcache, *rope, *scores;
     int *meta, *am;
     int* h_meta = nullptr;   // pinned {token, pos} slots
     int h_meta_slots = 0;
@@ -98,8 +98,8 @@ int enqueue_step(l2q_engine* e, hipStream_t st, float* dbg_x, float* dbg_tmp, bo
         rc = launch_rope_kv_append(e->qkv, e->qkv + d, e->qkv + d + kv, kc, vc, e->rope, e->meta, 0, d, kv, e->hs,
                                    e->max_t, st);
         if (rc) return rc;
-        rc = launch_attention(e->qkv, kc, vc, e->att, e->part_o, e->part_ml, e->S, e->meta, 0, c.n_heads, c.n_kv_heads,
-                              e->hs, e->max_t, st);
+        rc = launch_attention_exact(e->qkv, kc, vc, e->att, e->scores, e->S, e->meta, 0, c.n_heads, c.n_kv_heads,
+                                    e->hs, e->max_t, st);
         if (rc) return rc;
         if ((rc = launch_quantize(e->att, d, G, e->xq, e->xs, st))) return rc;
         GemvArgs oa{e->wo_out, e->xq, e->xs, e->wo_w + (size_t)l * d * e->rowb_d, e->wo_s + (size_t)l * d * nbd, d, d,
@@ -249,8 +249,7 @@ int build(l2q_engine* e, const void* weights, size_t weights_bytes) {
     const size_t kvfloats = L * kv * (size_t)e->max_t;
     const size_t o_kc = sa.take(kvfloats * 4), o_vc = sa.take(kvfloats * 4);
     const size_t o_rope = sa.take((size_t)e->max_t * e->hs * 4);
-    const size_t o_po = sa.take((size_t)c.n_heads * e->S * e->hs * 4);
-    const size_t o_pml = sa.take((size_t)c.n_heads * e->S * 2 * 4);
+    const size_t o_sc = sa.take((size_t)c.n_heads * e->max_t * 4);
     const size_t o_meta = sa.take(2 * sizeof(int)), o_am = sa.take(sizeof(int));
     e->sbytes = align_up(sa.used, 256);
     HIPCHK(hipMalloc(&e->sarena, e->sbytes), "hipMalloc(state)");
@@ -259,7 +258,7 @@ int build(l2q_engine* e, const void* weights, size_t weights_bytes) {
     e->wo_out = (float*)(S_ + o_wo); e->h13 = (float*)(S_ + o_h13); e->ffn_out = (float*)(S_ + o_ffn);
     e->logits = (float*)(S_ + o_logits); e->xq = (int8_t*)(S_ + o_xq); e->xs = (float*)(S_ + o_xs);
     e->kcache = (float*)(S_ + o_kc); e->vcache = (float*)(S_ + o_vc); e->rope = (float*)(S_ + o_rope);
-    e->part_o = (float*)(S_ + o_po); e->part_ml = (float*)(S_ + o_pml);
+    e->scores = (float*)(S_ + o_sc);
     e->meta = (int*)(S_ + o_meta); e->am = (int*)(S_ + o_am);
     // zero-fill the state (outside any graph) so unused cache rows are defined
     HIPCHK(hipMemsetAsync(e->sarena, 0, e->sbytes, e->stream), "hipMemset(state)");
@@ -314,7 +313,8 @@ int l2q_engine_create(const l2q_config* cfg, const void* weights, size_t weights
     const int hs = c.dim / c.n_heads;
     const int kv_dim = hs * c.n_kv_heads;
     if (!gemv_shape_ok(wbits, group, 1, c.dim) || !gemv_shape_ok(wbits, group, 1, c.hidden_dim) ||
-        !attention_shape_ok(c.n_heads, c.n_kv_heads, hs) || hs % 2 || c.dim > kNormThreads * kNormMaxPer) {
+        !attention_shape_ok(c.n_heads, c.n_kv_heads, hs) || hs % 2 || c.dim > kNormThreads * kNormMaxPer ||
+        !attention_exact_ok(max_steps <= 0 || max_steps > c.seq_len ? c.seq_len : max_steps)) {
         set_error("engine: unsupported shape (dim %d hidden %d heads %d group %d bits %d)", c.dim, c.hidden_dim,
                   c.n_heads, group, wbits);
         return L2Q_ERR_ARG;
@@ -327,8 +327,7 @@ int l2q_engine_create(const l2q_config* cfg, const void* weights, size_t weights
     e->hs = hs;
     e->kv_dim = kv_dim;
     e->max_t = (max_steps <= 0 || max_steps > c.seq_len) ? c.seq_len : max_steps;
-    int S = (e->max_t + kAttnTile - 1) / kAttnTile;
-    e->S = S < 1 ? 1 : (S > 64 ? 64 : S);
+    e->S = score_splits(e->max_t);
     hipError_t he = hipGetDevice(&e->device);
     if (he == hipSuccess) he = hipStreamCreateWithFlags(&e->stream, hipStreamNonBlocking);
     int rc = he == hipSuccess ? build(e, weights, weights_bytes) : hip_fail(he, "engine: device/stream");

@@ -14,7 +14,8 @@
 //     bytes, two v_dot4_i32_i8 per 8 weights;
 //   - all R*T weight loads are issued before the first dot product so a
 //     wave keeps R*T*G/2 (INT4) bytes in flight;
-//   - per-row partial sums are reduced across the wave at the end.
+//   - per-(row, group) terms are folded in group order by one lane per row,
+//     reproducing the reference's float accumulation bit for bit.
 #pragma once
 #include "device.h"
 
@@ -113,17 +114,36 @@ __device__ __forceinline__ int group_dot(const uint4* wv, const LaneActs<BITS, G
     return d;
 }
 
-// Plain GEMV on pre-quantized activations.  Grid: ceil(rows/R) waves,
-// 256 threads (4 waves) per workgroup.
-template <int BITS, int G, int T, int R>
+constexpr int kGemvRowsPerWave = 4;
+constexpr int kGemvWaves = 4;
+constexpr int kGemvRowsPerBlock = kGemvRowsPerWave * kGemvWaves;
+
+// LDS bytes of k_gemv for a given group count (per wave: ws and term of
+// 4 rows, rows padded to nb+1 floats so the folding lanes hit distinct banks).
+__host__ __device__ constexpr size_t gemv_lds_bytes(int nb) {
+    return (size_t)kGemvWaves * kGemvRowsPerWave * (nb + 1) * 2 * sizeof(float);
+}
+
+// GEMV on pre-quantized activations.  Each wave owns 4 rows; after the
+// dot products every (row, group) term t_b = xs_b*d_u8 - xt_b and its weight
+// scale ws_b go to LDS, and one lane per row folds them in group order,
+// sum = fma(ws_b, t_b, sum) for b = 0, 1, ..., exactly the sequence of
+// roundings of the reference loop (runq.c:150-156), so the fp32 output is
+// bit-identical to it.  Grid: ceil(rows/16) workgroups of 256 threads.
+template <int BITS, int G, int T>
 __global__ __launch_bounds__(256) void k_gemv(GemvArgs a) {
     constexpr int NV = GroupShape<BITS, G>::NV;
     constexpr int GB = GroupShape<BITS, G>::GB;
+    constexpr int R = kGemvRowsPerWave;
+    extern __shared__ float lds[];
     const int lane = threadIdx.x & (L2Q_WAVE - 1);
-    const int wave = (int)((blockIdx.x * blockDim.x + threadIdx.x) / L2Q_WAVE);
-    const int row0 = wave * R;
-    if (row0 >= a.rows) return;
+    const int wv = threadIdx.x / L2Q_WAVE;
+    const int row0 = blockIdx.x * kGemvRowsPerBlock + wv * R;
+    if (row0 >= a.rows) return;   // whole wave idle (wave-uniform)
     const int nb = a.cols / G;
+    const int stride = nb + 1;
+    float* ws_l = lds + (size_t)wv * R * stride * 2;
+    float* t_l = ws_l + R * stride;
     const size_t rowbytes = (size_t)a.cols * BITS / 8;
     const uint8_t* wbase = static_cast<const uint8_t*>(a.w);
 
@@ -132,7 +152,7 @@ __global__ __launch_bounds__(256) void k_gemv(GemvArgs a) {
     LaneActs<BITS, G, T> A;
     load_lane_acts<BITS, G, T>(A, a.xq, a.xs, nb, lane);
 
-    uint4 wv[R][T][NV];
+    uint4 wv4[R][T][NV];
     float wsc[R][T];
 #pragma unroll
     for (int r = 0; r < R; r++) {
@@ -141,38 +161,41 @@ __global__ __launch_bounds__(256) void k_gemv(GemvArgs a) {
         for (int t = 0; t < T; t++) {
             const int g = lane + L2Q_WAVE * t;
             if (row < a.rows && g < nb) {
-                const uint4* p = reinterpret_cast<const uint4*>(wbase + (size_t)row * rowbytes + (size_t)g * GB);
+                const uint8_t* p = wbase + (size_t)row * rowbytes + (size_t)g * GB;
 #pragma unroll
-                for (int v = 0; v < NV; v++) wv[r][t][v] = load_stream(p + v);
+                for (int v = 0; v < NV; v++) wv4[r][t][v] = load_stream(p + 16 * v);
                 wsc[r][t] = a.ws[(size_t)row * nb + g];
             } else {
 #pragma unroll
-                for (int v = 0; v < NV; v++) wv[r][t][v] = make_uint4(0, 0, 0, 0);
+                for (int v = 0; v < NV; v++) wv4[r][t][v] = make_uint4(0, 0, 0, 0);
                 wsc[r][t] = 0.0f;
             }
         }
     }
 
-
-    float acc[R];
 #pragma unroll
     for (int r = 0; r < R; r++) {
-        acc[r] = 0.0f;
         const int row = row0 + r;
 #pragma unroll
         for (int t = 0; t < T; t++) {
             const int g = lane + L2Q_WAVE * t;
-            const int d = group_dot<BITS, G, T>(wv[r][t], A, t);
+            const int d = group_dot<BITS, G, T>(wv4[r][t], A, t);
             if (g < nb) {
                 if (a.dots && row < a.rows) a.dots[(size_t)row * nb + g] = d;
-                acc[r] = group_accumulate(acc[r], wsc[r][t], A.xs[t], A.xt[t], d, A.sq[t]);
+                ws_l[r * stride + g] = wsc[r][t];
+                t_l[r * stride + g] = group_term(A.xs[t], A.xt[t], d, A.sq[t]);
             }
         }
     }
-#pragma unroll
-    for (int r = 0; r < R; r++) {
-        const float s = wave_sum(acc[r]);
-        if (lane == 0 && row0 + r < a.rows) a.out[row0 + r] = s;
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    if (lane < R && row0 + lane < a.rows) {
+        const float* wp = ws_l + lane * stride;
+        const float* tp = t_l + lane * stride;
+        float sum = 0.0f;
+        for (int b = 0; b < nb; b++) sum = __builtin_fmaf(wp[b], tp[b], sum);
+        a.out[row0 + lane] = sum;
     }
 }
 

@@ -7,6 +7,7 @@
 // serves every step; the op ABI passes them by value (meta == NULL).
 #pragma once
 #include "device.h"
+#include "exp_runq.h"
 
 namespace l2q {
 
@@ -34,17 +35,23 @@ __global__ __launch_bounds__(256) void k_quantize(const float* __restrict__ x, i
 // workgroup of 1024 threads; element i is owned by thread i % 1024, so each
 // wave holds 64 consecutive elements and groups stay inside a wave.
 // If `emb` is set, x is the embedding row of the token in meta[0].
-
+//
+// The sum of squares follows the reference's order exactly: 16 lanes each
+// accumulate x[j]*x[j] with FMA over j = l, l+16, ... (its AVX-512 loop),
+// the 16 partials are reduced pairwise (8, 4, then (0,2)+(1,3)) as
+// _mm512_reduce_add_ps does, and a tail of n % 16 elements is added the way
+// GCC compiles the reference's scalar loop (a block of 8 unfused, then
+// FMAs).  So inv, and every quantized activation, is bit-identical.
 template <int G>
 __global__ __launch_bounds__(kNormThreads) void k_rmsnorm_quant(
     const float* __restrict__ x, const float* __restrict__ emb, const int* __restrict__ meta,
     const float* __restrict__ resid, float* __restrict__ xout, const float* __restrict__ w, int n,
     int8_t* __restrict__ xq, float* __restrict__ xs) {
-    __shared__ float red[kNormThreads / L2Q_WAVE];
+    __shared__ float vs[kNormThreads * kNormMaxPer];
+    __shared__ float inv_s;
     const int tid = threadIdx.x;
     const float* src = emb ? emb + (size_t)meta[0] * n : x;
     float v[kNormMaxPer];
-    float ss = 0.0f;
 #pragma unroll
     for (int k = 0; k < kNormMaxPer; k++) {
         const int i = tid + k * kNormThreads;
@@ -52,17 +59,29 @@ __global__ __launch_bounds__(kNormThreads) void k_rmsnorm_quant(
         if (i < n) {
             t = src[i];
             if (resid) t += resid[i];
+            vs[i] = t;
         }
         v[k] = t;
-        ss = __builtin_fmaf(t, t, ss);
     }
-    ss = wave_sum(ss);
-    if ((tid & (L2Q_WAVE - 1)) == 0) red[tid / L2Q_WAVE] = ss;
     __syncthreads();
-    float tot = 0.0f;
-#pragma unroll
-    for (int k = 0; k < kNormThreads / L2Q_WAVE; k++) tot += red[k];
-    const float inv = 1.0f / sqrtf(tot / (float)n + 1e-5f);
+    if (tid < 16) {
+        float acc = 0.0f;
+        int j = 0;
+        for (; j + 16 <= n; j += 16) acc = __builtin_fmaf(vs[j + tid], vs[j + tid], acc);
+        // _mm512_reduce_add_ps: (l, l+8) -> (l, l+4) -> (0,2),(1,3) -> (0,1)
+        acc = __shfl_down(acc, 8, 16) + acc;
+        acc = __shfl_down(acc, 4, 16) + acc;
+        const float p = acc + __shfl_down(acc, 2, 16);   // lane0: a0+a2, lane1: a1+a3
+        float s = p + __shfl_down(p, 1, 16);
+        if (tid == 0) {
+            if (n - j >= 8)
+                for (int e = 0; e < 8; e++, j++) s = s + vs[j] * vs[j];
+            for (; j < n; j++) s = __builtin_fmaf(vs[j], vs[j], s);
+            inv_s = 1.0f / sqrtf(s / (float)n + 1e-5f);
+        }
+    }
+    __syncthreads();
+    const float inv = inv_s;
 #pragma unroll
     for (int k = 0; k < kNormMaxPer; k++) {
         const int i = tid + k * kNormThreads;
@@ -90,7 +109,7 @@ __global__ __launch_bounds__(256) void k_swiglu_quant(const float* __restrict__ 
     float g = 0.0f;
     if (in) {
         float h = hb[i];
-        h *= (1.0f / (1.0f + expf(-h)));
+        h *= (1.0f / (1.0f + exp_runq(-h)));
         g = h * hb2[i];
     }
     const float s = q8_scale(group_max<G>(fabsf(g)));
@@ -243,6 +262,131 @@ __host__ __device__ constexpr size_t attn_lds_bytes(int hs) {
     return (size_t)(kAttnTile * (hs + 4) + hs + 4 * kAttnTile + kAttnTile + kAttnThreads + 4) * sizeof(float);
 }
 
+// ---------------------------------------------------------------------------
+// Attention in the reference's exact order (runq.c:367-391, softmax
+// :307-318), in two kernels:
+//
+// k_attn_scores: workgroup (head h, split s) scores positions
+//   [s*C, min((s+1)*C, pos+1)), one lane per position, as the reference
+//   does: sum_i q_i*k_i over the whole head in index order (products
+//   rounded, added in order - GCC vectorises the reference loop that way;
+//   a remainder of head_size % 8 is fused), then / sqrtf(head_size).
+//   K rows are read with 128-bit loads; q is broadcast from LDS.
+// k_attn_softmax_v: workgroup (head h, 64-wide slice of the head) takes
+//   the max of all scores, e_t = expf(s_t - max) with the host-identical
+//   exp_runq, the sum of e_t in position order, p_t = e_t / sum, and then
+//   each lane owns one output element and accumulates fma(p_t, v_t[i], acc)
+//   in position order.  The V chain is serial per element by construction;
+//   the workgroup's other waves stream the next V tiles into LDS so the
+//   chain never waits on HBM.
+
+// Serial dot of the reference's attention loop (see above).
+__device__ __forceinline__ float attn_dot_runq(const float* __restrict__ q, const float* __restrict__ k, int hs) {
+#pragma clang fp contract(off)
+    const int nv = hs & ~7;
+    float score = 0.0f;
+    int i = 0;
+    for (; i < nv; i += 4) {
+        const float4 k4 = *reinterpret_cast<const float4*>(k + i);
+        const float4 q4 = *reinterpret_cast<const float4*>(q + i);
+        score = score + q4.x * k4.x;
+        score = score + q4.y * k4.y;
+        score = score + q4.z * k4.z;
+        score = score + q4.w * k4.w;
+    }
+    for (; i < hs; i++) score = __builtin_fmaf(q[i], k[i], score);
+    return score;
+}
+
+__global__ __launch_bounds__(kAttnThreads) void k_attn_scores(
+    const float* __restrict__ q, const float* __restrict__ kcache, float* __restrict__ scores,
+    const int* __restrict__ meta, int pos_arg, int kv_mul, int hs, int max_t) {
+    __shared__ __attribute__((aligned(16))) float qs[kAttnMaxHs];
+    const int h = blockIdx.x, s = blockIdx.y, S = gridDim.y;
+    const int pos = meta_pos(meta, pos_arg);
+    const int n = pos + 1;
+    const int C = (n + S - 1) / S;
+    const int t0 = s * C, t1 = min(n, t0 + C);
+    if (t0 >= t1) return;
+    for (int d = threadIdx.x; d < hs; d += kAttnThreads) qs[d] = q[(size_t)h * hs + d];
+    __syncthreads();
+    const float rs = sqrtf((float)hs);
+    const float* kbase = kcache + (size_t)(h / kv_mul) * max_t * hs;
+    for (int t = t0 + threadIdx.x; t < t1; t += kAttnThreads)
+        scores[(size_t)h * max_t + t] = attn_dot_runq(qs, kbase + (size_t)t * hs, hs) / rs;
+}
+
+constexpr int kAttnVSlice = 64;    // output elements per softmax/V workgroup
+constexpr int kAttnVTile = 64;     // positions per staged V tile
+
+__host__ __device__ constexpr size_t attn_v_lds_bytes(int max_t) {
+    return ((size_t)max_t + 2 * kAttnVTile * kAttnVSlice + 8) * sizeof(float);
+}
+
+__global__ __launch_bounds__(kAttnThreads) void k_attn_softmax_v(
+    const float* __restrict__ scores, const float* __restrict__ vcache, float* __restrict__ out,
+    const int* __restrict__ meta, int pos_arg, int kv_mul, int hs, int max_t) {
+#pragma clang fp contract(off)
+    extern __shared__ __attribute__((aligned(16))) float smem[];
+    float* p = smem;                               // [max_t] probabilities
+    float* vt = smem + max_t;                      // [2][kAttnVTile][kAttnVSlice]
+    float* red = vt + 2 * kAttnVTile * kAttnVSlice;    // [4] wave maxima, [4] sum
+    const int h = blockIdx.x, d0 = blockIdx.y * kAttnVSlice;
+    const int tid = threadIdx.x, lane = tid & (L2Q_WAVE - 1), wv = tid / L2Q_WAVE;
+    const int pos = meta_pos(meta, pos_arg);
+    const int n = pos + 1;
+    const float* sc = scores + (size_t)h * max_t;
+    // max (order-free)
+    float m = -INFINITY;
+    for (int t = tid; t < n; t += kAttnThreads) m = fmaxf(m, sc[t]);
+    m = wave_max(m);
+    if (lane == 0) red[wv] = m;
+    __syncthreads();
+    m = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+    for (int t = tid; t < n; t += kAttnThreads) p[t] = exp_runq(sc[t] - m);
+    __syncthreads();
+    if (tid == 0) {
+        float sum = 0.0f;
+        for (int t = 0; t < n; t++) sum += p[t];
+        red[4] = sum;
+    }
+    __syncthreads();
+    const float sum = red[4];
+    for (int t = tid; t < n; t += kAttnThreads) p[t] = p[t] / sum;
+
+    // V: waves 1..3 stage tiles of [kAttnVTile positions][kAttnVSlice dims]
+    // into a double buffer; wave 0 runs the serial per-element chains.
+    const float* vbase = vcache + (size_t)(h / kv_mul) * max_t * hs + d0;
+    const int width = min(kAttnVSlice, hs - d0);
+    const int ntiles = (n + kAttnVTile - 1) / kAttnVTile;
+    auto stage = [&](int tile, int buf) {
+        // 192 threads of waves 1..3 copy nt rows of `width` floats
+        const int tb = tile * kAttnVTile;
+        const int nt = min(kAttnVTile, n - tb);
+        float* dst = vt + buf * kAttnVTile * kAttnVSlice;
+        for (int e = tid - L2Q_WAVE; e < nt * kAttnVSlice; e += kAttnThreads - L2Q_WAVE) {
+            const int r = e / kAttnVSlice, c = e - r * kAttnVSlice;
+            if (c < width) dst[e] = vbase[(size_t)(tb + r) * hs + c];
+        }
+    };
+    if (wv > 0) stage(0, 0);
+    __syncthreads();   // also publishes p[]
+    float acc = 0.0f;
+    for (int tile = 0; tile < ntiles; tile++) {
+        const int buf = tile & 1;
+        if (wv > 0) {
+            if (tile + 1 < ntiles) stage(tile + 1, buf ^ 1);
+        } else if (lane < width) {
+            const int tb = tile * kAttnVTile;
+            const int nt = min(kAttnVTile, n - tb);
+            const float* src = vt + buf * kAttnVTile * kAttnVSlice + lane;
+            for (int j = 0; j < nt; j++) acc = __builtin_fmaf(p[tb + j], src[j * kAttnVSlice], acc);
+        }
+        __syncthreads();
+    }
+    if (wv == 0 && lane < width) out[(size_t)h * hs + d0 + lane] = acc;
+}
+
 // Merge the S partials of each head: out = sum_s e^(m_s-M) o_s / sum_s e^(m_s-M) l_s.
 __global__ __launch_bounds__(256) void k_attn_combine(const float* __restrict__ part_o,
                                                       const float* __restrict__ part_ml,
@@ -299,6 +443,12 @@ __global__ void k_embed(const float* __restrict__ emb, const int* __restrict__ m
                         int dim) {
     const int i = blockIdx.x * blockDim.x + threadIdx.x;
     if (i < dim) x[i] = emb[(size_t)meta[0] * dim + i];
+}
+
+// Elementwise exp_runq (exposed for the exhaustive identity check).
+__global__ void k_expf(const float* __restrict__ x, float* __restrict__ y, size_t n) {
+    const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) y[i] = exp_runq(x[i]);
 }
 
 // One-time un-bias of QLL8 weights (u8 = q + 128 -> s8), 16 bytes a thread.

@@ -32,11 +32,24 @@ int launch_rope_kv_append(float* q, const float* k, const float* v, float* kcach
                           const float* rope, const int* meta, int pos, int dim, int kv_dim, int hs,
                           int max_t, hipStream_t st);
 
-// Split-context attention: S splits per head, partial buffers of
-// n_heads*S*hs and n_heads*S*2 floats.
-int launch_attention(const float* q, const float* kcache, const float* vcache, float* out,
-                     float* part_o, float* part_ml, int S, const int* meta, int pos, int n_heads,
-                     int n_kv_heads, int hs, int max_t, hipStream_t st);
+// Split-context attention (tolerance path): S splits per head, partial
+// buffers of n_heads*S*hs and n_heads*S*2 floats.
+int launch_attention_split(const float* q, const float* kcache, const float* vcache, float* out, float* part_o,
+                           float* part_ml, int S, const int* meta, int pos, int n_heads, int n_kv_heads, int hs,
+                           int max_t, hipStream_t st);
+
+// Attention in the reference's exact order: `scores` is n_heads*max_t
+// floats of scratch, S the number of score workgroups per head.
+int launch_attention_exact(const float* q, const float* kcache, const float* vcache, float* out, float* scores,
+                           int S, const int* meta, int pos, int n_heads, int n_kv_heads, int hs, int max_t,
+                           hipStream_t st);
+bool attention_exact_ok(int max_t);
+
+// Score workgroups for n positions: ~128 positions each, at most 64.
+inline int score_splits(int n) {
+    const int S = (n + 127) / 128;
+    return S < 1 ? 1 : (S > 64 ? 64 : S);
+}
 
 int launch_argmax(const float* v, int n, int* out, hipStream_t st);
 int launch_unbias(const uint8_t* src, int8_t* dst, size_t n, hipStream_t st);

@@ -32,9 +32,9 @@ int check_launch(const char* what) {
 static bool aligned16(const void* p) { return ((uintptr_t)p & 15) == 0; }
 
 // ---------------------------------------------------------------------------
-// GEMV dispatch.  T = groups per lane = ceil((cols/G)/64); R = rows per wave
-// chosen so a wave keeps a few KB of weights in flight without spilling.
-constexpr int kMaxT = 8;
+// GEMV dispatch.  T = groups per lane = ceil((cols/G)/64); the per-wave LDS
+// fold area bounds it (7 -> cols <= 448*G).
+constexpr int kMaxT = 7;
 
 bool gemv_shape_ok(int bits, int group, int rows, int cols) {
     if (bits != 4 && bits != 8) return false;
@@ -44,11 +44,10 @@ bool gemv_shape_ok(int bits, int group, int rows, int cols) {
     return T <= kMaxT;
 }
 
-template <int BITS, int G, int T, int R>
+template <int BITS, int G, int T>
 static int go_gemv(const GemvArgs& a, hipStream_t st) {
-    const int waves = (a.rows + R - 1) / R;
-    const int blocks = (waves + 3) / 4;
-    hipLaunchKernelGGL((k_gemv<BITS, G, T, R>), dim3(blocks), dim3(256), 0, st, a);
+    const int blocks = (a.rows + kGemvRowsPerBlock - 1) / kGemvRowsPerBlock;
+    hipLaunchKernelGGL((k_gemv<BITS, G, T>), dim3(blocks), dim3(256), gemv_lds_bytes(a.cols / G), st, a);
     return check_launch("gemv");
 }
 
@@ -56,16 +55,15 @@ template <int BITS, int G>
 static int gemv_by_t(const GemvArgs& a, hipStream_t st) {
     const int T = (a.cols / G + L2Q_WAVE - 1) / L2Q_WAVE;
     switch (T) {
-        case 1: return go_gemv<BITS, G, 1, 4>(a, st);
-        case 2: return go_gemv<BITS, G, 2, 4>(a, st);
-        case 3: return go_gemv<BITS, G, 3, 2>(a, st);
-        case 4: return go_gemv<BITS, G, 4, 2>(a, st);
-        case 5: return go_gemv<BITS, G, 5, 1>(a, st);
-        case 6: return go_gemv<BITS, G, 6, 1>(a, st);
-        case 7: return go_gemv<BITS, G, 7, 1>(a, st);
-        case 8: return go_gemv<BITS, G, 8, 1>(a, st);
+        case 1: return go_gemv<BITS, G, 1>(a, st);
+        case 2: return go_gemv<BITS, G, 2>(a, st);
+        case 3: return go_gemv<BITS, G, 3>(a, st);
+        case 4: return go_gemv<BITS, G, 4>(a, st);
+        case 5: return go_gemv<BITS, G, 5>(a, st);
+        case 6: return go_gemv<BITS, G, 6>(a, st);
+        case 7: return go_gemv<BITS, G, 7>(a, st);
     }
-    set_error("gemv: cols/group = %d groups exceeds %d per lane", a.cols / G, kMaxT * L2Q_WAVE);
+    set_error("gemv: cols/group = %d groups exceeds %d", a.cols / G, kMaxT * L2Q_WAVE);
     return L2Q_ERR_ARG;
 }
 
@@ -129,9 +127,9 @@ bool attention_shape_ok(int n_heads, int n_kv_heads, int hs) {
            hs <= kAttnMaxHs;
 }
 
-int launch_attention(const float* q, const float* kcache, const float* vcache, float* out, float* part_o,
-                     float* part_ml, int S, const int* meta, int pos, int n_heads, int n_kv_heads, int hs, int max_t,
-                     hipStream_t st) {
+int launch_attention_split(const float* q, const float* kcache, const float* vcache, float* out, float* part_o,
+                           float* part_ml, int S, const int* meta, int pos, int n_heads, int n_kv_heads, int hs,
+                           int max_t, hipStream_t st) {
     if (!attention_shape_ok(n_heads, n_kv_heads, hs) || S <= 0 || max_t <= 0 ||
         (!meta && (pos < 0 || pos >= max_t))) {
         set_error("attention: bad shape heads=%d kv_heads=%d hs=%d S=%d pos=%d max_t=%d", n_heads, n_kv_heads, hs, S,
@@ -144,6 +142,27 @@ int launch_attention(const float* q, const float* kcache, const float* vcache, f
     if (rc) return rc;
     hipLaunchKernelGGL(k_attn_combine, dim3(n_heads), dim3(hs < 256 ? hs : 256), 0, st, part_o, part_ml, out, S, hs);
     return check_launch("attention_combine");
+}
+
+bool attention_exact_ok(int max_t) { return attn_v_lds_bytes(max_t) <= 65536; }
+
+int launch_attention_exact(const float* q, const float* kcache, const float* vcache, float* out, float* scores,
+                           int S, const int* meta, int pos, int n_heads, int n_kv_heads, int hs, int max_t,
+                           hipStream_t st) {
+    if (!attention_shape_ok(n_heads, n_kv_heads, hs) || S <= 0 || max_t <= 0 || !attention_exact_ok(max_t) ||
+        (!meta && (pos < 0 || pos >= max_t))) {
+        set_error("attention: bad shape heads=%d kv_heads=%d hs=%d S=%d pos=%d max_t=%d", n_heads, n_kv_heads, hs, S,
+                  pos, max_t);
+        return L2Q_ERR_ARG;
+    }
+    const int kv_mul = n_heads / n_kv_heads;
+    hipLaunchKernelGGL(k_attn_scores, dim3(n_heads, S), dim3(kAttnThreads), 0, st, q, kcache, scores, meta, pos,
+                       kv_mul, hs, max_t);
+    int rc = check_launch("attention_scores");
+    if (rc) return rc;
+    hipLaunchKernelGGL(k_attn_softmax_v, dim3(n_heads, (hs + kAttnVSlice - 1) / kAttnVSlice), dim3(kAttnThreads),
+                       attn_v_lds_bytes(max_t), st, scores, vcache, out, meta, pos, kv_mul, hs, max_t);
+    return check_launch("attention_softmax_v");
 }
 
 int launch_argmax(const float* v, int n, int* out, hipStream_t st) {
@@ -159,9 +178,8 @@ int launch_unbias(const uint8_t* src, int8_t* dst, size_t n, hipStream_t st) {
     return check_launch("unbias");
 }
 
-// Split count for a one-off attention call: ~32 positions per workgroup,
-// at most 128 splits per head.
-static int attention_splits(int pos) {
+// Split counts for a one-off attention call.
+static int attention_splits(int pos) {     // split-context path: ~32 positions per workgroup
     int S = (pos + 1 + 31) / 32;
     return S < 1 ? 1 : (S > 128 ? 128 : S);
 }
@@ -262,12 +280,33 @@ int l2q_attention(const float* q, const float* kcache, const float* vcache, floa
                   pos, max_t);
         return L2Q_ERR_ARG;
     }
+    float* scratch = nullptr;
+    int rc = attn_scratch((size_t)n_heads * max_t, &scratch);
+    if (rc) return rc;
+    return launch_attention_exact(q, kcache, vcache, out, scratch, score_splits(pos + 1), nullptr, pos, n_heads,
+                                  n_kv_heads, head_size, max_t, (hipStream_t)stream);
+}
+
+int l2q_attention_split(const float* q, const float* kcache, const float* vcache, float* out, int pos, int n_heads,
+                        int n_kv_heads, int head_size, int max_t, void* stream) {
+    if (!attention_shape_ok(n_heads, n_kv_heads, head_size) || pos < 0 || pos >= max_t) {
+        set_error("attention: bad shape heads=%d kv_heads=%d hs=%d pos=%d max_t=%d", n_heads, n_kv_heads, head_size,
+                  pos, max_t);
+        return L2Q_ERR_ARG;
+    }
     const int S = attention_splits(pos);
     float* scratch = nullptr;
     int rc = attn_scratch((size_t)n_heads * S * (head_size + 2), &scratch);
     if (rc) return rc;
-    return launch_attention(q, kcache, vcache, out, scratch, scratch + (size_t)n_heads * S * head_size, S, nullptr, pos,
-                            n_heads, n_kv_heads, head_size, max_t, (hipStream_t)stream);
+    return launch_attention_split(q, kcache, vcache, out, scratch, scratch + (size_t)n_heads * S * head_size, S,
+                                  nullptr, pos, n_heads, n_kv_heads, head_size, max_t, (hipStream_t)stream);
+}
+
+int l2q_expf(const float* x, float* y, size_t n, void* stream) {
+    if (n == 0) return L2Q_OK;
+    if (!x || !y) { set_error("expf: null pointer"); return L2Q_ERR_ARG; }
+    hipLaunchKernelGGL(k_expf, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, (hipStream_t)stream, x, y, n);
+    return check_launch("expf");
 }
 
 void l2q_rope_table(float* table, int max_t, int head_size) {

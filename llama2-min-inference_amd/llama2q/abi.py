@@ -52,6 +52,8 @@ SIGNATURES = {
     "l2q_swiglu_quant": (I, [P, P, I, I, P, P, P, P]),
     "l2q_rope_kv_append": (I, [P, P, P, P, P, P, I, I, I, I, I, P]),
     "l2q_attention": (I, [P, P, P, P, I, I, I, I, I, P]),
+    "l2q_attention_split": (I, [P, P, P, P, I, I, I, I, I, P]),
+    "l2q_expf": (I, [P, P, C.c_size_t, P]),
     "l2q_rope_table": (None, [P, I, I]),
 }
 

@@ -341,3 +341,9 @@ void orc_greedy(orc_model* m, const int* prompt, int n_prompt, int n_steps, int*
         token = next;
     }
 }
+
+/* glibc expf over an array (the host function the reference calls). */
+void orc_expf_array(const float* x, float* y, size_t n) {
+    #pragma omp parallel for schedule(static)
+    for (long long i = 0; i < (long long)n; i++) y[i] = expf(x[i]);
+}

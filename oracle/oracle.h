@@ -84,6 +84,9 @@ void orc_greedy(orc_model* m, const int* prompt, int n_prompt, int n_steps, int*
 /* First index of the maximum, runq.c:578-585. */
 int orc_argmax(const float* v, int n);
 
+/* y[i] = expf(x[i]) with the host C library (the reference's expf). */
+void orc_expf_array(const float* x, float* y, size_t n);
+
 /* RoPE (cos, sin) table, runq.c:351-356, [max_t][head_size/2][2]. */
 void orc_rope_table(float* table, int max_t, int head_size);
 

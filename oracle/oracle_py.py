@@ -48,6 +48,7 @@ def olib():
             "orc_rope": (None, [P, P, I, I, I, I]),
             "orc_attention": (None, [P, P, P, P, I, I, I, I, C.c_size_t, C.c_size_t, P, I]),
             "orc_swiglu": (None, [P, P, P, I]),
+            "orc_expf_array": (None, [P, P, C.c_size_t]),
         }
         for n, (r, a) in sig.items():
             f = getattr(L, n)
@@ -124,6 +125,14 @@ def swiglu(h: np.ndarray, h2: np.ndarray) -> np.ndarray:
     out = np.empty_like(h)
     olib().orc_swiglu(_p(out), _p(h), _p(np.ascontiguousarray(h2, dtype=np.float32)), h.size)
     return out
+
+
+def expf_host(x: np.ndarray) -> np.ndarray:
+    """The host C library's expf, elementwise."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    y = np.empty_like(x)
+    olib().orc_expf_array(_p(x), _p(y), x.size)
+    return y
 
 
 class Oracle:

@@ -2,9 +2,12 @@
 
 c1: stories15M-shaped INT8 model (group 32, the reference's own format),
 16 random prompt ids then 240 greedy steps: ids identical to the oracle
-and to the reference runq.c golden ids; residual stream within 1e-4
-relative after every layer.  INT4 models: the same bars at group 32 and
-group 64 (the 7B shape with fewer layers, and the full 32 layers).
+and to the golden ids of the compiled reference runq.c.  Every kernel
+evaluates the reference's arithmetic in its order, so the residual stream
+after every layer and the logits are bit-identical to the oracle's (the
+stated bar of 1e-4 relative per layer is met with zero error).  INT4
+models: the same bars at group 32 (c1 shape; its golden ids come from
+runq on the model lifted to INT8) and at group 64 (the 7B shape).
 """
 import json
 import os
@@ -53,9 +56,8 @@ def test_c1_q8_layers_and_logits(gpu_lib, c1_q8):
     for pos in range(40):
         xl_g, lg_g = eng.forward_debug(token, pos)
         xl_o, lg_o = orc.forward(token, pos, layers=True)
-        for l in range(xl_o.shape[0]):
-            assert rel_err(xl_g[l], xl_o[l]) < 1e-4, (pos, l)
-        assert rel_err(lg_g, lg_o) < 1e-4
+        np.testing.assert_array_equal(xl_g, xl_o)
+        np.testing.assert_array_equal(lg_g, lg_o)
         token = prompt[pos + 1] if pos < len(prompt) - 1 else int(np.argmax(lg_o))
     eng.close()
 
@@ -92,8 +94,14 @@ def int4_case(cfg, group, n_prompt, n_steps, seed=99):
 
 
 def test_int4_g32_c1_shape(gpu_lib):
-    ids_gpu, ids_orc = int4_case(host.config_15m(), 32, 16, 256)
-    assert ids_gpu == ids_orc
+    with open(os.path.join(GOLDEN, "c1_q4_lifted.json")) as f:
+        gold = json.load(f)
+    cfg = host.config_15m()
+    ck = host.synth_checkpoint(cfg, 4, 32, seed=gold["seed"], q4_divisor=gold["divisor"])
+    eng = Engine(ck, max_steps=256)
+    ids_gpu = eng.greedy(gold["prompt"], 256)
+    eng.close()
+    assert ids_gpu == gold["ids"]
 
 
 def test_int4_g64_7b_shape_2_layers(gpu_lib):
@@ -113,8 +121,7 @@ def test_int4_g64_7b_layers_debug(gpu_lib):
     for pos in range(8):
         xl_g, lg_g = eng.forward_debug(token, pos)
         xl_o, lg_o = orc.forward(token, pos, layers=True)
-        for l in range(xl_o.shape[0]):
-            assert rel_err(xl_g[l], xl_o[l]) < 1e-4, (pos, l)
-        assert rel_err(lg_g, lg_o) < 1e-4
+        np.testing.assert_array_equal(xl_g, xl_o)
+        np.testing.assert_array_equal(lg_g, lg_o)
         token = int(np.argmax(lg_o))
     eng.close()

@@ -1,10 +1,12 @@
 """Op-level parity on the GPU: every HIP op through the C ABI against the
 CPU oracle on the same seeded inputs.
 
-Bars: int32 group dots and Q8 activations bit-exact; GEMV fp32 outputs
-within 1e-5 relative (absolute floor: the RMS of the reference vector);
-RoPE/KV append bit-exact (host-built libm table, same FMA form); attention
-within 1e-5 relative.
+The oracle reproduces the compiled reference runq.c bit for bit, and every
+GPU op evaluates the reference's arithmetic in the reference's order, so
+the bar is bit-exact for all of them: int32 group dots, Q8 activations,
+GEMV fp32 outputs, RMSNorm, SwiGLU, RoPE/KV append and attention.  The
+split-context attention (a throughput variant with a different summation
+order) is held to 1e-5 relative with an absolute floor of the output RMS.
 """
 import numpy as np
 import pytest
@@ -64,7 +66,7 @@ def test_gemv_matches_oracle(gpu_lib, torch_cuda, bits, group, shape):
     ref, ref_dots = O.matmul(bits, xq, xs, xt, q, s, rows, cols, group)
     out, dots = run_gemv(torch_cuda, bits, group, q, s, xq, xs, rows, cols)
     np.testing.assert_array_equal(dots, ref_dots)
-    assert_close(out, ref, 1e-5, what=f"gemv{bits} g{group} {shape}")
+    np.testing.assert_array_equal(out, ref)
 
 
 def test_gemv_int4_extremes(gpu_lib, torch_cuda):
@@ -79,7 +81,7 @@ def test_gemv_int4_extremes(gpu_lib, torch_cuda):
     ref, ref_dots = O.matmul(4, xq, xs, xt, q, s, rows, cols, group)
     out, dots = run_gemv(torch_cuda, 4, group, q, s, xq, xs, rows, cols)
     np.testing.assert_array_equal(dots, ref_dots)
-    assert_close(out, ref, 1e-5, what="int4 extremes")
+    np.testing.assert_array_equal(out, ref)
 
 
 @pytest.mark.parametrize("group", [32, 64])
@@ -101,7 +103,7 @@ def test_quantize_act_bit_exact(gpu_lib, torch_cuda, group, n):
 
 
 @pytest.mark.parametrize("group", [32, 64])
-@pytest.mark.parametrize("n", [288, 4096])
+@pytest.mark.parametrize("n", [288, 768, 4096, 4128])
 def test_rmsnorm_quant(gpu_lib, torch_cuda, group, n):
     if n % group:
         pytest.skip("group does not divide n")
@@ -120,15 +122,8 @@ def test_rmsnorm_quant(gpu_lib, torch_cuda, group, n):
              xq.data_ptr(), xs.data_ptr(), stream(t))
     t.cuda.synchronize()
     np.testing.assert_array_equal(xout.cpu().numpy(), v)          # the residual add is one rounding
-    gq, gs = xq.cpu().numpy(), xs.cpu().numpy()
-    # the sum of squares is reduced in a different order than runq's 16-lane
-    # FMA tree, so scales agree to ~1 ulp and a value sitting on a rounding
-    # boundary may move by one step
-    assert rel_err(gs, xs_ref) < 1e-6
-    diff = np.abs(gq.astype(int) - xq_ref.astype(int))
-    assert diff.max() <= 1 and (diff > 0).mean() < 1e-3
-    deq = gq.reshape(-1, group) * gs[:, None]
-    assert_close(deq.ravel(), o_ref, 1e-2, what="dequantized norm output")
+    np.testing.assert_array_equal(xq.cpu().numpy(), xq_ref)
+    np.testing.assert_array_equal(xs.cpu().numpy(), xs_ref)
 
 
 @pytest.mark.parametrize("group", [32, 64])
@@ -148,14 +143,12 @@ def test_swiglu_quant(gpu_lib, torch_cuda, group, n):
     abi.call("l2q_swiglu_quant", d_h.data_ptr(), d_h2.data_ptr(), n, group, xq.data_ptr(), xs.data_ptr(),
              gout.data_ptr(), stream(t))
     t.cuda.synchronize()
-    # device expf vs glibc expf: within a few ulp
-    assert_close(gout.cpu().numpy(), g_ref, 1e-6, what="swiglu")
-    diff = np.abs(xq.cpu().numpy().astype(int) - xq_ref.astype(int))
-    assert diff.max() <= 1 and (diff > 0).mean() < 1e-3
-    assert rel_err(xs.cpu().numpy(), xs_ref) < 1e-6
+    np.testing.assert_array_equal(gout.cpu().numpy(), g_ref)
+    np.testing.assert_array_equal(xq.cpu().numpy(), xq_ref)
+    np.testing.assert_array_equal(xs.cpu().numpy(), xs_ref)
 
 
-def attention_case(t, n_heads, n_kv, hs, max_t, pos, seed):
+def attention_case(t, n_heads, n_kv, hs, max_t, pos, seed, entry="l2q_attention"):
     """Fill caches for positions < pos, then RoPE + append at pos and attend."""
     kv_dim = n_kv * hs
     kc = host.gauss(n_kv * max_t * hs, seed, 1, 1.0).reshape(n_kv, max_t, hs)
@@ -177,7 +170,7 @@ def attention_case(t, n_heads, n_kv, hs, max_t, pos, seed):
     out = t.empty(n_heads * hs, dtype=t.float32, device="cuda")
     abi.call("l2q_rope_kv_append", d_q.data_ptr(), d_k.data_ptr(), d_v.data_ptr(), d_kc.data_ptr(),
              d_vc.data_ptr(), d_rope.data_ptr(), pos, n_heads, n_kv, hs, max_t, stream(t))
-    abi.call("l2q_attention", d_q.data_ptr(), d_kc.data_ptr(), d_vc.data_ptr(), out.data_ptr(), pos, n_heads, n_kv,
+    abi.call(entry, d_q.data_ptr(), d_kc.data_ptr(), d_vc.data_ptr(), out.data_ptr(), pos, n_heads, n_kv,
              hs, max_t, stream(t))
     t.cuda.synchronize()
     return (qr, kc_ref, vc_ref, out_ref), (d_q.cpu().numpy(), d_kc.cpu().numpy(), d_vc.cpu().numpy(),
@@ -192,7 +185,14 @@ def test_rope_append_attention_c4(gpu_lib, torch_cuda, ctx):
     np.testing.assert_array_equal(got[0], ref[0])     # rotated q
     np.testing.assert_array_equal(got[1], ref[1])     # K cache incl. the appended row
     np.testing.assert_array_equal(got[2], ref[2])     # V cache
-    assert_close(got[3], ref[3], 1e-5, what=f"attention ctx={ctx}")
+    np.testing.assert_array_equal(got[3], ref[3])     # output, bit-exact
+
+
+@pytest.mark.parametrize("ctx", [1, 65, 256, 1024, 2048, 4096])
+def test_attention_split_c4(gpu_lib, torch_cuda, ctx):
+    """The split-context variant: 1e-5 relative (c4 tolerance)."""
+    ref, got = attention_case(torch_cuda, 32, 32, 128, 4096, ctx - 1, 40 + ctx, "l2q_attention_split")
+    assert_close(got[3], ref[3], 1e-5, what=f"split attention ctx={ctx}")
 
 
 @pytest.mark.parametrize("n_heads,n_kv,hs,max_t,pos", [
@@ -203,7 +203,25 @@ def test_attention_other_heads(gpu_lib, torch_cuda, n_heads, n_kv, hs, max_t, po
     ref, got = attention_case(torch_cuda, n_heads, n_kv, hs, max_t, pos, 7)
     np.testing.assert_array_equal(got[0], ref[0])
     np.testing.assert_array_equal(got[1], ref[1])
-    assert_close(got[3], ref[3], 1e-5, what="attention")
+    np.testing.assert_array_equal(got[3], ref[3])
+
+
+def test_expf_identical_to_host_on_every_input(gpu_lib, torch_cuda):
+    """The device exp used by softmax and SwiGLU equals the host C library's
+    expf on all 2^32 float bit patterns (NaNs compared as NaN)."""
+    t = torch_cuda
+    chunk = 1 << 27
+    ybuf = t.empty(chunk, dtype=t.float32, device="cuda")
+    for c in range((1 << 32) // chunk):
+        bits = np.arange(c * chunk, (c + 1) * chunk, dtype=np.uint64).astype(np.uint32)
+        x = bits.view(np.float32)
+        d_x = dev(t, x)
+        abi.call("l2q_expf", d_x.data_ptr(), ybuf.data_ptr(), chunk, stream(t))
+        t.cuda.synchronize()
+        y = ybuf.cpu().numpy()
+        ref = O.expf_host(x)
+        same = (y.view(np.uint32) == ref.view(np.uint32)) | (np.isnan(y) & np.isnan(ref))
+        assert same.all(), f"chunk {c}: {int((~same).sum())} mismatches, first x={x[~same][0]!r}"
 
 
 def test_unbias(gpu_lib, torch_cuda):
