@@ -1,0 +1,237 @@
+#!/usr/bin/env python3
+"""Benchmark of the batch-1 quantized decode hot path on one MI355X.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W]
+
+Workload: a Llama-2-7B-shaped decoder (dim 4096, 32
+layers, 32 heads x 128, SwiGLU hidden 11008, vocab 32000) with random-init
+N(0, 0.02) weights quantized to INT4, group 64 (scale = amax/7), activations
+Q8 per group of 64, fp32 KV cache.  128 random prompt ids are forced, then
+W warmup and K timed greedy steps run through the engine's captured
+hipGraph with the argmax on the device (the decode loop of runq.c:681-718).
+A "step" is one decode position; value = K / timed seconds (tok/s).
+
+Also reported on the same JSON line:
+  roofline      the dominant kernel (the INT4 GEMV at the largest per-layer
+                shape, 22016 x 4096 = w1|w3) timed live with HIP events over
+                rotating weight sets (>= 1 GiB, so the 256 MB MALL cannot
+                serve them): algorithmic bytes per launch / mean duration,
+                against the 8 TB/s HBM3E peak;
+  cpu_baseline  the reference's CPU runner (v1-int8-vnni/runq.c, AVX-512
+                VNNI, OpenMP), compiled from its own source, decoding the
+                7B shape at its native INT8 group 32 on this host's cores.
+"""
+import argparse
+import ctypes as C
+import json
+import os
+import sys
+import time
+
+REPO = os.path.dirname(os.path.abspath(__file__))
+PKG = os.path.join(REPO, "llama2-min-inference_amd")
+sys.path.insert(0, PKG)
+
+import numpy as np  # noqa: E402
+
+HBM_PEAK_GBS = 8000.0
+METRIC = "batch-1 decode tok/s, Llama-2-7B-shape INT4; GEMV achieved HBM GB/s (% peak)"
+
+
+def gemv_bytes(rows, cols, bits, group):
+    """Algorithmic bytes of one GEMV: weights + weight scales + activations
+    + activation scales + fp32 output."""
+    return rows * cols * bits // 8 + rows * (cols // group) * 4 + cols + (cols // group) * 4 + rows * 4
+
+
+def step_bytes(cfg, group, pos):
+    """Algorithmic bytes of one decode step at position pos (INT4 weights)."""
+    d, h, L, V = cfg.dim, cfg.hidden_dim, cfg.n_layers, cfg.vocab_size
+    kv = d * cfg.n_kv_heads // cfg.n_heads
+    per_layer = (gemv_bytes(d + 2 * kv, d, 4, group) + gemv_bytes(d, d, 4, group)
+                 + gemv_bytes(2 * h, d, 4, group) + gemv_bytes(d, h, 4, group))
+    kv_read = L * 2 * (pos + 1) * kv * 4
+    kv_write = L * 2 * kv * 4
+    return L * per_layer + gemv_bytes(V, d, 4, group) + kv_read + kv_write + d * 4
+
+
+def time_gemv(torch, abi, rows, cols, bits, group, min_bytes=1 << 30, reps=20):
+    """Mean duration (ms) of the GEMV over rotating weight sets, HIP events
+    on the stream the kernel is launched on."""
+    wbytes = rows * cols * bits // 8
+    nb = cols // group
+    nset = max(2, -(-min_bytes // (wbytes + rows * nb * 4)))
+    g = torch.Generator(device="cuda")
+    g.manual_seed(7)
+    ws = [torch.randint(0, 256, (wbytes,), dtype=torch.uint8, device="cuda", generator=g) for _ in range(nset)]
+    ss = [torch.rand(rows * nb, dtype=torch.float32, device="cuda", generator=g) * 1e-3 for _ in range(nset)]
+    xq = torch.randint(-127, 128, (cols,), dtype=torch.int8, device="cuda", generator=g)
+    xs = torch.rand(nb, dtype=torch.float32, device="cuda", generator=g)
+    out = torch.empty(rows, dtype=torch.float32, device="cuda")
+    st = torch.cuda.current_stream()
+    name = "l2q_gemv_q4" if bits == 4 else "l2q_gemv_q8"
+    fn = getattr(abi.lib(), name)
+
+    def launch(i):
+        rc = fn(out.data_ptr(), xq.data_ptr(), xs.data_ptr(), ws[i % nset].data_ptr(), ss[i % nset].data_ptr(),
+                rows, cols, group, None, st.cuda_stream)
+        if rc:
+            abi.check(rc)
+
+    for i in range(nset):
+        launch(i)
+    torch.cuda.synchronize()
+    n = nset * reps
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(st)
+    for i in range(n):
+        launch(i)
+    e1.record(st)
+    e1.synchronize()
+    ms = e0.elapsed_time(e1) / n
+    del ws, ss
+    torch.cuda.empty_cache()
+    return ms, n
+
+
+def cpu_baseline(seconds_budget=20.0):
+    """The reference runq.c (AVX-512 VNNI + OpenMP) on this host: 7B-shaped
+    INT8 group-32 decode (its own format; the reference has no CPU INT4
+    path).  Timed as the reference does: from the end of the first step."""
+    sys.path.insert(0, os.path.join(REPO, "oracle"))
+    import oracle_py as O
+    from llama2q import host
+    if not O.ref_available():
+        return None
+    cfg = host.config_7b(seq_len=4096)
+    t0 = time.time()
+    ck = host.synth_checkpoint(cfg, 8, 32, seed=11)
+    t_synth = time.time() - t0
+    ref = O.RefRunq(image=ck.data)
+    prompt = [int(v) for v in host.uniform_ints(64, 11, 100, 3, cfg.vocab_size)]
+    ref.forward(prompt[0], 0)                 # first step: not timed (runq.c:710)
+    t0 = time.time()
+    n = 0
+    while True:
+        n += 1
+        ref.forward(prompt[n], n)
+        el = time.time() - t0
+        if el > seconds_budget or n + 1 >= len(prompt):
+            break
+    ref.close()
+    del ck
+    cores = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
+    return {"value": round(n / el, 3), "unit": "tok/s", "cores": cores, "kind": "reference",
+            "sample": f"runq.c forward, Llama-2-7B shape INT8 group 32 (7.96 GB, random-init), "
+                      f"{n} decode steps at positions 1..{n} after one untimed step; OpenMP threads={cores}; "
+                      f"checkpoint synthesis {t_synth:.1f}s not timed"}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=256)
+    ap.add_argument("--warmup", type=int, default=16)
+    ap.add_argument("--prompt", type=int, default=128)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--cpu-seconds", type=float, default=15.0)
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py: this build runs on one GPU; --gpus {args.gpus} is not supported "
+              "(the decode path is single-device; see DESIGN.md for how it would shard)", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+    from llama2q import abi, host
+    from llama2q.model import Engine
+    assert torch.cuda.is_available(), "bench.py needs a GPU"
+
+    cfg = host.config_7b(seq_len=4096)
+    group = 64
+    t0 = time.time()
+    ck = host.synth_checkpoint(cfg, 4, group, seed=2024, q4_divisor=7.0)
+    t_synth = time.time() - t0
+    max_steps = args.prompt + args.warmup + args.steps
+    eng = Engine(ck, max_steps=max_steps)
+    del ck
+    prompt = [int(v) for v in host.uniform_ints(args.prompt, 2024, 100, 3, cfg.vocab_size)]
+
+    # prompt forcing, then warmup greedy steps
+    for pos in range(args.prompt - 1):
+        eng.step(prompt[pos], pos)
+    token = prompt[-1]
+    pos = args.prompt - 1
+    for _ in range(args.warmup):
+        token = eng.forward_argmax(token, pos)
+        pos += 1
+    torch.cuda.synchronize()
+    pos_start = pos
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        token = eng.forward_argmax(token, pos)
+        pos += 1
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t0
+    # the same positions replayed back to back without per-token host sync
+    dev_ms = eng.time_steps([prompt[i % len(prompt)] for i in range(args.steps)], pos_start)
+    eng.close()
+
+    ms_per_step = elapsed * 1e3 / args.steps
+    tok_s = args.steps / elapsed
+    avg_bytes = np.mean([step_bytes(cfg, group, p) for p in range(pos_start, pos_start + args.steps)])
+
+    # roofline of the dominant kernel + the other GEMV shapes of the step
+    shapes = {"w13": (2 * cfg.hidden_dim, cfg.dim), "qkv": (3 * cfg.dim, cfg.dim), "wo": (cfg.dim, cfg.dim),
+              "w2": (cfg.dim, cfg.hidden_dim), "wcls": (cfg.vocab_size, cfg.dim)}
+    gemv = {}
+    for k, (r, c) in shapes.items():
+        ms, n = time_gemv(torch, abi, r, c, 4, group)
+        b = gemv_bytes(r, c, 4, group)
+        gemv[k] = {"rows": r, "cols": c, "us": round(ms * 1e3, 3), "GB/s": round(b / ms / 1e6, 1),
+                   "frac": round(b / ms / 1e6 / HBM_PEAK_GBS, 4), "launches": n}
+    dom = gemv["w13"]
+    dom_bytes = gemv_bytes(*shapes["w13"], 4, group)
+
+    traffic = None
+    tpath = os.path.join(REPO, "profiles", "gemv_q4_g64_w13_traffic.txt")
+    if os.path.exists(tpath):
+        with open(tpath) as f:
+            for line in f:
+                if line.startswith("hbm_bytes_per_launch="):
+                    traffic = int(line.split("=", 1)[1])
+
+    cpu = None if args.no_cpu_baseline else cpu_baseline(args.cpu_seconds)
+
+    line = {
+        "metric": METRIC,
+        "value": round(tok_s, 2),
+        "unit": "tok/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "int4xint8",
+        "data": "synthetic (random-init N(0,0.02) weights, seeded random prompt ids)",
+        "config": {"workload": "Llama-2-7B-shape INT4 g64 batch-1 greedy decode (BASELINE config 5)",
+                   "dim": cfg.dim, "layers": cfg.n_layers, "heads": cfg.n_heads, "hidden": cfg.hidden_dim,
+                   "vocab": cfg.vocab_size, "group": group, "prompt_tokens": args.prompt,
+                   "positions": [pos_start, pos_start + args.steps - 1], "parallelism": "single GPU"},
+        "roofline": {"bound": "hbm", "achieved": dom["GB/s"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": dom["frac"], "traffic": traffic,
+                     "kernel": "k_gemv<4,64,1> (INT4 g64 GEMV), 22016 x 4096 (w1|w3 of one layer)",
+                     "bytes_per_launch": dom_bytes, "mean_us": dom["us"]},
+        "cpu_baseline": cpu,
+        "step_bytes_avg": int(avg_bytes),
+        "step_effective_GBs": round(avg_bytes / (ms_per_step * 1e-3) / 1e9, 1),
+        "device_replay_ms_per_step": round(dev_ms / args.steps, 4),
+        "gemv": gemv,
+        "synth_seconds": round(t_synth, 1),
+    }
+    print(json.dumps(line))
+
+
+if __name__ == "__main__":
+    main()

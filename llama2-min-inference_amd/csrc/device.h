@@ -20,9 +20,16 @@ constexpr int kAttnMaxHs = 256;      // largest head size
 
 typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 
-// 128-bit streaming load (non-temporal: weights are read once per step).
+// 128-bit weight load.
+#ifndef L2Q_WEIGHT_NT
+#define L2Q_WEIGHT_NT 1
+#endif
 __device__ __forceinline__ uint4 load_stream(const void* p) {
+#if L2Q_WEIGHT_NT
     u32x4 v = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
+#else
+    u32x4 v = *reinterpret_cast<const u32x4*>(p);
+#endif
     return make_uint4(v.x, v.y, v.z, v.w);
 }
 

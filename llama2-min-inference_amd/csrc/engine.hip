@@ -5,13 +5,23 @@
 //   qkv_w      [L][d + 2kv][d*bits/8] rows of wq, wk, wv of a layer, back to back
 //   qkv_s      [L][d + 2kv][d/G]      fp32 scales in the same row order
 //   wo_w/s     [L][d][...]            as in the file
-//   w13_w/s    [L][2h][...]           rows of w1 then w3 of a layer
+//   w13_w/s    [L][2h][...]           rows of w1 and w3 interleaved (w1[i], w3[i], ...)
 //   w2_w/s     [L][d][...]
 //   wcls_w/s   [V][...]
 //   INT8 weights are stored signed (the file's +128 bias removed at load).
 //   kcache/vcache fp32 [L][n_kv_heads][max_t][hs]
-// Concatenating wq|wk|wv and w1|w3 turns 5 GEMV launches per layer into 2
-// with 12288- and 22016-row grids at the 7B shape.
+// Concatenating wq|wk|wv and interleaving w1/w3 turns 5 GEMV launches per
+// layer into 2 with 12288- and 22016-row grids at the 7B shape, and lets the
+// SwiGLU run in the GEMV's epilogue.
+//
+// A layer is six launches (runq.c:335-415):
+//   QKV   residual add + RMSNorm + quantize prologue, RoPE + KV append epilogue
+//   attention scores, attention softmax + p*V        (exact order, two kernels)
+//   wo    quantize prologue
+//   W13   residual add + RMSNorm + quantize prologue, SwiGLU epilogue
+//   W2    quantize prologue
+// The residual stream ping-pongs between xa and xb: a norm prologue reads one
+// and its workgroup 0 persists x + resid into the other.
 //
 // One decode step (runq.c:320-421) is captured once into a hipGraph; the
 // token and position are read from device memory (`meta`), so every step
@@ -21,6 +31,7 @@
 #include <stdlib.h>
 #include <string.h>
 
+#include <cstring>
 #include <new>
 #include <vector>
 
@@ -44,9 +55,7 @@ struct l2q_engine {
     float *qkv_s, *wo_s, *w13_s, *w2_s, *wcls_s;
     size_t rowb_d, rowb_h;   // weight bytes of a row with d / h columns
     // state
-    float *x, *qkv, *att, *wo_out, *h13, *ffn_out, *logits;
-    int8_t* xq;
-    float* xs;
+    float *xa, *xb, *q, *att, *wo_out, *hb, *ffn_out, *logits;
     float *kcache, *vcache, *rope, *scores;
     int *meta, *am;
     int* h_meta = nullptr;   // pinned {token, pos} slots
@@ -85,49 +94,79 @@ int enqueue_step(l2q_engine* e, hipStream_t st, float* dbg_x, float* dbg_tmp, bo
     const size_t nbd = (size_t)d / G, nbh = (size_t)h / G;
     int rc;
     for (int l = 0; l < c.n_layers; l++) {
-        // attention rmsnorm; the FFN output of layer l-1 is the pending residual
-        rc = launch_rmsnorm_quant(e->x, l == 0 ? e->emb : nullptr, e->meta, l == 0 ? nullptr : e->ffn_out, e->x,
-                                  e->rms_att + (size_t)l * d, d, G, e->xq, e->xs, st);
-        if (rc) return rc;
-        if (dbg_x && l == 0) HIPCHK(hipMemcpyAsync(dbg_x, e->x, d * sizeof(float), hipMemcpyDeviceToHost, st), "copy x");
-        GemvArgs qa{e->qkv, e->xq, e->xs, e->qkv_w + (size_t)l * qkv_rows * e->rowb_d,
-                    e->qkv_s + (size_t)l * qkv_rows * nbd, qkv_rows, d, nullptr};
-        if ((rc = launch_gemv(bits, G, qa, st))) return rc;
         float* kc = e->kcache + (size_t)l * kv * e->max_t;
         float* vc = e->vcache + (size_t)l * kv * e->max_t;
-        rc = launch_rope_kv_append(e->qkv, e->qkv + d, e->qkv + d + kv, kc, vc, e->rope, e->meta, 0, d, kv, e->hs,
-                                   e->max_t, st);
-        if (rc) return rc;
-        rc = launch_attention_exact(e->qkv, kc, vc, e->att, e->scores, e->S, e->meta, 0, c.n_heads, c.n_kv_heads,
+        // QKV: x = (l == 0 ? emb[token] : xa + ffn_out) -> xb; RMSNorm; q, k, v
+        GemvArgs qa{};
+        qa.out = e->q;
+        qa.w = e->qkv_w + (size_t)l * qkv_rows * e->rowb_d;
+        qa.ws = e->qkv_s + (size_t)l * qkv_rows * nbd;
+        qa.rows = qkv_rows;
+        qa.cols = d;
+        qa.x_in = e->xa;
+        qa.emb = l == 0 ? e->emb : nullptr;
+        qa.resid = l == 0 ? nullptr : e->ffn_out;
+        qa.x_out = e->xb;
+        qa.norm_w = e->rms_att + (size_t)l * d;
+        qa.meta = e->meta;
+        qa.dim = d; qa.kv_dim = kv; qa.hs = e->hs; qa.max_t = e->max_t;
+        qa.kcache = kc; qa.vcache = vc; qa.rope = e->rope;
+        if ((rc = launch_gemv_fused(bits, G, kNorm, kRopeKV, qa, st))) return rc;
+        if (dbg_x && l == 0) HIPCHK(hipMemcpyAsync(dbg_x, e->xb, d * sizeof(float), hipMemcpyDeviceToHost, st), "copy x");
+        rc = launch_attention_exact(e->q, kc, vc, e->att, e->scores, e->S, e->meta, 0, c.n_heads, c.n_kv_heads,
                                     e->hs, e->max_t, st);
         if (rc) return rc;
-        if ((rc = launch_quantize(e->att, d, G, e->xq, e->xs, st))) return rc;
-        GemvArgs oa{e->wo_out, e->xq, e->xs, e->wo_w + (size_t)l * d * e->rowb_d, e->wo_s + (size_t)l * d * nbd, d, d,
-                    nullptr};
-        if ((rc = launch_gemv(bits, G, oa, st))) return rc;
-        // ffn rmsnorm; the attention output is the pending residual (persisted into x)
-        rc = launch_rmsnorm_quant(e->x, nullptr, e->meta, e->wo_out, e->x, e->rms_ffn + (size_t)l * d, d, G, e->xq,
-                                  e->xs, st);
-        if (rc) return rc;
-        GemvArgs ha{e->h13, e->xq, e->xs, e->w13_w + (size_t)l * 2 * h * e->rowb_d,
-                    e->w13_s + (size_t)l * 2 * h * nbd, 2 * h, d, nullptr};
-        if ((rc = launch_gemv(bits, G, ha, st))) return rc;
-        if ((rc = launch_swiglu_quant(e->h13, e->h13 + h, h, G, e->xq, e->xs, nullptr, st))) return rc;
-        GemvArgs fa{e->ffn_out, e->xq, e->xs, e->w2_w + (size_t)l * d * e->rowb_h, e->w2_s + (size_t)l * d * nbh, d, h,
-                    nullptr};
-        if ((rc = launch_gemv(bits, G, fa, st))) return rc;
+        // wo: quantize the attention output in the prologue
+        GemvArgs oa{};
+        oa.out = e->wo_out;
+        oa.w = e->wo_w + (size_t)l * d * e->rowb_d;
+        oa.ws = e->wo_s + (size_t)l * d * nbd;
+        oa.rows = d;
+        oa.cols = d;
+        oa.x_in = e->att;
+        if ((rc = launch_gemv_fused(bits, G, kQuant, kStore, oa, st))) return rc;
+        // W13: x = xb + wo_out -> xa; RMSNorm; SwiGLU(w1 x, w3 x) -> hb
+        GemvArgs ha{};
+        ha.out = e->hb;
+        ha.w = e->w13_w + (size_t)l * 2 * h * e->rowb_d;
+        ha.ws = e->w13_s + (size_t)l * 2 * h * nbd;
+        ha.rows = 2 * h;
+        ha.cols = d;
+        ha.x_in = e->xb;
+        ha.resid = e->wo_out;
+        ha.x_out = e->xa;
+        ha.norm_w = e->rms_ffn + (size_t)l * d;
+        ha.meta = e->meta;
+        if ((rc = launch_gemv_fused(bits, G, kNorm, kSwiglu, ha, st))) return rc;
+        // W2: quantize hb in the prologue
+        GemvArgs fa{};
+        fa.out = e->ffn_out;
+        fa.w = e->w2_w + (size_t)l * d * e->rowb_h;
+        fa.ws = e->w2_s + (size_t)l * d * nbh;
+        fa.rows = d;
+        fa.cols = h;
+        fa.x_in = e->hb;
+        if ((rc = launch_gemv_fused(bits, G, kQuant, kStore, fa, st))) return rc;
         if (dbg_x) {
             float* dst = dbg_x + (size_t)(l + 1) * d;
-            HIPCHK(hipMemcpyAsync(dst, e->x, d * sizeof(float), hipMemcpyDeviceToHost, st), "copy x");
+            HIPCHK(hipMemcpyAsync(dst, e->xa, d * sizeof(float), hipMemcpyDeviceToHost, st), "copy x");
             HIPCHK(hipMemcpyAsync(dbg_tmp, e->ffn_out, d * sizeof(float), hipMemcpyDeviceToHost, st), "copy ffn");
             HIPCHK(hipStreamSynchronize(st), "sync");
             for (int i = 0; i < d; i++) dst[i] = dst[i] + dbg_tmp[i];   // the add the next norm performs
         }
     }
-    rc = launch_rmsnorm_quant(e->x, nullptr, e->meta, e->ffn_out, e->x, e->rms_final, d, G, e->xq, e->xs, st);
-    if (rc) return rc;
-    GemvArgs ca{e->logits, e->xq, e->xs, e->wcls_w, e->wcls_s, c.vocab_size, d, nullptr};
-    if ((rc = launch_gemv(bits, G, ca, st))) return rc;
+    // final RMSNorm of xa + ffn_out, classifier
+    GemvArgs ca{};
+    ca.out = e->logits;
+    ca.w = e->wcls_w;
+    ca.ws = e->wcls_s;
+    ca.rows = c.vocab_size;
+    ca.cols = d;
+    ca.x_in = e->xa;
+    ca.resid = e->ffn_out;
+    ca.norm_w = e->rms_final;
+    ca.meta = e->meta;
+    if ((rc = launch_gemv_fused(bits, G, kNorm, kStore, ca, st))) return rc;
     if (argmax) return launch_argmax(e->logits, c.vocab_size, e->am, st);
     return L2Q_OK;
 }
@@ -214,6 +253,8 @@ int build(l2q_engine* e, const void* weights, size_t weights_bytes) {
     if ((rc = copy_h2d(e->rms_att, F + lay.rms_att, L * d * 4))) return rc;
     if ((rc = copy_h2d(e->rms_ffn, F + lay.rms_ffn, L * d * 4))) return rc;
     if ((rc = copy_h2d(e->rms_final, F + lay.rms_final, d * 4))) return rc;
+    std::vector<uint8_t> stage_w(2 * h * e->rowb_d);
+    std::vector<float> stage_s(2 * h * nbd);
     for (size_t l = 0; l < L; l++) {
         uint8_t* qw = e->qkv_w + l * qkv_rows * e->rowb_d;
         float* qs = e->qkv_s + l * qkv_rows * nbd;
@@ -223,12 +264,15 @@ int build(l2q_engine* e, const void* weights, size_t weights_bytes) {
         if ((rc = copy_h2d(qs, F + lay.wq_s + l * d * nbd * 4, d * nbd * 4))) return rc;
         if ((rc = copy_h2d(qs + d * nbd, F + lay.wk_s + l * kv * nbd * 4, kv * nbd * 4))) return rc;
         if ((rc = copy_h2d(qs + (d + kv) * nbd, F + lay.wv_s + l * kv * nbd * 4, kv * nbd * 4))) return rc;
-        uint8_t* hw = e->w13_w + l * 2 * h * e->rowb_d;
-        float* hsc = e->w13_s + l * 2 * h * nbd;
-        if ((rc = copy_h2d(hw, F + lay.w1 + l * h * e->rowb_d, h * e->rowb_d))) return rc;
-        if ((rc = copy_h2d(hw + h * e->rowb_d, F + lay.w3 + l * h * e->rowb_d, h * e->rowb_d))) return rc;
-        if ((rc = copy_h2d(hsc, F + lay.w1_s + l * h * nbd * 4, h * nbd * 4))) return rc;
-        if ((rc = copy_h2d(hsc + h * nbd, F + lay.w3_s + l * h * nbd * 4, h * nbd * 4))) return rc;
+        // w1/w3 rows interleaved: row 2i = w1[i], row 2i+1 = w3[i]
+        for (size_t i = 0; i < h; i++) {
+            std::memcpy(stage_w.data() + (2 * i) * e->rowb_d, F + lay.w1 + (l * h + i) * e->rowb_d, e->rowb_d);
+            std::memcpy(stage_w.data() + (2 * i + 1) * e->rowb_d, F + lay.w3 + (l * h + i) * e->rowb_d, e->rowb_d);
+            std::memcpy(stage_s.data() + (2 * i) * nbd, F + lay.w1_s + (l * h + i) * nbd * 4, nbd * 4);
+            std::memcpy(stage_s.data() + (2 * i + 1) * nbd, F + lay.w3_s + (l * h + i) * nbd * 4, nbd * 4);
+        }
+        if ((rc = copy_h2d(e->w13_w + l * 2 * h * e->rowb_d, stage_w.data(), stage_w.size()))) return rc;
+        if ((rc = copy_h2d(e->w13_s + l * 2 * h * nbd, stage_s.data(), stage_s.size() * 4))) return rc;
     }
     if ((rc = copy_h2d(e->wo_w, F + lay.wo, L * d * e->rowb_d))) return rc;
     if ((rc = copy_h2d(e->wo_s, F + lay.wo_s, L * d * nbd * 4))) return rc;
@@ -242,10 +286,9 @@ int build(l2q_engine* e, const void* weights, size_t weights_bytes) {
 
     // state arena
     Arena sa;
-    const size_t maxn = h > d ? h : d;
-    const size_t o_x = sa.take(d * 4), o_qkv = sa.take(qkv_rows * 4), o_att = sa.take(d * 4);
-    const size_t o_wo = sa.take(d * 4), o_h13 = sa.take(2 * h * 4), o_ffn = sa.take(d * 4);
-    const size_t o_logits = sa.take(V * 4), o_xq = sa.take(maxn), o_xs = sa.take(maxn / G * 4);
+    const size_t o_xa = sa.take(d * 4), o_xb = sa.take(d * 4), o_q = sa.take(d * 4), o_att = sa.take(d * 4);
+    const size_t o_wo = sa.take(d * 4), o_hb = sa.take(h * 4), o_ffn = sa.take(d * 4);
+    const size_t o_logits = sa.take(V * 4);
     const size_t kvfloats = L * kv * (size_t)e->max_t;
     const size_t o_kc = sa.take(kvfloats * 4), o_vc = sa.take(kvfloats * 4);
     const size_t o_rope = sa.take((size_t)e->max_t * e->hs * 4);
@@ -254,9 +297,9 @@ int build(l2q_engine* e, const void* weights, size_t weights_bytes) {
     e->sbytes = align_up(sa.used, 256);
     HIPCHK(hipMalloc(&e->sarena, e->sbytes), "hipMalloc(state)");
     char* S_ = e->sarena;
-    e->x = (float*)(S_ + o_x); e->qkv = (float*)(S_ + o_qkv); e->att = (float*)(S_ + o_att);
-    e->wo_out = (float*)(S_ + o_wo); e->h13 = (float*)(S_ + o_h13); e->ffn_out = (float*)(S_ + o_ffn);
-    e->logits = (float*)(S_ + o_logits); e->xq = (int8_t*)(S_ + o_xq); e->xs = (float*)(S_ + o_xs);
+    e->xa = (float*)(S_ + o_xa); e->xb = (float*)(S_ + o_xb); e->q = (float*)(S_ + o_q); e->att = (float*)(S_ + o_att);
+    e->wo_out = (float*)(S_ + o_wo); e->hb = (float*)(S_ + o_hb); e->ffn_out = (float*)(S_ + o_ffn);
+    e->logits = (float*)(S_ + o_logits);
     e->kcache = (float*)(S_ + o_kc); e->vcache = (float*)(S_ + o_vc); e->rope = (float*)(S_ + o_rope);
     e->scores = (float*)(S_ + o_sc);
     e->meta = (int*)(S_ + o_meta); e->am = (int*)(S_ + o_am);

@@ -8,6 +8,7 @@
 #pragma once
 #include "device.h"
 #include "exp_runq.h"
+#include "gemv.h"
 
 namespace l2q {
 
@@ -64,21 +65,9 @@ __global__ __launch_bounds__(kNormThreads) void k_rmsnorm_quant(
         v[k] = t;
     }
     __syncthreads();
-    if (tid < 16) {
-        float acc = 0.0f;
-        int j = 0;
-        for (; j + 16 <= n; j += 16) acc = __builtin_fmaf(vs[j + tid], vs[j + tid], acc);
-        // _mm512_reduce_add_ps: (l, l+8) -> (l, l+4) -> (0,2),(1,3) -> (0,1)
-        acc = __shfl_down(acc, 8, 16) + acc;
-        acc = __shfl_down(acc, 4, 16) + acc;
-        const float p = acc + __shfl_down(acc, 2, 16);   // lane0: a0+a2, lane1: a1+a3
-        float s = p + __shfl_down(p, 1, 16);
-        if (tid == 0) {
-            if (n - j >= 8)
-                for (int e = 0; e < 8; e++, j++) s = s + vs[j] * vs[j];
-            for (; j < n; j++) s = __builtin_fmaf(vs[j], vs[j], s);
-            inv_s = 1.0f / sqrtf(s / (float)n + 1e-5f);
-        }
+    if (tid < L2Q_WAVE) {
+        const float ss = runq_sumsq(vs, n, tid);
+        if (tid == 0) inv_s = 1.0f / sqrtf(ss / (float)n + 1e-5f);
     }
     __syncthreads();
     const float inv = inv_s;
@@ -266,61 +255,70 @@ __host__ __device__ constexpr size_t attn_lds_bytes(int hs) {
 // Attention in the reference's exact order (runq.c:367-391, softmax
 // :307-318), in two kernels:
 //
-// k_attn_scores: workgroup (head h, split s) scores positions
-//   [s*C, min((s+1)*C, pos+1)), one lane per position, as the reference
-//   does: sum_i q_i*k_i over the whole head in index order (products
+// k_attn_scores: workgroup (head h, block of kScoreTile positions) stages
+//   the K rows in LDS with coalesced 128-bit loads, then one lane per
+//   position forms sum_i q_i*k_i over the head in index order (products
 //   rounded, added in order - GCC vectorises the reference loop that way;
 //   a remainder of head_size % 8 is fused), then / sqrtf(head_size).
-//   K rows are read with 128-bit loads; q is broadcast from LDS.
-// k_attn_softmax_v: workgroup (head h, 64-wide slice of the head) takes
-//   the max of all scores, e_t = expf(s_t - max) with the host-identical
-//   exp_runq, the sum of e_t in position order, p_t = e_t / sum, and then
-//   each lane owns one output element and accumulates fma(p_t, v_t[i], acc)
-//   in position order.  The V chain is serial per element by construction;
-//   the workgroup's other waves stream the next V tiles into LDS so the
-//   chain never waits on HBM.
+// k_attn_softmax_v: workgroup (head h, 32-wide slice of the head) takes
+//   the max of the head's scores, e_t = expf(s_t - max) with the
+//   host-identical exp_runq, the sum of e_t in position order (one lane),
+//   p_t = e_t / sum, and then one lane per output element accumulates
+//   fma(p_t, v_t[i], acc) in position order.  V is streamed through LDS
+//   in chunks of kVChunk positions by the whole workgroup (the next chunk's
+//   loads are in flight while the current chunk is folded), so the serial
+//   chains never wait on HBM.
+constexpr int kScoreTile = 64;
+constexpr int kVSlice = 32;
+constexpr int kVChunk = 128;
+constexpr int kVPer = kVChunk * kVSlice / 4 / kAttnThreads;   // float4 per thread per chunk
+constexpr int kScorePer = 16;                                   // scores per thread -> n <= 4096
 
-// Serial dot of the reference's attention loop (see above).
-__device__ __forceinline__ float attn_dot_runq(const float* __restrict__ q, const float* __restrict__ k, int hs) {
-#pragma clang fp contract(off)
-    const int nv = hs & ~7;
-    float score = 0.0f;
-    int i = 0;
-    for (; i < nv; i += 4) {
-        const float4 k4 = *reinterpret_cast<const float4*>(k + i);
-        const float4 q4 = *reinterpret_cast<const float4*>(q + i);
-        score = score + q4.x * k4.x;
-        score = score + q4.y * k4.y;
-        score = score + q4.z * k4.z;
-        score = score + q4.w * k4.w;
-    }
-    for (; i < hs; i++) score = __builtin_fmaf(q[i], k[i], score);
-    return score;
+__host__ __device__ constexpr size_t attn_scores_lds_bytes(int hs) {
+    return ((size_t)kScoreTile * (hs + 4) + hs) * sizeof(float);
+}
+__host__ __device__ constexpr size_t attn_v_lds_bytes(int max_t) {
+    return ((size_t)max_t + 4 + 2 * kVChunk * kVSlice + 8) * sizeof(float);
 }
 
 __global__ __launch_bounds__(kAttnThreads) void k_attn_scores(
     const float* __restrict__ q, const float* __restrict__ kcache, float* __restrict__ scores,
     const int* __restrict__ meta, int pos_arg, int kv_mul, int hs, int max_t) {
-    __shared__ __attribute__((aligned(16))) float qs[kAttnMaxHs];
-    const int h = blockIdx.x, s = blockIdx.y, S = gridDim.y;
+#pragma clang fp contract(off)
+    extern __shared__ __attribute__((aligned(16))) float sm[];
+    const int hsp = hs + 4;
+    float* kt = sm;                       // [kScoreTile][hsp]
+    float* qs = kt + kScoreTile * hsp;    // [hs]
+    const int h = blockIdx.x;
     const int pos = meta_pos(meta, pos_arg);
     const int n = pos + 1;
-    const int C = (n + S - 1) / S;
-    const int t0 = s * C, t1 = min(n, t0 + C);
-    if (t0 >= t1) return;
+    const int t0 = blockIdx.y * kScoreTile;
+    if (t0 >= n) return;                  // uniform: the grid covers max_t
+    const int nt = min(kScoreTile, n - t0);
+    const int f4 = hs / 4;
+    const float* kbase = kcache + ((size_t)(h / kv_mul) * max_t + t0) * hs;
+    for (int f = threadIdx.x; f < nt * f4; f += kAttnThreads) {
+        const int r = f / f4, c4 = f - r * f4;
+        *reinterpret_cast<float4*>(kt + r * hsp + 4 * c4) = *reinterpret_cast<const float4*>(kbase + (size_t)r * hs + 4 * c4);
+    }
     for (int d = threadIdx.x; d < hs; d += kAttnThreads) qs[d] = q[(size_t)h * hs + d];
     __syncthreads();
-    const float rs = sqrtf((float)hs);
-    const float* kbase = kcache + (size_t)(h / kv_mul) * max_t * hs;
-    for (int t = t0 + threadIdx.x; t < t1; t += kAttnThreads)
-        scores[(size_t)h * max_t + t] = attn_dot_runq(qs, kbase + (size_t)t * hs, hs) / rs;
-}
-
-constexpr int kAttnVSlice = 64;    // output elements per softmax/V workgroup
-constexpr int kAttnVTile = 64;     // positions per staged V tile
-
-__host__ __device__ constexpr size_t attn_v_lds_bytes(int max_t) {
-    return ((size_t)max_t + 2 * kAttnVTile * kAttnVSlice + 8) * sizeof(float);
+    if (threadIdx.x < nt) {
+        const float* kr = kt + threadIdx.x * hsp;
+        const int nv = hs & ~7;
+        float score = 0.0f;
+        int i = 0;
+        for (; i < nv; i += 4) {
+            const float4 k4 = *reinterpret_cast<const float4*>(kr + i);
+            const float4 q4 = *reinterpret_cast<const float4*>(qs + i);
+            score = score + q4.x * k4.x;
+            score = score + q4.y * k4.y;
+            score = score + q4.z * k4.z;
+            score = score + q4.w * k4.w;
+        }
+        for (; i < hs; i++) score = __builtin_fmaf(qs[i], kr[i], score);
+        scores[(size_t)h * max_t + t0 + threadIdx.x] = score / sqrtf((float)hs);
+    }
 }
 
 __global__ __launch_bounds__(kAttnThreads) void k_attn_softmax_v(
@@ -328,60 +326,99 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn_softmax_v(
     const int* __restrict__ meta, int pos_arg, int kv_mul, int hs, int max_t) {
 #pragma clang fp contract(off)
     extern __shared__ __attribute__((aligned(16))) float smem[];
-    float* p = smem;                               // [max_t] probabilities
-    float* vt = smem + max_t;                      // [2][kAttnVTile][kAttnVSlice]
-    float* red = vt + 2 * kAttnVTile * kAttnVSlice;    // [4] wave maxima, [4] sum
-    const int h = blockIdx.x, d0 = blockIdx.y * kAttnVSlice;
+    float* p = smem;                                     // [max_t] probabilities
+    float* vb = smem + ((max_t + 3) & ~3);               // [2][kVChunk][kVSlice]
+    float* red = vb + 2 * kVChunk * kVSlice;             // [4] wave maxima, [4] sum
+    const int h = blockIdx.x, d0 = blockIdx.y * kVSlice;
     const int tid = threadIdx.x, lane = tid & (L2Q_WAVE - 1), wv = tid / L2Q_WAVE;
     const int pos = meta_pos(meta, pos_arg);
     const int n = pos + 1;
+    const int width = min(kVSlice, hs - d0);
     const float* sc = scores + (size_t)h * max_t;
-    // max (order-free)
+    const float* vbase = vcache + (size_t)(h / kv_mul) * max_t * hs + d0;
+    const int nchunks = (n + kVChunk - 1) / kVChunk;
+
+    // scores first, then the first V chunk (loads complete in order)
+    float s[kScorePer];
+#pragma unroll
+    for (int k = 0; k < kScorePer; k++) {
+        const int t = tid + kAttnThreads * k;
+        s[k] = t < n ? sc[t] : -INFINITY;
+    }
+    float4 vr[kVPer];
+    auto load_chunk = [&](int c) {
+#pragma unroll
+        for (int k = 0; k < kVPer; k++) {
+            const int e = tid + kAttnThreads * k;                 // float4 index in the chunk
+            const int r = e / (kVSlice / 4), c4 = e % (kVSlice / 4);
+            const int t = c * kVChunk + r;
+            vr[k] = (t < n && 4 * c4 < width) ? *reinterpret_cast<const float4*>(vbase + (size_t)t * hs + 4 * c4)
+                                              : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        }
+    };
+    auto store_chunk = [&](int buf) {
+        float* dst = vb + buf * kVChunk * kVSlice;
+#pragma unroll
+        for (int k = 0; k < kVPer; k++) reinterpret_cast<float4*>(dst)[tid + kAttnThreads * k] = vr[k];
+    };
+    load_chunk(0);
+
+    // softmax in the reference's order
     float m = -INFINITY;
-    for (int t = tid; t < n; t += kAttnThreads) m = fmaxf(m, sc[t]);
+#pragma unroll
+    for (int k = 0; k < kScorePer; k++) m = fmaxf(m, s[k]);
     m = wave_max(m);
     if (lane == 0) red[wv] = m;
     __syncthreads();
     m = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
-    for (int t = tid; t < n; t += kAttnThreads) p[t] = exp_runq(sc[t] - m);
+#pragma unroll
+    for (int k = 0; k < kScorePer; k++) {
+        const int t = tid + kAttnThreads * k;
+        if (t < n) p[t] = exp_runq(s[k] - m);
+    }
     __syncthreads();
     if (tid == 0) {
         float sum = 0.0f;
-        for (int t = 0; t < n; t++) sum += p[t];
+        int t = 0;
+        for (; t + 8 <= n; t += 8) {
+            float e[8];
+#pragma unroll
+            for (int u = 0; u < 8; u++) e[u] = p[t + u];
+#pragma unroll
+            for (int u = 0; u < 8; u++) sum += e[u];
+        }
+        for (; t < n; t++) sum += p[t];
         red[4] = sum;
     }
     __syncthreads();
     const float sum = red[4];
-    for (int t = tid; t < n; t += kAttnThreads) p[t] = p[t] / sum;
+#pragma unroll
+    for (int k = 0; k < kScorePer; k++) {
+        const int t = tid + kAttnThreads * k;
+        if (t < n) p[t] = p[t] / sum;
+    }
+    store_chunk(0);
+    __syncthreads();
 
-    // V: waves 1..3 stage tiles of [kAttnVTile positions][kAttnVSlice dims]
-    // into a double buffer; wave 0 runs the serial per-element chains.
-    const float* vbase = vcache + (size_t)(h / kv_mul) * max_t * hs + d0;
-    const int width = min(kAttnVSlice, hs - d0);
-    const int ntiles = (n + kAttnVTile - 1) / kAttnVTile;
-    auto stage = [&](int tile, int buf) {
-        // 192 threads of waves 1..3 copy nt rows of `width` floats
-        const int tb = tile * kAttnVTile;
-        const int nt = min(kAttnVTile, n - tb);
-        float* dst = vt + buf * kAttnVTile * kAttnVSlice;
-        for (int e = tid - L2Q_WAVE; e < nt * kAttnVSlice; e += kAttnThreads - L2Q_WAVE) {
-            const int r = e / kAttnVSlice, c = e - r * kAttnVSlice;
-            if (c < width) dst[e] = vbase[(size_t)(tb + r) * hs + c];
-        }
-    };
-    if (wv > 0) stage(0, 0);
-    __syncthreads();   // also publishes p[]
+    // serial p*V chains, one lane per output element, V double-buffered in LDS
     float acc = 0.0f;
-    for (int tile = 0; tile < ntiles; tile++) {
-        const int buf = tile & 1;
-        if (wv > 0) {
-            if (tile + 1 < ntiles) stage(tile + 1, buf ^ 1);
-        } else if (lane < width) {
-            const int tb = tile * kAttnVTile;
-            const int nt = min(kAttnVTile, n - tb);
-            const float* src = vt + buf * kAttnVTile * kAttnVSlice + lane;
-            for (int j = 0; j < nt; j++) acc = __builtin_fmaf(p[tb + j], src[j * kAttnVSlice], acc);
+    for (int c = 0; c < nchunks; c++) {
+        if (c + 1 < nchunks) load_chunk(c + 1);
+        if (wv == 0 && lane < width) {
+            const int tb = c * kVChunk;
+            const int nt = min(kVChunk, n - tb);
+            const float* src = vb + (c & 1) * kVChunk * kVSlice + lane;
+            int j = 0;
+            for (; j + 8 <= nt; j += 8) {
+                float pv[8], vv[8];
+#pragma unroll
+                for (int u = 0; u < 8; u++) { pv[u] = p[tb + j + u]; vv[u] = src[(j + u) * kVSlice]; }
+#pragma unroll
+                for (int u = 0; u < 8; u++) acc = __builtin_fmaf(pv[u], vv[u], acc);
+            }
+            for (; j < nt; j++) acc = __builtin_fmaf(p[tb + j], src[j * kVSlice], acc);
         }
+        if (c + 1 < nchunks) store_chunk((c + 1) & 1);
         __syncthreads();
     }
     if (wv == 0 && lane < width) out[(size_t)h * hs + d0 + lane] = acc;

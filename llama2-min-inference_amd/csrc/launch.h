@@ -15,8 +15,10 @@ void set_error(const char* fmt, ...) __attribute__((format(printf, 1, 2)));
 int hip_fail(hipError_t e, const char* what);   // records and returns L2Q_ERR_HIP
 int check_launch(const char* what);             // hipGetLastError after a launch
 
-// GEMV: bits 4/8, group 32/64.  Validates shape and 16-byte alignment.
-int launch_gemv(int bits, int group, const GemvArgs& a, hipStream_t st);
+// GEMV: bits 4/8, group 32/64, prologue kPreq/kQuant/kNorm, epilogue
+// kStore/kRopeKV/kSwiglu (see gemv.h).  Validates shapes and alignment.
+int launch_gemv_fused(int bits, int group, int pro, int epi, const GemvArgs& a, hipStream_t st);
+int launch_gemv(int bits, int group, const GemvArgs& a, hipStream_t st);   // kPreq + kStore
 
 int launch_quantize(const float* x, int n, int group, int8_t* xq, float* xs, hipStream_t st);
 

@@ -32,50 +32,113 @@ int check_launch(const char* what) {
 static bool aligned16(const void* p) { return ((uintptr_t)p & 15) == 0; }
 
 // ---------------------------------------------------------------------------
-// GEMV dispatch.  T = groups per lane = ceil((cols/G)/64); the per-wave LDS
-// fold area bounds it (7 -> cols <= 448*G).
-constexpr int kMaxT = 7;
+// GEMV dispatch.  NS = 1 KiB sweeps per row = ceil(cols*bits/8 / 1024).
+constexpr int kMaxNS = 12;
 
 bool gemv_shape_ok(int bits, int group, int rows, int cols) {
     if (bits != 4 && bits != 8) return false;
     if (group != 32 && group != 64) return false;
     if (rows <= 0 || cols <= 0 || cols % group) return false;
-    const int T = (cols / group + L2Q_WAVE - 1) / L2Q_WAVE;
-    return T <= kMaxT;
+    return gemv_sweeps(bits, cols) <= kMaxNS;
 }
 
-template <int BITS, int G, int T>
+// Workgroups of a persistent GEMV launch: as many tiles per workgroup as
+// it takes to fit every workgroup on the device at once, spread evenly.
+static int resident_blocks(const void* fn, size_t lds) {
+    struct Entry { const void* fn; size_t lds; int dev; int blocks; };
+    static thread_local Entry cache[64];
+    static thread_local int used = 0;
+    int dev = 0;
+    (void)hipGetDevice(&dev);
+    for (int i = 0; i < used; i++)
+        if (cache[i].fn == fn && cache[i].lds == lds && cache[i].dev == dev) return cache[i].blocks;
+    int per_cu = 0, cus = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fn, kGemvThreads, lds) != hipSuccess || per_cu < 1) per_cu = 1;
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus < 1) cus = 1;
+    (void)hipGetLastError();
+    const int blocks = per_cu * cus;
+    if (used < 64) cache[used++] = Entry{fn, lds, dev, blocks};
+    return blocks;
+}
+
+template <int BITS, int G, int NS, int PRO, int EPI>
 static int go_gemv(const GemvArgs& a, hipStream_t st) {
-    const int blocks = (a.rows + kGemvRowsPerBlock - 1) / kGemvRowsPerBlock;
-    hipLaunchKernelGGL((k_gemv<BITS, G, T>), dim3(blocks), dim3(256), gemv_lds_bytes(a.cols / G), st, a);
+    constexpr int RB = gemv_rows_per_block(NS);
+    const int ntiles = (a.rows + RB - 1) / RB;
+    const size_t lds = gemv_lds_bytes(PRO, a.cols, G, BITS);
+    const int maxb = resident_blocks(reinterpret_cast<const void*>(&k_gemv<BITS, G, NS, PRO, EPI>), lds);
+    const int per = (ntiles + maxb - 1) / maxb;
+    const int blocks = (ntiles + per - 1) / per;
+    hipLaunchKernelGGL((k_gemv<BITS, G, NS, PRO, EPI>), dim3(blocks), dim3(kGemvThreads), lds, st, a);
     return check_launch("gemv");
 }
 
-template <int BITS, int G>
+template <int BITS, int G, int PRO, int EPI>
 static int gemv_by_t(const GemvArgs& a, hipStream_t st) {
-    const int T = (a.cols / G + L2Q_WAVE - 1) / L2Q_WAVE;
-    switch (T) {
-        case 1: return go_gemv<BITS, G, 1>(a, st);
-        case 2: return go_gemv<BITS, G, 2>(a, st);
-        case 3: return go_gemv<BITS, G, 3>(a, st);
-        case 4: return go_gemv<BITS, G, 4>(a, st);
-        case 5: return go_gemv<BITS, G, 5>(a, st);
-        case 6: return go_gemv<BITS, G, 6>(a, st);
-        case 7: return go_gemv<BITS, G, 7>(a, st);
+    const int NS = gemv_sweeps(BITS, a.cols);
+    switch (NS) {
+        case 1: return go_gemv<BITS, G, 1, PRO, EPI>(a, st);
+        case 2: return go_gemv<BITS, G, 2, PRO, EPI>(a, st);
+        case 3: return go_gemv<BITS, G, 3, PRO, EPI>(a, st);
+        case 4: return go_gemv<BITS, G, 4, PRO, EPI>(a, st);
     }
-    set_error("gemv: cols/group = %d groups exceeds %d", a.cols / G, kMaxT * L2Q_WAVE);
+    if constexpr (PRO != kNorm) {   // the norm prologue only ever sees dim-long inputs
+        switch (NS) {
+            case 5: return go_gemv<BITS, G, 5, PRO, EPI>(a, st);
+            case 6: return go_gemv<BITS, G, 6, PRO, EPI>(a, st);
+            case 7: return go_gemv<BITS, G, 7, PRO, EPI>(a, st);
+            case 8: return go_gemv<BITS, G, 8, PRO, EPI>(a, st);
+            case 9: return go_gemv<BITS, G, 9, PRO, EPI>(a, st);
+            case 10: return go_gemv<BITS, G, 10, PRO, EPI>(a, st);
+            case 11: return go_gemv<BITS, G, 11, PRO, EPI>(a, st);
+            case 12: return go_gemv<BITS, G, 12, PRO, EPI>(a, st);
+        }
+    }
+    set_error("gemv: %d columns exceed the supported range for this prologue", a.cols);
     return L2Q_ERR_ARG;
 }
 
-int launch_gemv(int bits, int group, const GemvArgs& a, hipStream_t st) {
+template <int PRO, int EPI>
+static int gemv_by_bits(int bits, int group, const GemvArgs& a, hipStream_t st) {
+    if (bits == 4) return group == 32 ? gemv_by_t<4, 32, PRO, EPI>(a, st) : gemv_by_t<4, 64, PRO, EPI>(a, st);
+    return group == 32 ? gemv_by_t<8, 32, PRO, EPI>(a, st) : gemv_by_t<8, 64, PRO, EPI>(a, st);
+}
+
+int launch_gemv_fused(int bits, int group, int pro, int epi, const GemvArgs& a, hipStream_t st) {
     if (!gemv_shape_ok(bits, group, a.rows, a.cols)) {
         set_error("gemv: unsupported shape bits=%d group=%d rows=%d cols=%d", bits, group, a.rows, a.cols);
         return L2Q_ERR_ARG;
     }
-    if (!a.out || !a.xq || !a.xs || !a.w || !a.ws) { set_error("gemv: null pointer"); return L2Q_ERR_ARG; }
-    if (!aligned16(a.w) || !aligned16(a.xq)) { set_error("gemv: weights and activations must be 16-byte aligned"); return L2Q_ERR_ARG; }
-    if (bits == 4) return group == 32 ? gemv_by_t<4, 32>(a, st) : gemv_by_t<4, 64>(a, st);
-    return group == 32 ? gemv_by_t<8, 32>(a, st) : gemv_by_t<8, 64>(a, st);
+    if (!a.w || !a.ws || !aligned16(a.w)) { set_error("gemv: weights must be non-null and 16-byte aligned"); return L2Q_ERR_ARG; }
+    if (pro == kPreq && (!a.xq || !a.xs || !aligned16(a.xq))) {
+        set_error("gemv: activations must be non-null and 16-byte aligned");
+        return L2Q_ERR_ARG;
+    }
+    if (pro != kPreq && !a.x_in && !(pro == kNorm && a.emb)) { set_error("gemv: null prologue input"); return L2Q_ERR_ARG; }
+    if (pro == kNorm && (!a.norm_w || (a.emb && !a.meta))) { set_error("gemv: null norm weight / meta"); return L2Q_ERR_ARG; }
+    if (gemv_lds_bytes(pro, a.cols, group, bits) > 65536) { set_error("gemv: cols=%d needs too much LDS", a.cols); return L2Q_ERR_ARG; }
+    if (pro == kNorm && gemv_sweeps(bits, a.cols) > 4) {
+        set_error("gemv: the norm prologue supports rows of at most 4 KiB");
+        return L2Q_ERR_ARG;
+    }
+    if (epi == kRopeKV && (!a.meta || !a.rope || !a.kcache || !a.vcache || a.hs <= 0 || a.hs % 2 || a.dim % a.hs ||
+                           a.kv_dim % a.hs || a.rows != a.dim + 2 * a.kv_dim || !a.out || a.max_t <= 0)) {
+        set_error("gemv: bad RoPE/KV epilogue arguments");
+        return L2Q_ERR_ARG;
+    }
+    if (!a.out) { set_error("gemv: null output"); return L2Q_ERR_ARG; }
+    if (epi == kSwiglu && a.rows % 2) { set_error("gemv: the SwiGLU epilogue needs (w1, w3) row pairs"); return L2Q_ERR_ARG; }
+    if (pro == kPreq && epi == kStore) return gemv_by_bits<kPreq, kStore>(bits, group, a, st);
+    if (pro == kQuant && epi == kStore) return gemv_by_bits<kQuant, kStore>(bits, group, a, st);
+    if (pro == kNorm && epi == kStore) return gemv_by_bits<kNorm, kStore>(bits, group, a, st);
+    if (pro == kNorm && epi == kRopeKV) return gemv_by_bits<kNorm, kRopeKV>(bits, group, a, st);
+    if (pro == kNorm && epi == kSwiglu) return gemv_by_bits<kNorm, kSwiglu>(bits, group, a, st);
+    set_error("gemv: unsupported prologue/epilogue combination %d/%d", pro, epi);
+    return L2Q_ERR_ARG;
+}
+
+int launch_gemv(int bits, int group, const GemvArgs& a, hipStream_t st) {
+    return launch_gemv_fused(bits, group, kPreq, kStore, a, st);
 }
 
 // ---------------------------------------------------------------------------
@@ -144,23 +207,28 @@ int launch_attention_split(const float* q, const float* kcache, const float* vca
     return check_launch("attention_combine");
 }
 
-bool attention_exact_ok(int max_t) { return attn_v_lds_bytes(max_t) <= 65536; }
+bool attention_exact_ok(int max_t) {
+    return max_t <= kScorePer * kAttnThreads && attn_v_lds_bytes(max_t) <= 65536;
+}
 
 int launch_attention_exact(const float* q, const float* kcache, const float* vcache, float* out, float* scores,
                            int S, const int* meta, int pos, int n_heads, int n_kv_heads, int hs, int max_t,
                            hipStream_t st) {
-    if (!attention_shape_ok(n_heads, n_kv_heads, hs) || S <= 0 || max_t <= 0 || !attention_exact_ok(max_t) ||
+    (void)S;
+    if (!attention_shape_ok(n_heads, n_kv_heads, hs) || max_t <= 0 || !attention_exact_ok(max_t) ||
         (!meta && (pos < 0 || pos >= max_t))) {
-        set_error("attention: bad shape heads=%d kv_heads=%d hs=%d S=%d pos=%d max_t=%d", n_heads, n_kv_heads, hs, S,
-                  pos, max_t);
+        set_error("attention: bad shape heads=%d kv_heads=%d hs=%d pos=%d max_t=%d", n_heads, n_kv_heads, hs, pos,
+                  max_t);
         return L2Q_ERR_ARG;
     }
     const int kv_mul = n_heads / n_kv_heads;
-    hipLaunchKernelGGL(k_attn_scores, dim3(n_heads, S), dim3(kAttnThreads), 0, st, q, kcache, scores, meta, pos,
-                       kv_mul, hs, max_t);
+    // the graph covers every position the cache can hold; blocks past pos exit
+    const int tiles = meta ? (max_t + kScoreTile - 1) / kScoreTile : (pos + kScoreTile) / kScoreTile;
+    hipLaunchKernelGGL(k_attn_scores, dim3(n_heads, tiles), dim3(kAttnThreads), attn_scores_lds_bytes(hs), st, q,
+                       kcache, scores, meta, pos, kv_mul, hs, max_t);
     int rc = check_launch("attention_scores");
     if (rc) return rc;
-    hipLaunchKernelGGL(k_attn_softmax_v, dim3(n_heads, (hs + kAttnVSlice - 1) / kAttnVSlice), dim3(kAttnThreads),
+    hipLaunchKernelGGL(k_attn_softmax_v, dim3(n_heads, (hs + kVSlice - 1) / kVSlice), dim3(kAttnThreads),
                        attn_v_lds_bytes(max_t), st, scores, vcache, out, meta, pos, kv_mul, hs, max_t);
     return check_launch("attention_softmax_v");
 }
@@ -239,13 +307,15 @@ int l2q_quantize_act(const float* x, int n, int group, int8_t* xq, float* xs, vo
 
 int l2q_gemv_q8(float* out, const int8_t* xq, const float* xs, const int8_t* w, const float* ws, int rows, int cols,
                 int group, int32_t* dots, void* stream) {
-    GemvArgs a{out, xq, xs, w, ws, rows, cols, dots};
+    GemvArgs a{};
+    a.out = out; a.xq = xq; a.xs = xs; a.w = w; a.ws = ws; a.rows = rows; a.cols = cols; a.dots = dots;
     return launch_gemv(8, group, a, (hipStream_t)stream);
 }
 
 int l2q_gemv_q4(float* out, const int8_t* xq, const float* xs, const uint8_t* w, const float* ws, int rows, int cols,
                 int group, int32_t* dots, void* stream) {
-    GemvArgs a{out, xq, xs, w, ws, rows, cols, dots};
+    GemvArgs a{};
+    a.out = out; a.xq = xq; a.xs = xs; a.w = w; a.ws = ws; a.rows = rows; a.cols = cols; a.dots = dots;
     return launch_gemv(4, group, a, (hipStream_t)stream);
 }
 

@@ -228,6 +228,24 @@ size_t qll_synth_size(const l2q_config* c, int wbits, int group) {
 /* Stream ids of the tensors of a synthetic model. */
 enum { S_EMB = 1, S_WQ = 3, S_WK, S_WV, S_WO, S_W1 = 8, S_W2, S_W3, S_WCLS = 12 };
 
+/* Fill row r of a [rows][cols] matrix stream: elements come in Box-Muller
+ * pairs (2k, 2k+1) sharing one (u1, u2) draw, so each pair costs one log,
+ * one sqrt and one sincos; values equal qll_gauss(seed, stream, r*cols+j). */
+static void gauss_row(float* row, size_t cols, uint64_t key, uint64_t first, float sigma) {
+    size_t j = 0;
+    if (first & 1) { row[0] = sigma * gauss_from_key(key, first); j = 1; }
+    for (; j + 1 < cols; j += 2) {
+        uint64_t h = splitmix64(key + ((first + j) >> 1));
+        float u1 = (float)((h >> 40) + 1) * (1.0f / 16777216.0f);
+        float u2 = (float)((h >> 8) & 0xFFFFFFu) * (1.0f / 16777216.0f);
+        float r = sqrtf(-2.0f * logf(u1));
+        float th = 6.28318530717958647692f * u2;
+        row[j] = sigma * (r * cosf(th));
+        row[j + 1] = sigma * (r * sinf(th));
+    }
+    if (j < cols) row[j] = sigma * gauss_from_key(key, first + j);
+}
+
 static void synth_matrix(uint8_t* base, size_t off, size_t off_s, size_t rows, size_t cols,
                          int wbits, int group, float div, uint64_t seed, uint64_t stream,
                          float sigma) {
@@ -239,8 +257,7 @@ static void synth_matrix(uint8_t* base, size_t off, size_t off_s, size_t rows, s
         float* row = (float*)malloc(cols * sizeof(float));
         #pragma omp for schedule(static)
         for (long long r = 0; r < (long long)rows; r++) {
-            for (size_t j = 0; j < cols; j++)
-                row[j] = sigma * gauss_from_key(key, (uint64_t)r * cols + j);
+            gauss_row(row, cols, key, (uint64_t)r * cols, sigma);
             uint8_t* q = base + off + (size_t)r * rb;
             float* s = (float*)(base + off_s) + (size_t)r * nb;
             if (wbits == 4) qll_quantize_row_q4(row, (int)cols, group, div, q, s);
@@ -264,7 +281,7 @@ int qll_synth_write(void* dst, const l2q_config* c, int wbits, int group,
         float* emb = (float*)(base + lay.emb);
         uint64_t key = stream_key(seed, S_EMB);
         #pragma omp parallel for schedule(static)
-        for (long long i = 0; i < (long long)(V * d); i++) emb[i] = sigma * gauss_from_key(key, (uint64_t)i);
+        for (long long r = 0; r < (long long)V; r++) gauss_row(emb + (size_t)r * d, d, key, (uint64_t)r * d, sigma);
     }
     float* ra = (float*)(base + lay.rms_att);
     float* rf = (float*)(base + lay.rms_ffn);

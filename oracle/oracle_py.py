@@ -73,16 +73,18 @@ def matmul(bits: int, xq, xs, xt, w, ws, rows: int, cols: int, group: int, want_
     file (INT8: biased u8 [rows][cols]; INT4: packed [rows][cols/2])."""
     out = np.empty(rows, dtype=np.float32)
     dots = np.empty((rows, cols // group), dtype=np.int32) if want_dots else None
+    xq, xs, xt = (np.ascontiguousarray(a) for a in (xq, xs, xt))
+    w, ws = np.ascontiguousarray(w), np.ascontiguousarray(ws)
     f = olib().orc_matmul_q4 if bits == 4 else olib().orc_matmul_q8
-    f(_p(out), _p(xq), _p(xs), _p(xt), _p(np.ascontiguousarray(w)), _p(np.ascontiguousarray(ws)),
-      rows, cols, group, _p(dots))
+    f(_p(out), _p(xq), _p(xs), _p(xt), _p(w), _p(ws), rows, cols, group, _p(dots))
     return out, dots
 
 
 def rmsnorm(x: np.ndarray, w: np.ndarray) -> np.ndarray:
     x = np.ascontiguousarray(x, dtype=np.float32)
+    w = np.ascontiguousarray(w, dtype=np.float32)
     o = np.empty_like(x)
-    olib().orc_rmsnorm(_p(o), _p(x), _p(np.ascontiguousarray(w, dtype=np.float32)), x.size)
+    olib().orc_rmsnorm(_p(o), _p(x), _p(w), x.size)
     return o
 
 
@@ -122,8 +124,9 @@ def attention(q: np.ndarray, kcache: np.ndarray, vcache: np.ndarray, pos: int, n
 
 def swiglu(h: np.ndarray, h2: np.ndarray) -> np.ndarray:
     h = np.ascontiguousarray(h, dtype=np.float32)
+    h2 = np.ascontiguousarray(h2, dtype=np.float32)
     out = np.empty_like(h)
-    olib().orc_swiglu(_p(out), _p(h), _p(np.ascontiguousarray(h2, dtype=np.float32)), h.size)
+    olib().orc_swiglu(_p(out), _p(h), _p(h2), h.size)
     return out
 
 
@@ -188,6 +191,7 @@ def rlib():
         L = C.CDLL(REF_LIB)
         sig = {
             "ref_open": (I, [C.c_char_p]),
+            "ref_open_memory": (I, [P, C.c_size_t]),
             "ref_config": (None, [P]),
             "ref_forward": (C.POINTER(C.c_float), [I, I]),
             "ref_close": (None, []),
@@ -196,6 +200,14 @@ def rlib():
             "ref_rmsnorm": (None, [P, P, P, I]),
             "ref_softmax": (None, [P, I]),
             "ref_sample_argmax": (I, [P, I]),
+            "ref_tok_open": (None, [C.c_char_p, I]),
+            "ref_tok_encode": (I, [C.c_char_p, I, I, P]),
+            "ref_tok_decode": (C.c_char_p, [I, I]),
+            "ref_tok_close": (None, []),
+            "ref_sampler_open": (None, [I, C.c_float, C.c_float, C.c_ulonglong]),
+            "ref_sample": (I, [P]),
+            "ref_sampler_state": (C.c_ulonglong, []),
+            "ref_sampler_close": (None, []),
         }
         for n, (r, a) in sig.items():
             f = getattr(L, n)
@@ -206,10 +218,17 @@ def rlib():
 
 
 class RefRunq:
-    """runq.c's Transformer on a QLL8 (version 1, group 32) file."""
+    """runq.c's Transformer on a QLL8 (version 1, group 32) file, or on a
+    checkpoint image in memory (``image``: uint8 array of a whole file)."""
 
-    def __init__(self, path: str):
-        self.vocab = rlib().ref_open(path.encode())
+    def __init__(self, path: str = None, image: np.ndarray = None):
+        if image is not None:
+            self._image = image
+            self.vocab = rlib().ref_open_memory(_p(image), image.nbytes)
+            if self.vocab < 0:
+                raise ValueError("not a QLL8 version-1 image")
+        else:
+            self.vocab = rlib().ref_open(path.encode())
         cfg = np.empty(7, dtype=np.int32)
         rlib().ref_config(_p(cfg))
         self.cfg = [int(v) for v in cfg]
@@ -243,13 +262,52 @@ def ref_quantize_act(x: np.ndarray):
 
 def ref_matmul_q8(xq, xs, xt, w_u8, ws, rows: int, cols: int) -> np.ndarray:
     out = np.empty(rows, dtype=np.float32)
-    rlib().ref_matmul_q8(_p(out), _p(xq), _p(xs), _p(xt), _p(np.ascontiguousarray(w_u8)),
-                         _p(np.ascontiguousarray(ws)), rows, cols)
+    xq, xs, xt = (np.ascontiguousarray(a) for a in (xq, xs, xt))
+    w_u8, ws = np.ascontiguousarray(w_u8), np.ascontiguousarray(ws)
+    rlib().ref_matmul_q8(_p(out), _p(xq), _p(xs), _p(xt), _p(w_u8), _p(ws), rows, cols)
     return out
 
 
 def ref_rmsnorm(x: np.ndarray, w: np.ndarray) -> np.ndarray:
     x = np.ascontiguousarray(x, dtype=np.float32).copy()
+    w = np.ascontiguousarray(w, dtype=np.float32).copy()
     o = np.empty_like(x)
-    rlib().ref_rmsnorm(_p(o), _p(x), _p(np.ascontiguousarray(w, dtype=np.float32).copy()), x.size)
+    rlib().ref_rmsnorm(_p(o), _p(x), _p(w), x.size)
     return o
+
+
+class RefTokenizer:
+    """runq.c's build_tokenizer / encode / decode."""
+
+    def __init__(self, path: str, vocab_size: int):
+        rlib().ref_tok_open(path.encode(), vocab_size)
+
+    def encode(self, text: str, bos: bool = True, eos: bool = False):
+        b = text.encode()
+        out = np.empty(len(b) + 3, dtype=np.int32)
+        n = rlib().ref_tok_encode(b, int(bos), int(eos), _p(out))
+        return [int(v) for v in out[:n]]
+
+    def decode(self, prev: int, token: int) -> bytes:
+        return rlib().ref_tok_decode(prev, token)
+
+    def close(self):
+        rlib().ref_tok_close()
+
+
+class RefSampler:
+    """runq.c's build_sampler / sample."""
+
+    def __init__(self, vocab_size: int, temperature: float, topp: float, seed: int):
+        rlib().ref_sampler_open(vocab_size, temperature, topp, seed)
+
+    def sample(self, logits: np.ndarray) -> int:
+        buf = np.ascontiguousarray(logits, dtype=np.float32).copy()
+        return rlib().ref_sample(_p(buf))
+
+    @property
+    def rng_state(self) -> int:
+        return rlib().ref_sampler_state()
+
+    def close(self):
+        rlib().ref_sampler_close()

@@ -16,9 +16,35 @@ static int g_open = 0;
 
 /* build_transformer (runq.c:280) on a QLL8 v1 file. */
 int ref_open(char* checkpoint) {
-    if (g_open) { free_transformer(&g_t); g_open = 0; }
+    if (g_open == 1) free_transformer(&g_t);
+    else if (g_open == 2) free_run_state(&g_t.state);
+    g_open = 0;
     build_transformer(&g_t, checkpoint);
     g_open = 1;
+    return g_t.config.vocab_size;
+}
+
+/* The same set-up from a QLL8 v1 image already in memory (no file):
+ * header checks as read_checkpoint (runq.c:259-268), then the reference's
+ * memory_map_weights and malloc_run_state.  `data` must outlive the model. */
+int ref_open_memory(uint8_t* data, size_t size) {
+    if (g_open == 1) free_transformer(&g_t);
+    else if (g_open == 2) free_run_state(&g_t.state);
+    g_open = 0;
+    uint32_t magic, version;
+    if (size < 36) return -1;
+    memcpy(&magic, data, 4);
+    memcpy(&version, data + 4, 4);
+    if (magic != QMAGIC || version != QVERSION) return -1;
+    memcpy(&g_t.config, data + 8, sizeof(Config));
+    int shared = g_t.config.vocab_size > 0 ? 1 : 0;
+    g_t.config.vocab_size = abs(g_t.config.vocab_size);
+    g_t.fd = -1;
+    g_t.data = MAP_FAILED;
+    g_t.file_size = (ssize_t)size;
+    memory_map_weights(&g_t.weights, &g_t.config, data + 2 * sizeof(uint32_t) + sizeof(Config), shared);
+    malloc_run_state(&g_t.state, &g_t.config);
+    g_open = 2;
     return g_t.config.vocab_size;
 }
 
@@ -36,7 +62,8 @@ float* ref_forward(int token, int pos) { return forward(&g_t, token, pos); }
 float* ref_state_x(void) { return g_t.state.x; }
 
 void ref_close(void) {
-    if (g_open) free_transformer(&g_t);
+    if (g_open == 1) free_transformer(&g_t);
+    else if (g_open == 2) free_run_state(&g_t.state);
     g_open = 0;
 }
 
@@ -57,3 +84,47 @@ void ref_matmul_q8(float* out, const int8_t* xq, const float* xs, const float* x
 void ref_rmsnorm(float* o, float* x, float* w, int n) { rmsnorm(o, x, w, n); }
 void ref_softmax(float* x, int n) { softmax(x, n); }
 int ref_sample_argmax(float* p, int n) { return sample_argmax(p, n); }
+
+/* ---- the reference's tokenizer and sampler (runq.c:426-667) ---------- */
+
+static Tokenizer g_tok;
+static int g_tok_open = 0;
+
+void ref_tok_open(char* path, int vocab_size) {
+    if (g_tok_open) free_tokenizer(&g_tok);
+    build_tokenizer(&g_tok, path, vocab_size);
+    g_tok_open = 1;
+}
+
+/* encode (runq.c:500); returns the number of tokens */
+int ref_tok_encode(char* text, int bos, int eos, int* tokens) {
+    int n = 0;
+    encode(&g_tok, text, (int8_t)bos, (int8_t)eos, tokens, &n);
+    return n;
+}
+
+char* ref_tok_decode(int prev, int token) { return decode(&g_tok, prev, token); }
+
+void ref_tok_close(void) {
+    if (g_tok_open) free_tokenizer(&g_tok);
+    g_tok_open = 0;
+}
+
+static Sampler g_smp;
+static int g_smp_open = 0;
+
+void ref_sampler_open(int vocab_size, float temperature, float topp, unsigned long long seed) {
+    if (g_smp_open) free_sampler(&g_smp);
+    build_sampler(&g_smp, vocab_size, temperature, topp, seed);
+    g_smp_open = 1;
+}
+
+/* sample (runq.c:652); modifies logits like the reference */
+int ref_sample(float* logits) { return sample(&g_smp, logits); }
+
+unsigned long long ref_sampler_state(void) { return g_smp.rng_state; }
+
+void ref_sampler_close(void) {
+    if (g_smp_open) free_sampler(&g_smp);
+    g_smp_open = 0;
+}
