@@ -135,6 +135,9 @@ def main():
     ap.add_argument("--prompt", type=int, default=128)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="first run a 256 MiB device copy (x4): a kernel of known traffic for scaling "
+                         "rocprofv3 FETCH_SIZE / WRITE_SIZE readings")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU; --gpus {args.gpus} is not supported "
@@ -145,6 +148,13 @@ def main():
     from llama2q import abi, host
     from llama2q.model import Engine
     assert torch.cuda.is_available(), "bench.py needs a GPU"
+    if args.copy_calibration:
+        src = torch.empty(256 << 20, dtype=torch.uint8, device="cuda")
+        dst = torch.empty_like(src)
+        for _ in range(4):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        del src, dst
 
     cfg = host.config_7b(seq_len=4096)
     group = 64
@@ -221,7 +231,8 @@ def main():
                    "positions": [pos_start, pos_start + args.steps - 1], "parallelism": "single GPU"},
         "roofline": {"bound": "hbm", "achieved": dom["GB/s"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": dom["frac"], "traffic": traffic,
-                     "kernel": "k_gemv<4,64,1> (INT4 g64 GEMV), 22016 x 4096 (w1|w3 of one layer)",
+                     "kernel": "k_gemv<4,64,2,0,0,2> (INT4 g64 GEMV, pre-quantized input), "
+                               "22016 x 4096 (w1|w3 of one layer)",
                      "bytes_per_launch": dom_bytes, "mean_us": dom["us"]},
         "cpu_baseline": cpu,
         "step_bytes_avg": int(avg_bytes),

@@ -146,7 +146,7 @@ int l2q_quantize_act(const float* x, int n, int group,
  * bit-identical to runq.c:142-159 (matmul_q8; v3-cuda-kvcache/run.cu:177-202
  * is the GPU counterpart).  If `dots` is not NULL the int32 group dots are
  * written to dots[r*(cols/group) + b].  w is signed int8 [rows][cols];
- * cols <= 448*group. */
+ * rows of at most 12 KiB (cols*bits/8 <= 12288). */
 int l2q_gemv_q8(float* out, const int8_t* xq, const float* xs,
                 const int8_t* w, const float* ws, int rows, int cols,
                 int group, int32_t* dots, void* stream);
@@ -194,7 +194,7 @@ int l2q_rope_kv_append(float* q, const float* k, const float* v,
  * reference's order (serial dot per position, expf identical to the host
  * C library's, serial softmax sum, serial p*V accumulation per element), so
  * the output is bit-identical to runq.c:367-391 (+ softmax :307-318).
- * max_t <= 8184 (the probabilities of a head are staged in LDS). */
+ * max_t <= 4096 (the probabilities of a head are staged in LDS). */
 int l2q_attention(const float* q, const float* kcache, const float* vcache,
                   float* out, int pos, int n_heads, int n_kv_heads,
                   int head_size, int max_t, void* stream);

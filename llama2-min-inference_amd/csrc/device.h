@@ -48,26 +48,44 @@ __device__ __forceinline__ float wave_max(float v) {
     return v;
 }
 
-// Reduction over aligned groups of `W` consecutive lanes (W a power of two
-// <= 64): every lane gets the result of its own group.
-template <int W>
-__device__ __forceinline__ float group_max(float v) {
-#pragma unroll
-    for (int o = W / 2; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, L2Q_WAVE));
-    return v;
+// Lane permutations inside 16-lane rows via DPP (a VALU operand modifier:
+// no LDS round trip, unlike __shfl_*).  quad_perm [1,0,3,2] and [2,3,0,1]
+// are lane^1 and lane^2; row_half_mirror maps lane i to 7-i within each
+// 8-lane half row; row_mirror maps i to 15-i within the row.
+enum : int { kDppXor1 = 0xB1, kDppXor2 = 0x4E, kDppMirror = 0x140, kDppHalfMirror = 0x141 };
+
+template <int CTRL>
+__device__ __forceinline__ int dpp_i(int v) {
+    return __builtin_amdgcn_update_dpp(0, v, CTRL, 0xF, 0xF, false);
+}
+template <int CTRL>
+__device__ __forceinline__ float dpp_f(float v) {
+    return __int_as_float(dpp_i<CTRL>(__float_as_int(v)));
 }
 
+// Max / integer sum over aligned groups of `W` consecutive lanes (W a power
+// of two <= 64): every lane gets the result of its own group.  Both are
+// exact in any order; within a 16-lane row the butterfly is xor1, xor2,
+// half mirror, mirror (after the last two steps every lane has seen all 16).
 template <int W>
-__device__ __forceinline__ float group_sum(float v) {
-#pragma unroll
-    for (int o = W / 2; o > 0; o >>= 1) v += __shfl_xor(v, o, L2Q_WAVE);
+__device__ __forceinline__ float group_max(float v) {
+    if (W >= 2) v = fmaxf(v, dpp_f<kDppXor1>(v));
+    if (W >= 4) v = fmaxf(v, dpp_f<kDppXor2>(v));
+    if (W >= 8) v = fmaxf(v, dpp_f<kDppHalfMirror>(v));
+    if (W >= 16) v = fmaxf(v, dpp_f<kDppMirror>(v));
+    if (W >= 32) v = fmaxf(v, __shfl_xor(v, 16, L2Q_WAVE));
+    if (W >= 64) v = fmaxf(v, __shfl_xor(v, 32, L2Q_WAVE));
     return v;
 }
 
 template <int W>
 __device__ __forceinline__ int group_isum(int v) {
-#pragma unroll
-    for (int o = W / 2; o > 0; o >>= 1) v += __shfl_xor(v, o, L2Q_WAVE);
+    if (W >= 2) v += dpp_i<kDppXor1>(v);
+    if (W >= 4) v += dpp_i<kDppXor2>(v);
+    if (W >= 8) v += dpp_i<kDppHalfMirror>(v);
+    if (W >= 16) v += dpp_i<kDppMirror>(v);
+    if (W >= 32) v += __shfl_xor(v, 16, L2Q_WAVE);
+    if (W >= 64) v += __shfl_xor(v, 32, L2Q_WAVE);
     return v;
 }
 
@@ -86,6 +104,23 @@ __device__ __forceinline__ int q8_value(float x, float s) {
     float r = rintf(x / s);
     r = fminf(fmaxf(r, -127.0f), 127.0f);
     return (int)r;
+}
+
+// q8_value(x, s) without a division on the common path.  With r = rcp(s)
+// (v_rcp_f32, within 1 ulp) y = x*r is within 4 ulp(y) of x/s, so rint(y)
+// equals rint(fl(x/s)) unless y lies within that distance of a half-integer
+// (the only places where the two can round differently), i.e. unless
+// |y - rint(y)| >= 0.5 - margin; there, and for non-finite y (s denormal or
+// tiny), the correctly rounded division is taken.  The margin used,
+// |y|*2^-20, is four times the error bound.  No clamp is needed: s is
+// amax/127 rounded, so |x/s| < 127.5 for every x of the group.
+__device__ __forceinline__ float q8_recip(float s) { return __builtin_amdgcn_rcpf(s); }
+
+__device__ __forceinline__ int q8_value_fast(float x, float s, float r) {
+    const float y = x * r;
+    float q = rintf(y);
+    if (__builtin_expect(!(fabsf(y - q) < __builtin_fmaf(-fabsf(y), 0x1p-20f, 0.5f)), 0)) q = rintf(x / s);
+    return (int)q;
 }
 
 // runq.c:137: xt = s * 128 * sum(q), the bias-correction term of the

@@ -63,7 +63,9 @@ L2Q_HD inline uint32_t bits_of(float f) {
     return u;
 }
 
-L2Q_HD inline float exp_runq(float x) {
+// tab: kExp2Tab or a copy of it (a kernel may keep one in LDS so that the
+// lookup is not a global load queued behind its weight stream).
+L2Q_HD inline float exp_runq_t(float x, const uint64_t* tab) {
     const double kInvLn2N = 0x1.71547652b82fep+0 * 32;
     const double kShift = 0x1.8p+52;
     const double c0 = 0x1.c6af84b912394p-5 / 32 / 32 / 32;
@@ -81,7 +83,7 @@ L2Q_HD inline float exp_runq(float x) {
     const uint64_t ki = bits_of(kd);
     kd -= kShift;
     const double r = __builtin_fma(kInvLn2N, xd, -kd);
-    const uint64_t t = kExp2Tab[ki % 32] + (ki << 47);
+    const uint64_t t = tab[ki % 32] + (ki << 47);
     const double s = double_of(t);
     const double z = __builtin_fma(c0, r, c1);
     const double r2 = r * r;
@@ -90,5 +92,7 @@ L2Q_HD inline float exp_runq(float x) {
     y = y * s;
     return (float)y;
 }
+
+L2Q_HD inline float exp_runq(float x) { return exp_runq_t(x, kExp2Tab); }
 
 }  // namespace l2q

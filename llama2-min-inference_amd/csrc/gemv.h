@@ -6,22 +6,26 @@
 // d_u8 = d + 128*sum(xq_b) and xt[b] = xs[b]*128*sum(xq_b).
 //
 // Mapping (wave64, no MFMA: at batch 1 this is a pure weight stream):
-//   - a workgroup (4 waves) owns tiles of 4*R consecutive rows, a wave R;
+//   - rows are cut into units of PR consecutive rows; every wave of the
+//     grid owns a contiguous, equal (+-1 unit) range of units, so the whole
+//     grid finishes together and each wave streams one contiguous region;
 //   - a row is read in sweeps of 1 KiB: in sweep s lane j loads the 16
 //     bytes at s*1024 + 16*j, so every load instruction of a wave covers
-//     one contiguous KiB (the best-coalesced form of the stream);
+//     one contiguous KiB (the best-coalesced form of the stream); the
+//     row's group scales are loaded by all 64 lanes (one dword each);
+//   - the next unit's loads are issued while the current unit is consumed
+//     (a ring of PR rows in registers), so loads are always in flight;
 //   - a group spans P = G*BITS/128 consecutive lanes (1, 2 or 4); their
-//     partial int32 dots and activation sums are combined with lane
-//     shuffles, exactly (integer adds);
+//     partial int32 dots and activation sums are combined with DPP lane
+//     moves, exactly (integer adds);
 //   - the activation chunk a lane needs is the same for every row, so it is
 //     loaded (or taken from the prologue's LDS copy) once into registers;
-//   - every weight load of the wave is issued before any dependent work, so
-//     the activation set-up and the prologue run while weights stream in;
 //   - INT4 nibbles are consumed in place (see dot8_q4_x16): no unpack to
 //     bytes, two v_dot4_i32_i8 per 8 weights;
-//   - per-(row, group) terms go to LDS and one lane per row folds them in
-//     group order, sum = fma(ws_b, t_b, sum), reproducing the reference's
-//     float accumulation bit for bit.
+//   - per-(row, group) terms and scales go to LDS and one lane per row
+//     folds them in group order, sum = fma(ws_b, t_b, sum), reproducing the
+//     reference's float accumulation bit for bit; the PR rows of a unit are
+//     folded by PR lanes at once, with the LDS reads issued ahead.
 //
 // Prologues (how the activation vector reaches the lanes):
 //   kPreq   int8 activations + scales already in HBM (xq, xs);
@@ -73,27 +77,75 @@ struct GemvArgs {
 };
 
 
-constexpr int kGemvWaves = 4;
-constexpr int kGemvThreads = kGemvWaves * L2Q_WAVE;
 constexpr int kSweepBytes = 16 * L2Q_WAVE;   // one 128-bit load per lane
+constexpr int kGemvUnit = 2;                 // rows per unit (PR): (even, odd) pairs for the epilogues
 
-// Rows per wave: 4, or 2 for long rows (keeps the weight registers of a
-// tile within the register file).
-__host__ __device__ constexpr int gemv_rows_per_wave(int NS) { return NS <= 4 ? 4 : 2; }
-__host__ __device__ constexpr int gemv_rows_per_block(int NS) { return kGemvWaves * gemv_rows_per_wave(NS); }
 __host__ __device__ constexpr int gemv_sweeps(int bits, int cols) { return (cols * bits / 8 + kSweepBytes - 1) / kSweepBytes; }
 
-// A prologue thread holds ceil(cols/1024) float4 chunks of the input; with
-// cols*BITS/8 <= 1024*NS that is at most NS*8/BITS.
-__host__ __device__ constexpr int prologue_chunks(int NS, int BITS) { return NS * 8 / BITS; }
+// One workgroup per CU, as many waves as the register budget allows (12 =
+// 3 per SIMD for rows of up to 3 sweeps, else 8): the workgroup-wide
+// prologue is then shared by every wave of the CU instead of being
+// recomputed by several workgroups.
+__host__ __device__ constexpr int gemv_waves(int NS) { return NS <= 3 ? 12 : 8; }
 
-// LDS layout (floats): [fold: 4 waves x R rows x (nb+1) x 2][act: cols int8 + nb scales][vs: cols (kNorm)][misc 4]
-__host__ __device__ constexpr size_t gemv_fold_floats(int nb, int NS) {
-    return (size_t)gemv_rows_per_block(NS) * (nb + 1) * 2;
+// Rows folded at once per wave (F lanes run F ordered FMA chains side by
+// side): the fold's instructions are issued for the whole wave whatever the
+// number of active lanes, so batching rows divides their cost by F/PR.  F
+// is 8, or 4 / 2 where the fold area would exceed 96 KiB of LDS.
+constexpr size_t kGemvFoldBudget = 96 * 1024;
+__host__ __device__ constexpr int gemv_nbp(int nb);
+__host__ __device__ constexpr int gemv_fold_rows(int nb, int waves) {
+    return (size_t)waves * 2 * 8 * gemv_nbp(nb) * 4 <= kGemvFoldBudget   ? 8
+           : (size_t)waves * 2 * 4 * gemv_nbp(nb) * 4 <= kGemvFoldBudget ? 4
+                                                                          : 2;
 }
-__host__ __device__ constexpr size_t gemv_lds_bytes(int pro, int cols, int group, int bits) {
-    return (gemv_fold_floats(cols / group, gemv_sweeps(bits, cols)) + (pro == kPreq ? 0 : (size_t)cols / 4 + cols / group) +
-            (pro == kNorm ? (size_t)cols : 0) + 4) * sizeof(float);
+
+// Scale sweeps (64 dwords each) for rows of at most NS weight sweeps.
+__host__ __device__ constexpr int gemv_scale_sweeps(int bits, int group, int NS) {
+    return (NS * kSweepBytes * 8 / bits / group + L2Q_WAVE - 1) / L2Q_WAVE;
+}
+
+// A prologue thread holds ceil(cols/4/threads) float4 chunks of the input;
+// with cols*BITS/8 <= 1024*NS that is at most ceil(NS*2048/(BITS*threads)).
+__host__ __device__ constexpr int prologue_chunks(int NS, int BITS, int threads) {
+    return (NS * 2048 / BITS + threads - 1) / threads;
+}
+
+// Row stride (floats) of the per-wave fold area: nb rounded up to a float4,
+// plus one float4 so that the PR folding lanes start on different banks.
+__host__ __device__ constexpr int gemv_nbp(int nb) { return (nb + 3) / 4 * 4 + 4; }
+
+// Row stride (floats) of the transposed norm input: row l holds elements
+// l, l+16, l+32, ... (one reference FMA accumulator each), padded to a
+// float4 multiple plus one float4 so that 16 lanes reading float4s at the
+// same step hit distinct banks.
+__host__ __device__ constexpr int sumsq_stride(int n) { return ((n + 15) / 16 + 3) / 4 * 4 + 4; }
+
+// LDS layout: [fold: waves x (terms, scales) x F x nbp floats]
+//             [act_q: cols int8, padded to 32 B][act_s: nb floats, padded to 4]
+//             [vt: the residual sum, transposed for the norm chains (kNorm): 16 x sumsq_stride(cols) floats]
+//             [misc: 4 floats | exp table: 32 doubles | RoPE row of the position: up to 256 floats]
+constexpr int kGemvMiscFloats = 4 + 64 + 256;
+__host__ __device__ constexpr size_t gemv_fold_floats(int nb, int waves) {
+    return (size_t)waves * 2 * gemv_fold_rows(nb, waves) * gemv_nbp(nb);
+}
+//
+// Rows of more than 4 sweeps keep the activations in LDS (read per chunk)
+// instead of registers, which keeps the kernel at two or more waves per
+// SIMD; the INT4 form is stored pre-split per 32-element chunk as
+// [even-column dwords E0..E3 | odd-column dwords O0..O3] (see act_split_addr).
+__host__ __device__ constexpr bool gemv_act_lds(int NS) { return NS > 4; }
+__host__ __device__ constexpr size_t gemv_lds_bytes(int pro, int cols, int group, int bits, int PR) {
+    return gemv_fold_floats(cols / group, gemv_waves(gemv_sweeps(bits, cols))) * sizeof(float) +
+           (pro == kPreq && !gemv_act_lds(gemv_sweeps(bits, cols))
+                ? 0
+                : (size_t)(cols + 31) / 32 * 32 + (size_t)(cols / group + 3) / 4 * 16) +
+           (pro == kNorm ? (size_t)16 * sumsq_stride(cols) * sizeof(float) : 0) + kGemvMiscFloats * sizeof(float);
+}
+
+// Byte address of element e in the pre-split INT4 activation layout.
+__device__ __forceinline__ int act_split_addr(int e) {
+    return (e & ~31) + ((e & 1) << 4) + (((e >> 3) & 3) << 2) + ((e & 7) >> 1);
 }
 
 // Geometry of one 16-byte lane chunk.
@@ -106,16 +158,20 @@ struct Chunk {
     static_assert(GB % 16 == 0 && kSweepBytes % GB == 0, "unsupported group");
 };
 
-// Activation chunks of a lane, held in registers for all rows.
-template <int BITS, int G, int NS>
+// Activation chunks of a lane, held in registers for all rows (x only when
+// the activations are not read from LDS).
+template <int BITS, int G, int NS, bool XR = true>
 struct LaneActs {
-    int x[NS][32 / BITS];     // INT8: natural order; INT4: [even dwords | odd dwords] per 8 elements
+    int x[XR ? NS : 1][32 / BITS];   // INT8: natural order; INT4: [even dwords | odd dwords] per 8 elements
     float xs[NS];                    // scale of the chunk's group
     float xt[NS];                    // bias term of the group (runq.c:137)
     int sq[NS];                      // sum(q) over the whole group
 };
 
-// Raw activation words of lane chunk (s, lane): loads only.
+// Raw activation words of lane chunk (s, lane): loads only.  Every load is
+// issued (lanes past the row read the last chunk and zero it afterwards),
+// so the number of loads in flight is known to the compiler and waiting
+// for these never waits for the weight loads issued after them.
 template <int BITS, int G, int NS>
 __device__ __forceinline__ void load_lane_raw(int (&raw)[NS][32 / BITS], float (&sc)[NS], const int8_t* xq,
                                               const float* xs, int cols, int lane) {
@@ -123,16 +179,19 @@ __device__ __forceinline__ void load_lane_raw(int (&raw)[NS][32 / BITS], float (
 #pragma unroll
     for (int s = 0; s < NS; s++) {
         const int e0 = (s * kSweepBytes + 16 * lane) * 8 / BITS;   // first element of the chunk
-        if (e0 < cols) {
-            const uint4* p = reinterpret_cast<const uint4*>(xq + e0);
+        const int ec = min(e0, cols - C::EL);
+        const uint4* p = reinterpret_cast<const uint4*>(xq + ec);
 #pragma unroll
-            for (int v = 0; v < C::AD / 4; v++) {
-                const uint4 u = p[v];
-                raw[s][4 * v + 0] = (int)u.x; raw[s][4 * v + 1] = (int)u.y;
-                raw[s][4 * v + 2] = (int)u.z; raw[s][4 * v + 3] = (int)u.w;
-            }
-            sc[s] = xs[e0 / G];
-        } else {
+        for (int v = 0; v < C::AD / 4; v++) {
+            const uint4 u = p[v];
+            raw[s][4 * v + 0] = (int)u.x; raw[s][4 * v + 1] = (int)u.y;
+            raw[s][4 * v + 2] = (int)u.z; raw[s][4 * v + 3] = (int)u.w;
+        }
+        sc[s] = xs[ec / G];
+    }
+#pragma unroll
+    for (int s = 0; s < NS; s++) {
+        if ((s * kSweepBytes + 16 * lane) * 8 / BITS >= cols) {
 #pragma unroll
             for (int k = 0; k < C::AD; k++) raw[s][k] = 0;
             sc[s] = 0.0f;
@@ -143,14 +202,12 @@ __device__ __forceinline__ void load_lane_raw(int (&raw)[NS][32 / BITS], float (
 // Sum over the P lanes of a group (P = 1, 2, 4): exact integer adds.
 template <int P>
 __device__ __forceinline__ int group_lanes_isum(int v) {
-    if (P >= 2) v += __shfl_xor(v, 1, L2Q_WAVE);
-    if (P >= 4) v += __shfl_xor(v, 2, L2Q_WAVE);
-    return v;
+    return group_isum<P>(v);
 }
 
 // sum(q) over the group, the bias term and (INT4) the even/odd byte split.
 template <int BITS, int G, int NS>
-__device__ __forceinline__ void finish_lane_acts(LaneActs<BITS, G, NS>& A, const int (&raw)[NS][32 / BITS],
+__device__ __forceinline__ void finish_lane_acts(LaneActs<BITS, G, NS, true>& A, const int (&raw)[NS][32 / BITS],
                                                  const float (&sc)[NS]) {
     using C = Chunk<BITS, G>;
 #pragma unroll
@@ -175,20 +232,63 @@ __device__ __forceinline__ void finish_lane_acts(LaneActs<BITS, G, NS>& A, const
     }
 }
 
-// Partial int32 dot of one 16-byte weight chunk (x16 for INT4).
-template <int BITS, int G, int NS>
-__device__ __forceinline__ int chunk_dot(const uint4 w, const LaneActs<BITS, G, NS>& A, int s) {
-    using C = Chunk<BITS, G>;
+// Partial int32 dot of one 16-byte weight chunk against the lane's
+// activation dwords x (x16 for INT4).
+template <int BITS>
+__device__ __forceinline__ int chunk_dot_x(const uint4 w, const int* x) {
     if (BITS == 8) {
-        int d = dot4((int)w.x, A.x[s][0], 0);
-        d = dot4((int)w.y, A.x[s][1], d);
-        d = dot4((int)w.z, A.x[s][2], d);
-        return dot4((int)w.w, A.x[s][3], d);
+        int d = dot4((int)w.x, x[0], 0);
+        d = dot4((int)w.y, x[1], d);
+        d = dot4((int)w.z, x[2], d);
+        return dot4((int)w.w, x[3], d);
     } else {
-        int d = dot8_q4_x16(w.x, A.x[s][0], A.x[s][C::AD / 2 + 0], 0);
-        d = dot8_q4_x16(w.y, A.x[s][1], A.x[s][C::AD / 2 + 1], d);
-        d = dot8_q4_x16(w.z, A.x[s][2], A.x[s][C::AD / 2 + 2], d);
-        return dot8_q4_x16(w.w, A.x[s][3], A.x[s][C::AD / 2 + 3], d);
+        int d = dot8_q4_x16(w.x, x[0], x[4], 0);
+        d = dot8_q4_x16(w.y, x[1], x[5], d);
+        d = dot8_q4_x16(w.z, x[2], x[6], d);
+        return dot8_q4_x16(w.w, x[3], x[7], d);
+    }
+}
+
+template <int BITS, int G, int NS>
+__device__ __forceinline__ int chunk_dot(const uint4 w, const LaneActs<BITS, G, NS, true>& A, int s) {
+    return chunk_dot_x<BITS>(w, A.x[s]);
+}
+
+// The lane's activation dwords of the chunk starting at element e0, from
+// the LDS copy (INT8 natural order, INT4 pre-split): 16 or 32 bytes.
+template <int BITS>
+__device__ __forceinline__ void lds_chunk(const int8_t* act, int e0, int (&x)[32 / BITS]) {
+    const int4* p = reinterpret_cast<const int4*>(act + e0);
+    const int4 v = p[0];
+    x[0] = v.x; x[1] = v.y; x[2] = v.z; x[3] = v.w;
+    if (BITS == 4) {
+        const int4 u = p[1];
+        x[4] = u.x; x[5] = u.y; x[6] = u.z; x[7] = u.w;
+    }
+}
+
+// Per-sweep scale, bias term and group sum of q for a lane whose
+// activations stay in LDS.
+template <int BITS, int G, int NS>
+__device__ __forceinline__ void lane_scalars_lds(LaneActs<BITS, G, NS, false>& A, const int8_t* act,
+                                                 const float* act_s, int cols, int lane) {
+    using C = Chunk<BITS, G>;
+#pragma unroll
+    for (int s = 0; s < NS; s++) {
+        const int e0 = (s * kSweepBytes + 16 * lane) * 8 / BITS;
+        int q = 0;
+        float sc = 0.0f;
+        if (e0 < cols) {
+            int x[32 / BITS];
+            lds_chunk<BITS>(act, e0, x);
+#pragma unroll
+            for (int k = 0; k < C::AD; k++) q = dot4(x[k], 0x01010101, q);
+            sc = act_s[e0 / G];
+        }
+        q = group_lanes_isum<C::P>(q);
+        A.sq[s] = q;
+        A.xs[s] = sc;
+        A.xt[s] = q8_bias_term(sc, q);
     }
 }
 
@@ -196,21 +296,40 @@ __device__ __forceinline__ int chunk_dot(const uint4 w, const LaneActs<BITS, G, 
 // lanes 0..15 of the calling wave each run one of its 16 FMA accumulators
 // (j = l, l+16, ...), then the _mm512_reduce_add_ps tree, then the tail as
 // GCC compiles the scalar loop (a block of 8 unfused, then FMAs).  The
-// result is valid in lane 0.  v is in LDS; all 64 lanes must call.
+// result is valid in lane 0.  v is in LDS; all 64 lanes must call.  The
+// next block's 16 reads are issued before the current block's FMAs, so
+// the chain waits on LDS only once.
 __device__ __forceinline__ float runq_sumsq(const float* v, int n, int lane) {
 #pragma clang fp contract(off)
     float acc = 0.0f;
     if (lane < 16) {
         const int nfull = n & ~15;
-        int j = 0;
-        for (; j + 16 * 16 <= nfull; j += 16 * 16) {
-            float a[16];
+        const int nblk = nfull / 256;
+        float a[16], b[16];
+        auto rd = [&](float (&dst)[16], int blk) {
+            const int j = (blk < nblk ? blk : nblk - 1) * 256;
 #pragma unroll
-            for (int u = 0; u < 16; u++) a[u] = v[j + 16 * u + lane];
+            for (int u = 0; u < 16; u++) dst[u] = v[j + 16 * u + lane];
+        };
+        auto chain = [&](const float (&src)[16]) {
 #pragma unroll
-            for (int u = 0; u < 16; u++) acc = __builtin_fmaf(a[u], a[u], acc);
+            for (int u = 0; u < 16; u++) acc = __builtin_fmaf(src[u], src[u], acc);
+        };
+        if (nblk > 0) {
+            rd(a, 0);
+            for (int blk = 0; blk < nblk; blk += 2) {
+                rd(b, blk + 1);                     // in flight during a's chain
+                __builtin_amdgcn_sched_barrier(0);
+                chain(a);
+                __builtin_amdgcn_sched_barrier(0);
+                if (blk + 1 >= nblk) break;
+                rd(a, blk + 2);
+                __builtin_amdgcn_sched_barrier(0);
+                chain(b);
+                __builtin_amdgcn_sched_barrier(0);
+            }
         }
-        for (; j < nfull; j += 16) {
+        for (int j = nblk * 256; j < nfull; j += 16) {
             const float e = v[j + lane];
             acc = __builtin_fmaf(e, e, acc);
         }
@@ -228,12 +347,63 @@ __device__ __forceinline__ float runq_sumsq(const float* v, int n, int lane) {
     return s;
 }
 
+// runq_sumsq over the transposed copy vt (row l = accumulator l's elements
+// in order, see sumsq_stride): the same operations in the same order, each
+// lane reading its own chain with float4 loads issued a block ahead.
+__device__ __forceinline__ float runq_sumsq_t(const float* vt, int n, int stride, int lane) {
+#pragma clang fp contract(off)
+    float acc = 0.0f;
+    if (lane < 16) {
+        const int steps = (n & ~15) / 16;             // chain length
+        const float4* p = reinterpret_cast<const float4*>(vt + lane * stride);
+        const int nblk = steps / 32;                  // blocks of 8 float4
+        float4 a[8], b[8];
+        auto rd = [&](float4 (&d)[8], int blk) {
+            const int q = (blk < nblk ? blk : nblk - 1) * 8;
+#pragma unroll
+            for (int u = 0; u < 8; u++) d[u] = p[q + u];
+        };
+        auto chain = [&](const float4 (&v)[8]) {
+#pragma unroll
+            for (int u = 0; u < 8; u++) {
+                acc = __builtin_fmaf(v[u].x, v[u].x, acc);
+                acc = __builtin_fmaf(v[u].y, v[u].y, acc);
+                acc = __builtin_fmaf(v[u].z, v[u].z, acc);
+                acc = __builtin_fmaf(v[u].w, v[u].w, acc);
+            }
+        };
+        if (nblk > 0) {
+            rd(a, 0);
+            for (int blk = 0; blk < nblk; blk += 2) {
+                rd(b, blk + 1);
+                chain(a);
+                if (blk + 1 >= nblk) break;
+                rd(a, blk + 2);
+                chain(b);
+            }
+        }
+        for (int k = nblk * 32; k < steps; k++) acc = __builtin_fmaf(vt[lane * stride + k], vt[lane * stride + k], acc);
+    }
+    acc = __shfl_down(acc, 8, 16) + acc;
+    acc = __shfl_down(acc, 4, 16) + acc;
+    const float p = acc + __shfl_down(acc, 2, 16);
+    float s = p + __shfl_down(p, 1, 16);
+    if (lane == 0) {
+        int j = n & ~15;
+        auto at = [&](int e) { return vt[(e & 15) * stride + (e >> 4)]; };
+        if (n - j >= 8)
+            for (int e = 0; e < 8; e++, j++) s = s + at(j) * at(j);
+        for (; j < n; j++) s = __builtin_fmaf(at(j), at(j), s);
+    }
+    return s;
+}
+
 // Workgroup prologue: quantize (for kNorm: residual add + RMSNorm first) the
 // fp32 vector into LDS act_q[cols] / act_s[nb].  Thread t handles float4
 // chunks c = t + 256*k (elements 4c..4c+3); a group is G/4 consecutive
-// threads of one wave, so group maxima are lane-group reductions.  The
+// threads of one wave, so group maxima are DPP lane-group reductions.  The
 // inputs were loaded to registers by the caller before the weight loads.
-template <int G, int PRO, int PC, int RC>
+template <int G, int PRO, int PC, int RC, bool SPLIT, int THREADS>
 __device__ __forceinline__ void prologue_compute(const GemvArgs& a, float4 (&xin)[PC], const float4 (&res)[RC],
                                                  const float4 (&nw)[RC], int8_t* act_q, float* act_s, float* vs,
                                                  float* misc, int nchunks) {
@@ -246,18 +416,23 @@ __device__ __forceinline__ void prologue_compute(const GemvArgs& a, float4 (&xin
     if constexpr (PRO == kNorm) {
 #pragma unroll
         for (int k = 0; k < kProChunks; k++) {
-            const int c = tid + kGemvThreads * k;
+            const int c = tid + THREADS * k;
             if (c < nchunks) {
                 float4 v = xin[k];
                 if (a.resid) { v.x += res[k].x; v.y += res[k].y; v.z += res[k].z; v.w += res[k].w; }
                 xin[k] = v;
-                *reinterpret_cast<float4*>(vs + 4 * c) = v;
+                const int st = sumsq_stride(n);
+                const int e = 4 * c;   // elements e..e+3: accumulators e%16.., step e/16
+                vs[((e + 0) & 15) * st + (e >> 4)] = v.x;
+                vs[((e + 1) & 15) * st + (e >> 4)] = v.y;
+                vs[((e + 2) & 15) * st + (e >> 4)] = v.z;
+                vs[((e + 3) & 15) * st + (e >> 4)] = v.w;
                 if (a.x_out && blockIdx.x == 0) *reinterpret_cast<float4*>(a.x_out + 4 * c) = v;
             }
         }
         __syncthreads();
         if (tid < L2Q_WAVE) {
-            const float ss = runq_sumsq(vs, n, lane);
+            const float ss = runq_sumsq_t(vs, n, sumsq_stride(n), lane);
             if (lane == 0) misc[0] = 1.0f / sqrtf(ss / (float)n + 1e-5f);
         }
         __syncthreads();
@@ -265,8 +440,8 @@ __device__ __forceinline__ void prologue_compute(const GemvArgs& a, float4 (&xin
     }
 #pragma unroll
     for (int k = 0; k < kProChunks; k++) {
-        if (kGemvThreads * k >= nchunks) break;   // uniform across the workgroup
-        const int c = tid + kGemvThreads * k;
+        if (THREADS * k >= nchunks) break;   // uniform across the workgroup
+        const int c = tid + THREADS * k;
         const bool in = c < nchunks;
         float4 o = xin[k];
         if constexpr (PRO == kNorm) {
@@ -277,153 +452,282 @@ __device__ __forceinline__ void prologue_compute(const GemvArgs& a, float4 (&xin
         float m = fmaxf(fmaxf(fabsf(o.x), fabsf(o.y)), fmaxf(fabsf(o.z), fabsf(o.w)));
         m = group_max<G / 4>(m);
         const float s = q8_scale(m);
+        const float r = q8_recip(s);
         if (in) {
-            const int q0 = q8_value(o.x, s), q1 = q8_value(o.y, s), q2 = q8_value(o.z, s), q3 = q8_value(o.w, s);
-            const int packed = (q0 & 0xff) | ((q1 & 0xff) << 8) | ((q2 & 0xff) << 16) | ((q3 & 0xff) << 24);
-            reinterpret_cast<int*>(act_q)[c] = packed;
+            const int q0 = q8_value_fast(o.x, s, r), q1 = q8_value_fast(o.y, s, r);
+            const int q2 = q8_value_fast(o.z, s, r), q3 = q8_value_fast(o.w, s, r);
+            if (SPLIT) {   // INT4 pre-split layout: (q0, q2) to E, (q1, q3) to O
+                *reinterpret_cast<uint16_t*>(act_q + act_split_addr(4 * c)) = (uint16_t)((q0 & 0xff) | ((q2 & 0xff) << 8));
+                *reinterpret_cast<uint16_t*>(act_q + act_split_addr(4 * c + 1)) = (uint16_t)((q1 & 0xff) | ((q3 & 0xff) << 8));
+            } else {
+                const int packed = (q0 & 0xff) | ((q1 & 0xff) << 8) | ((q2 & 0xff) << 16) | ((q3 & 0xff) << 24);
+                reinterpret_cast<int*>(act_q)[c] = packed;
+            }
             if ((c % (G / 4)) == 0) act_s[c / (G / 4)] = s;
         }
     }
     __syncthreads();
 }
 
-// Persistent over row tiles: workgroup b handles tiles b, b + gridDim.x, ...
-// (4*R rows each); the prologue runs once per workgroup and the next tile's
-// weight loads are issued before the current tile's fold and epilogue.
-template <int BITS, int G, int NS, int PRO, int EPI>
-__global__ __launch_bounds__(kGemvThreads) void k_gemv(GemvArgs a) {
+// Ordered fold of one row: sum_b fma(ws_b, t_b, sum) for b = 0..nb-1, the
+// terms and scales read from LDS 16 groups ahead of the FMA chain.
+__device__ __forceinline__ float fold_row(const float* tp, const float* sp, int nb) {
+    float sum = 0.0f;
+    const float4* t4 = reinterpret_cast<const float4*>(tp);
+    const float4* s4 = reinterpret_cast<const float4*>(sp);
+    const int n4 = nb >> 2;
+    int b = 0;
+    if (n4 >= 4) {
+        float4 t[4], s[4];
+#pragma unroll
+        for (int u = 0; u < 4; u++) { t[u] = t4[u]; s[u] = s4[u]; }
+        for (; b + 8 <= n4; b += 4) {
+            float4 tn[4], sn[4];
+#pragma unroll
+            for (int u = 0; u < 4; u++) { tn[u] = t4[b + 4 + u]; sn[u] = s4[b + 4 + u]; }
+#pragma unroll
+            for (int u = 0; u < 4; u++) {
+                sum = __builtin_fmaf(s[u].x, t[u].x, sum);
+                sum = __builtin_fmaf(s[u].y, t[u].y, sum);
+                sum = __builtin_fmaf(s[u].z, t[u].z, sum);
+                sum = __builtin_fmaf(s[u].w, t[u].w, sum);
+            }
+#pragma unroll
+            for (int u = 0; u < 4; u++) { t[u] = tn[u]; s[u] = sn[u]; }
+        }
+#pragma unroll
+        for (int u = 0; u < 4; u++) {
+            sum = __builtin_fmaf(s[u].x, t[u].x, sum);
+            sum = __builtin_fmaf(s[u].y, t[u].y, sum);
+            sum = __builtin_fmaf(s[u].z, t[u].z, sum);
+            sum = __builtin_fmaf(s[u].w, t[u].w, sum);
+        }
+        b += 4;
+    }
+    for (; b < n4; b++) {
+        const float4 t = t4[b], s = s4[b];
+        sum = __builtin_fmaf(s.x, t.x, sum);
+        sum = __builtin_fmaf(s.y, t.y, sum);
+        sum = __builtin_fmaf(s.z, t.z, sum);
+        sum = __builtin_fmaf(s.w, t.w, sum);
+    }
+    for (int g = n4 * 4; g < nb; g++) sum = __builtin_fmaf(sp[g], tp[g], sum);
+    return sum;
+}
+
+__device__ __forceinline__ void wave_lds_sync() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+// Persistent over units of PR rows: wave w of the grid owns units
+// [U*w/W, U*(w+1)/W) (U units, W waves).  The wave's first unit is loaded
+// before the prologue (which runs once per workgroup while it streams in);
+// unit u+1 is loaded as soon as unit u has been consumed.  Terms of F rows
+// (F/PR units) are collected before one ordered fold on F lanes.  A wave
+// without units loads row 0 (never used), so every path issues the same
+// loads and no wait covers younger loads than it must.
+template <int BITS, int G, int NS, int PRO, int EPI, int PR>
+__global__ __launch_bounds__(gemv_waves(NS) * L2Q_WAVE) void k_gemv(GemvArgs a) {
+    constexpr int WAVES = gemv_waves(NS);
+    constexpr int THREADS = WAVES * L2Q_WAVE;
+    static_assert(PR == 2, "fold batches hold whole units of two rows");
     using C = Chunk<BITS, G>;
-    constexpr int R = gemv_rows_per_wave(NS);
-    constexpr int RB = gemv_rows_per_block(NS);
+    constexpr int NSS = gemv_scale_sweeps(BITS, G, NS);
+    constexpr bool ACTL = gemv_act_lds(NS);           // activations read from LDS per chunk
+    constexpr bool SPLIT = ACTL && BITS == 4;
+    static_assert(PR % 2 == 0 || EPI == kStore, "pair epilogues need an even unit");
+    static_assert(EPI == kStore || PRO == kNorm, "fused epilogues run after the norm prologue");
     extern __shared__ __attribute__((aligned(16))) float lds[];
     const int lane = threadIdx.x & (L2Q_WAVE - 1);
     const int wv = threadIdx.x / L2Q_WAVE;
     const int nb = a.cols / G;
-    const int stride = nb + 1;
-    const int ntiles = (a.rows + RB - 1) / RB;
-    float* ws_l = lds + (size_t)wv * R * stride * 2;
-    float* t_l = ws_l + R * stride;
-    int8_t* act_q = reinterpret_cast<int8_t*>(lds + gemv_fold_floats(nb, NS));
-    float* act_s = reinterpret_cast<float*>(act_q + a.cols);
-    float* vs = act_s + nb;
-    float* misc = vs + (PRO == kNorm ? a.cols : 0);
-    const size_t rowbytes = (size_t)a.cols * BITS / 8;
+    const int nbp = gemv_nbp(nb);
+    const int F = gemv_fold_rows(nb, WAVES);   // rows per fold batch
+    const int UB = F / PR;                     // units per fold batch
+    float* tb = lds + (size_t)wv * 2 * F * nbp;
+    float* sb = tb + F * nbp;
+    int8_t* act_q = reinterpret_cast<int8_t*>(lds + gemv_fold_floats(nb, WAVES));
+    float* act_s = reinterpret_cast<float*>(act_q + (a.cols + 31) / 32 * 32);
+    float* vs = act_s + (nb + 3) / 4 * 4;
+    float* misc = vs + (PRO == kNorm ? 16 * sumsq_stride(a.cols) : 0);
+    uint64_t* etab = reinterpret_cast<uint64_t*>(misc + 4);   // exp table (kSwiglu)
+    float* rope_l = misc + 4 + 64;                             // RoPE row of the position (kRopeKV)
+    const int rowbytes = a.cols * BITS / 8;
     const uint8_t* wbase = static_cast<const uint8_t*>(a.w);
     const bool leader = (lane % C::P) == 0;
 
+    const int nunits = (a.rows + PR - 1) / PR;
+    const int nwaves = gridDim.x * WAVES;
+    const int gw = blockIdx.x * WAVES + wv;
+    const int u0 = (int)((long long)nunits * gw / nwaves);
+    const int u1 = (int)((long long)nunits * (gw + 1) / nwaves);
+
     // 1. prologue inputs first, so that waiting for them never waits on the
     //    weight loads issued after them (vector loads complete in order)
-    constexpr int kProChunks = PRO == kPreq ? 1 : prologue_chunks(NS, BITS);
+    constexpr int kProChunks = PRO == kPreq ? 1 : prologue_chunks(NS, BITS, THREADS);
     constexpr int kResChunks = PRO == kNorm ? kProChunks : 1;
     float4 xin[kProChunks], res[kResChunks], nw[kResChunks];
     const int nchunks = a.cols / 4;
     if (PRO != kPreq) {
+        // unconditional loads (clamped chunk index; see load_lane_raw)
         const float* src = (PRO == kNorm && a.emb) ? a.emb + (size_t)a.meta[0] * a.cols : a.x_in;
+        const float* rsrc = (PRO == kNorm && a.resid) ? a.resid : src;
 #pragma unroll
         for (int k = 0; k < kProChunks; k++) {
-            const int c = threadIdx.x + kGemvThreads * k;
-            if (kGemvThreads * k < nchunks && c < nchunks) {
-                xin[k] = reinterpret_cast<const float4*>(src)[c];
-                if constexpr (PRO == kNorm) {
-                    res[k] = a.resid ? reinterpret_cast<const float4*>(a.resid)[c] : make_float4(0, 0, 0, 0);
-                    nw[k] = reinterpret_cast<const float4*>(a.norm_w)[c];
-                }
+            const int c = min((int)threadIdx.x + THREADS * k, nchunks - 1);
+            xin[k] = reinterpret_cast<const float4*>(src)[c];
+            if constexpr (PRO == kNorm) {
+                res[k] = reinterpret_cast<const float4*>(rsrc)[c];
+                nw[k] = reinterpret_cast<const float4*>(a.norm_w)[c];
             }
         }
     }
-    int raw[NS][32 / BITS];
-    float sc[NS];
-    if (PRO == kPreq) load_lane_raw<BITS, G, NS>(raw, sc, a.xq, a.xs, a.cols, lane);
+    // epilogue tables: loaded with the prologue inputs, stored to LDS by the
+    // prologue, so the epilogue never waits on a global load queued behind
+    // the weight stream
+    uint64_t etab_v = 0;
+    float rope_v = 0.0f;
+    if (EPI == kSwiglu) etab_v = kExp2Tab[threadIdx.x & 31];
+    if (EPI == kRopeKV) rope_v = a.rope[(size_t)a.meta[1] * a.hs + min((int)threadIdx.x, a.hs - 1)];
+    int raw[ACTL ? 1 : NS][32 / BITS];
+    float sc[ACTL ? 1 : NS];
+    constexpr int kCopyChunks = ACTL && PRO == kPreq ? (NS * 512 / BITS + THREADS - 1) / THREADS : 1;   // 16-byte xq chunks
+    constexpr int kXsChunks = ACTL && PRO == kPreq ? (NS * kSweepBytes * 8 / BITS / G + THREADS - 1) / THREADS : 1;
+    uint4 xcp[kCopyChunks];
+    float xsv[kXsChunks];
+    const int ncopy = a.cols / 16;
+    if (PRO == kPreq) {
+        if constexpr (!ACTL) {
+            load_lane_raw<BITS, G, NS>(raw, sc, a.xq, a.xs, a.cols, lane);
+        } else {
+#pragma unroll
+            for (int k = 0; k < kCopyChunks; k++)
+                xcp[k] = reinterpret_cast<const uint4*>(a.xq)[min((int)threadIdx.x + THREADS * k, ncopy - 1)];
+#pragma unroll
+            for (int k = 0; k < kXsChunks; k++) xsv[k] = a.xs[min((int)threadIdx.x + THREADS * k, nb - 1)];
+        }
+    }
     __builtin_amdgcn_sched_barrier(0);
 
-    // 2. weight loads of this wave's rows of a tile: chunk (r, s) is the 16
-    //    bytes at row*rowbytes + s*1024 + 16*lane; the scale is loaded by
-    //    the group's leader lane
-    uint4 w4[R][NS];
-    float wsc[R][NS];
-    auto load_tile = [&](int tile) {
-        const int row0 = tile * RB + wv * R;
+    // 2. weight loads: every load is issued unconditionally (addresses past
+    //    the row are clamped to valid ones, units past the wave's range read
+    //    row 0; neither value is used), so the in-flight count is the same on
+    //    every path and waits never cover more than they must
+    uint4 w4[PR][NS];
+    float wsv[PR][NSS];
+    auto load_unit = [&](int u) {
+        const bool real = u < u1;
 #pragma unroll
-        for (int r = 0; r < R; r++) {
-            const int row = row0 + r;
+        for (int k = 0; k < PR; k++) {
+            const int row = real ? min(u * PR + k, a.rows - 1) : 0;
+            const uint8_t* p = wbase + (size_t)row * rowbytes;
 #pragma unroll
             for (int s = 0; s < NS; s++) {
-                const int off = s * kSweepBytes + 16 * lane;
-                if (row < a.rows && off < (int)rowbytes) {
-                    w4[r][s] = load_stream(wbase + (size_t)row * rowbytes + off);
-                    wsc[r][s] = leader ? a.ws[(size_t)row * nb + off / C::GB] : 0.0f;
-                } else {
-                    w4[r][s] = make_uint4(0, 0, 0, 0);
-                    wsc[r][s] = 0.0f;
-                }
+                int off = s * kSweepBytes + 16 * lane;
+                if (s == NS - 1) off = min(off, rowbytes - 16);
+                w4[k][s] = load_stream(p + off);
             }
+            const float* q = a.ws + (size_t)row * nb;
+#pragma unroll
+            for (int ss = 0; ss < NSS; ss++) wsv[k][ss] = q[min(ss * L2Q_WAVE + lane, nb - 1)];
         }
     };
-    int tile = blockIdx.x;
-    load_tile(tile);
+    const bool has_work = u0 < u1;   // wave-uniform
+    load_unit(u0);
     __builtin_amdgcn_sched_barrier(0);
 
     // 3. prologue (workgroup-wide) while the weights stream in
+    if (EPI == kSwiglu && threadIdx.x < 32) etab[threadIdx.x] = etab_v;
+    if (EPI == kRopeKV && (int)threadIdx.x < a.hs) rope_l[threadIdx.x] = rope_v;
     if (PRO != kPreq) {
-        prologue_compute<G, PRO, kProChunks, kResChunks>(a, xin, res, nw, act_q, act_s, vs, misc, nchunks);
-        load_lane_raw<BITS, G, NS>(raw, sc, act_q, act_s, a.cols, lane);
-    }
-    LaneActs<BITS, G, NS> A;
-    finish_lane_acts<BITS, G, NS>(A, raw, sc);
-
-    for (; tile < ntiles; tile += gridDim.x) {
-        const int row0 = tile * RB + wv * R;
-        const bool active = row0 < a.rows;   // wave-uniform
-        // 4. dots and per-group terms of this tile
-        if (active) {
+        prologue_compute<G, PRO, kProChunks, kResChunks, SPLIT, THREADS>(a, xin, res, nw, act_q, act_s, vs, misc, nchunks);
+        if constexpr (!ACTL) load_lane_raw<BITS, G, NS>(raw, sc, act_q, act_s, a.cols, lane);
+    } else if constexpr (ACTL) {
+        // copy xq (and xs) into LDS, INT4 in the pre-split layout
 #pragma unroll
-            for (int r = 0; r < R; r++) {
-                const int row = row0 + r;
-#pragma unroll
-                for (int s = 0; s < NS; s++) {
-                    const int off = s * kSweepBytes + 16 * lane;
-                    int d = group_lanes_isum<C::P>(chunk_dot<BITS, G, NS>(w4[r][s], A, s));
-                    if (BITS == 4) d >>= 4;   // exact: the x16 dot is a multiple of 16
-                    if (leader && off < (int)rowbytes) {
-                        const int g = off / C::GB;
-                        if (a.dots && row < a.rows) a.dots[(size_t)row * nb + g] = d;
-                        ws_l[r * stride + g] = wsc[r][s];
-                        t_l[r * stride + g] = group_term(A.xs[s], A.xt[s], d, A.sq[s]);
-                    }
+        for (int k = 0; k < kCopyChunks; k++) {
+            const int c = threadIdx.x + THREADS * k;
+            if (c < ncopy) {
+                const uint4 v = xcp[k];
+                if (SPLIT) {
+                    const int e0 = 16 * c;
+                    uint2 ev, od;
+                    ev.x = (unsigned)even_bytes((int)v.x, (int)v.y); ev.y = (unsigned)even_bytes((int)v.z, (int)v.w);
+                    od.x = (unsigned)odd_bytes((int)v.x, (int)v.y); od.y = (unsigned)odd_bytes((int)v.z, (int)v.w);
+                    *reinterpret_cast<uint2*>(act_q + act_split_addr(e0)) = ev;
+                    *reinterpret_cast<uint2*>(act_q + act_split_addr(e0 + 1)) = od;
+                } else {
+                    reinterpret_cast<uint4*>(act_q)[c] = v;
                 }
             }
         }
-        // the next tile's weights stream in during this tile's fold
-        if (tile + (int)gridDim.x < ntiles) load_tile(tile + gridDim.x);
-        if (!active) continue;
-        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-        __builtin_amdgcn_wave_barrier();
-        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-
-        // 5. ordered fold: lane r folds row row0 + r
-        float sum = 0.0f;
-        if (lane < R) {
-            const float* wp = ws_l + lane * stride;
-            const float* tp = t_l + lane * stride;
-            for (int b = 0; b < nb; b++) sum = __builtin_fmaf(wp[b], tp[b], sum);
+#pragma unroll
+        for (int k = 0; k < kXsChunks; k++) {
+            const int i = threadIdx.x + THREADS * k;
+            if (i < nb) act_s[i] = xsv[k];
         }
+        __syncthreads();
+    }
+    if (!has_work) return;
+    LaneActs<BITS, G, NS, !ACTL> A;
+    if constexpr (ACTL) lane_scalars_lds<BITS, G, NS>(A, act_q, act_s, a.cols, lane);
+    else finish_lane_acts<BITS, G, NS>(A, raw, sc);
 
-        // 6. epilogue on lanes 0..R-1 (R is even: pairs stay in one wave)
+    // dots and per-group terms of row k of unit u into fold-batch row br
+    auto consume_row = [&](int k, int u) {
+        const int row = u * PR + k;
+        const int br = ((u - u0) % UB) * PR + k;
+#pragma unroll
+        for (int s = 0; s < NS; s++) {
+            const int off = s * kSweepBytes + 16 * lane;
+            int dp;
+            if constexpr (ACTL) {
+                // lanes past the row read a valid chunk; their dots are never used
+                int x[32 / BITS];
+                lds_chunk<BITS>(act_q, min(off * 8 / BITS, a.cols - C::EL), x);
+                dp = chunk_dot_x<BITS>(w4[k][s], x);
+            } else {
+                dp = chunk_dot<BITS, G, NS>(w4[k][s], A, s);
+            }
+            int d = group_lanes_isum<C::P>(dp);
+            if (BITS == 4) d >>= 4;   // exact: the x16 dot is a multiple of 16
+            if (leader && off < rowbytes) {
+                const int g = off / C::GB;
+                if (a.dots && row < a.rows) a.dots[(size_t)row * nb + g] = d;
+                tb[br * nbp + g] = group_term(A.xs[s], A.xt[s], d, A.sq[s]);
+            }
+        }
+#pragma unroll
+        for (int ss = 0; ss < NSS; ss++) {
+            const int g = ss * L2Q_WAVE + lane;
+            if (g < nb) sb[br * nbp + g] = wsv[k][ss];
+        }
+    };
+
+    // ordered fold of a batch of nrows rows (first row row0) on lanes
+    // 0..nrows-1, then the epilogue
+    auto fold_batch = [&](int row0, int nrows) {
+        wave_lds_sync();
+        float sum = 0.0f;
+        if (lane < nrows) sum = fold_row(tb + lane * nbp, sb + lane * nbp, nb);
+        const bool mine = lane < nrows;
         const int row = row0 + lane;
         if (EPI == kStore) {
-            if (lane < R && row < a.rows) a.out[row] = sum;
+            if (mine && row < a.rows) a.out[row] = sum;
         } else if (EPI == kRopeKV) {
-            // rows come in (even, odd) pairs held by lanes (0,1), (2,3)
-            const float other = __shfl_xor(sum, 1, L2Q_WAVE);
-            if (lane < R && row < a.rows) {
+            // rows come in (even, odd) pairs held by lanes (0,1), (2,3), ...
+            const float other = dpp_f<kDppXor1>(sum);
+            if (mine && row < a.rows) {
                 const int pos = a.meta[1];
                 const bool odd = row & 1;
                 const float v0 = odd ? other : sum, v1 = odd ? sum : other;
                 if (row < a.dim + a.kv_dim) {            // q or k: rotate
                     const int e = row < a.dim ? row : row - a.dim;
                     const int hd = (e & ~1) % a.hs;
-                    const float c = a.rope[(size_t)pos * a.hs + hd];
-                    const float s = a.rope[(size_t)pos * a.hs + hd + 1];
+                    const float c = rope_l[hd];
+                    const float s = rope_l[hd + 1];
                     const float r = odd ? __builtin_fmaf(v0, s, v1 * c) : __builtin_fmaf(v0, c, -(v1 * s));
                     if (row < a.dim) a.out[row] = r;
                     else a.kcache[((size_t)(e / a.hs) * a.max_t + pos) * a.hs + (e % a.hs)] = r;
@@ -432,21 +736,33 @@ __global__ __launch_bounds__(kGemvThreads) void k_gemv(GemvArgs a) {
                     a.vcache[((size_t)(e / a.hs) * a.max_t + pos) * a.hs + (e % a.hs)] = sum;
                 }
             }
-        } else {   // kSwiglu: (w1, w3) pairs on lanes (0,1), (2,3)
-            const float h3 = __shfl_xor(sum, 1, L2Q_WAVE);
-            if (lane < R && (lane & 1) == 0 && row < a.rows) {
+        } else {   // kSwiglu: (w1, w3) pairs on lanes (0,1), (2,3), ...
+            const float h3 = dpp_f<kDppXor1>(sum);
+            if (mine && (lane & 1) == 0 && row < a.rows) {
 #pragma clang fp contract(off)
                 float h = sum;
-                h *= (1.0f / (1.0f + exp_runq(-h)));
+                h *= (1.0f / (1.0f + exp_runq_t(-h, etab)));
                 a.out[row >> 1] = h * h3;
             }
         }
-        // the LDS fold area is reused by the next tile: keep the next
-        // tile's term writes behind this tile's fold reads
-        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-        __builtin_amdgcn_wave_barrier();
-        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        // the fold area is reused by the next unit: keep its term writes
+        // behind this unit's fold reads
+        wave_lds_sync();
+    };
+
+    for (int u = u0; u + 1 < u1; u++) {
+#pragma unroll
+        for (int k = 0; k < PR; k++) consume_row(k, u);
+        // the unit's registers are free again: the next unit streams in
+        __builtin_amdgcn_sched_barrier(0);
+        load_unit(u + 1);
+        __builtin_amdgcn_sched_barrier(0);
+        if ((u - u0 + 1) % UB == 0) fold_batch((u + 1 - UB) * PR, F);
     }
+#pragma unroll
+    for (int k = 0; k < PR; k++) consume_row(k, u1 - 1);
+    const int last = (u1 - u0 - 1) % UB + 1;   // units in the last batch
+    fold_batch((u1 - last) * PR, last * PR);
 }
 
 }  // namespace l2q

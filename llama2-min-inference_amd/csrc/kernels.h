@@ -25,7 +25,7 @@ __global__ __launch_bounds__(256) void k_quantize(const float* __restrict__ x, i
     const float v = in ? x[i] : 0.0f;
     const float s = q8_scale(group_max<G>(fabsf(v)));
     if (in) {
-        xq[i] = (int8_t)q8_value(v, s);
+        xq[i] = (int8_t)q8_value_fast(v, s, q8_recip(s));
         if ((i % G) == 0) xs[i / G] = s;
     }
 }
@@ -80,7 +80,7 @@ __global__ __launch_bounds__(kNormThreads) void k_rmsnorm_quant(
         const float s = q8_scale(group_max<G>(fabsf(o)));
         if (in) {
             if (xout) xout[i] = v[k];
-            xq[i] = (int8_t)q8_value(o, s);
+            xq[i] = (int8_t)q8_value_fast(o, s, q8_recip(s));
             if ((i % G) == 0) xs[i / G] = s;
         }
     }
@@ -103,7 +103,7 @@ __global__ __launch_bounds__(256) void k_swiglu_quant(const float* __restrict__ 
     }
     const float s = q8_scale(group_max<G>(fabsf(g)));
     if (in) {
-        xq[i] = (int8_t)q8_value(g, s);
+        xq[i] = (int8_t)q8_value_fast(g, s, q8_recip(s));
         if ((i % G) == 0) xs[i / G] = s;
         if (gout) gout[i] = g;
     }

@@ -42,9 +42,9 @@ bool gemv_shape_ok(int bits, int group, int rows, int cols) {
     return gemv_sweeps(bits, cols) <= kMaxNS;
 }
 
-// Workgroups of a persistent GEMV launch: as many tiles per workgroup as
-// it takes to fit every workgroup on the device at once, spread evenly.
-static int resident_blocks(const void* fn, size_t lds) {
+// Workgroups of a persistent GEMV launch: the resident workgroups per CU
+// (occupancy), at most `cap` per CU, times the CU count.
+static int resident_blocks(const void* fn, int threads, size_t lds, int cap) {
     struct Entry { const void* fn; size_t lds; int dev; int blocks; };
     static thread_local Entry cache[64];
     static thread_local int used = 0;
@@ -53,23 +53,37 @@ static int resident_blocks(const void* fn, size_t lds) {
     for (int i = 0; i < used; i++)
         if (cache[i].fn == fn && cache[i].lds == lds && cache[i].dev == dev) return cache[i].blocks;
     int per_cu = 0, cus = 0;
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fn, kGemvThreads, lds) != hipSuccess || per_cu < 1) per_cu = 1;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fn, threads, lds) != hipSuccess || per_cu < 1) per_cu = 1;
     if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus < 1) cus = 1;
     (void)hipGetLastError();
-    const int blocks = per_cu * cus;
+    const int blocks = (per_cu < cap ? per_cu : cap) * cus;
     if (used < 64) cache[used++] = Entry{fn, lds, dev, blocks};
     return blocks;
 }
 
+// One workgroup per CU (see gemv_waves).
+constexpr int kGemvBlocksPerCu = 1;
+constexpr size_t kGemvMaxLds = 160 * 1024;   // gfx950 LDS per workgroup
+
 template <int BITS, int G, int NS, int PRO, int EPI>
 static int go_gemv(const GemvArgs& a, hipStream_t st) {
-    constexpr int RB = gemv_rows_per_block(NS);
-    const int ntiles = (a.rows + RB - 1) / RB;
-    const size_t lds = gemv_lds_bytes(PRO, a.cols, G, BITS);
-    const int maxb = resident_blocks(reinterpret_cast<const void*>(&k_gemv<BITS, G, NS, PRO, EPI>), lds);
-    const int per = (ntiles + maxb - 1) / maxb;
-    const int blocks = (ntiles + per - 1) / per;
-    hipLaunchKernelGGL((k_gemv<BITS, G, NS, PRO, EPI>), dim3(blocks), dim3(kGemvThreads), lds, st, a);
+    constexpr int PR = kGemvUnit;
+    const size_t lds = gemv_lds_bytes(PRO, a.cols, G, BITS, PR);
+    constexpr int W = gemv_waves(NS);
+    const void* fn = reinterpret_cast<const void*>(&k_gemv<BITS, G, NS, PRO, EPI, PR>);
+    if (lds > 65536) {   // above the default dynamic-LDS limit: raise it once per kernel
+        static int raised = 0;
+        if (raised < (int)lds) {
+            hipError_t e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+            if (e != hipSuccess) return hip_fail(e, "gemv: raising the LDS limit");
+            raised = (int)lds;
+        }
+    }
+    const int maxb = resident_blocks(fn, W * L2Q_WAVE, lds, kGemvBlocksPerCu);
+    const int nunits = (a.rows + PR - 1) / PR;
+    int blocks = (nunits + W - 1) / W;
+    if (blocks > maxb) blocks = maxb;
+    hipLaunchKernelGGL((k_gemv<BITS, G, NS, PRO, EPI, PR>), dim3(blocks), dim3(W * L2Q_WAVE), lds, st, a);
     return check_launch("gemv");
 }
 
@@ -116,7 +130,10 @@ int launch_gemv_fused(int bits, int group, int pro, int epi, const GemvArgs& a, 
     }
     if (pro != kPreq && !a.x_in && !(pro == kNorm && a.emb)) { set_error("gemv: null prologue input"); return L2Q_ERR_ARG; }
     if (pro == kNorm && (!a.norm_w || (a.emb && !a.meta))) { set_error("gemv: null norm weight / meta"); return L2Q_ERR_ARG; }
-    if (gemv_lds_bytes(pro, a.cols, group, bits) > 65536) { set_error("gemv: cols=%d needs too much LDS", a.cols); return L2Q_ERR_ARG; }
+    if (gemv_lds_bytes(pro, a.cols, group, bits, kGemvUnit) > kGemvMaxLds) {
+        set_error("gemv: cols=%d needs too much LDS", a.cols);
+        return L2Q_ERR_ARG;
+    }
     if (pro == kNorm && gemv_sweeps(bits, a.cols) > 4) {
         set_error("gemv: the norm prologue supports rows of at most 4 KiB");
         return L2Q_ERR_ARG;

@@ -102,6 +102,38 @@ def test_quantize_act_bit_exact(gpu_lib, torch_cuda, group, n):
     np.testing.assert_array_equal(xs.cpu().numpy(), xs_ref)
 
 
+def near_tie_inputs(n, group, seed):
+    """Inputs within a few ulps of (k + 1/2) * s for the group's own scale s:
+    the cases where the division-free quantizer must fall back to x / s."""
+    rng = np.random.default_rng(seed)
+    ng = n // group
+    amax = (np.abs(rng.standard_normal(ng)) * 10.0 ** rng.integers(-4, 3, ng)).astype(np.float32) + np.float32(1e-3)
+    s = (amax / np.float32(127)).astype(np.float32)
+    k = rng.integers(-127, 127, n).astype(np.float32) + np.float32(0.5)
+    x = (k * np.repeat(s, group)).astype(np.float32)
+    for _ in range(3):
+        step = rng.integers(-1, 2, n)
+        x = np.where(step > 0, np.nextafter(x, np.float32(np.inf)),
+                     np.where(step < 0, np.nextafter(x, np.float32(-np.inf)), x)).astype(np.float32)
+    x = np.clip(x, -np.repeat(amax, group), np.repeat(amax, group)).astype(np.float32)
+    x[::group] = amax * np.where(rng.random(ng) < 0.5, 1, -1).astype(np.float32)   # pins each group's amax
+    return x
+
+
+@pytest.mark.parametrize("group", [32, 64])
+def test_quantize_act_near_ties(gpu_lib, torch_cuda, group):
+    n = 1 << 16
+    x = near_tie_inputs(n, group, 3)
+    xq_ref, xs_ref, _ = O.quantize_act(x, group)
+    d_x = dev(torch_cuda, x)
+    xq = torch_cuda.empty(n, dtype=torch_cuda.int8, device="cuda")
+    xs = torch_cuda.empty(n // group, dtype=torch_cuda.float32, device="cuda")
+    abi.call("l2q_quantize_act", d_x.data_ptr(), n, group, xq.data_ptr(), xs.data_ptr(), stream(torch_cuda))
+    torch_cuda.cuda.synchronize()
+    np.testing.assert_array_equal(xs.cpu().numpy(), xs_ref)
+    np.testing.assert_array_equal(xq.cpu().numpy(), xq_ref)
+
+
 @pytest.mark.parametrize("group", [32, 64])
 @pytest.mark.parametrize("n", [288, 768, 4096, 4128])
 def test_rmsnorm_quant(gpu_lib, torch_cuda, group, n):

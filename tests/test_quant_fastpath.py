@@ -1,0 +1,44 @@
+"""The GPU quantizer's division-free path (device.h q8_value_fast), restated
+in numpy float32 on the CPU: y = x * rcp(s), q = rint(y), and the correctly
+rounded x / s wherever |y - q| >= 0.5 - |y| * 2^-20.  It must equal the
+reference's rint(x / s) (runq.c:117-139) on every input, including inputs
+a few ulps from the rounding boundaries (k + 1/2) * s, with rcp modelled as
+1 ulp off in either direction.  The GPU kernel itself is checked against the
+oracle in tests/test_gpu_ops.py."""
+import numpy as np
+
+F = np.float32
+
+
+def fast_quantize(x, s, r):
+    y = (x * r).astype(F)
+    q = np.rint(y).astype(F)
+    thr = (F(0.5) - np.abs(y).astype(np.float64) * 2.0 ** -20).astype(F)   # one rounding, as the fma
+    slow = ~(np.abs((y - q).astype(F)) < thr)
+    return np.where(slow, np.rint((x / s).astype(F)), q), slow
+
+
+def test_fast_quantizer_equals_division():
+    rng = np.random.default_rng(0)
+    n, g = 1 << 20, 64
+    amax = (np.abs(rng.standard_normal(n // g)) * 10.0 ** rng.integers(-6, 6, n // g)).astype(F)
+    s = np.where(amax == 0, F(1e-8), (amax / F(127)).astype(F)).astype(F)
+    S, A = np.repeat(s, g), np.repeat(amax, g)
+    x = (rng.uniform(-1, 1, n).astype(F) * A).astype(F)
+    k = rng.integers(-127, 127, n).astype(F) + F(0.5)
+    near = (k * S).astype(F)
+    for _ in range(3):
+        step = rng.integers(-1, 2, n)
+        near = np.where(step > 0, np.nextafter(near, F(np.inf)),
+                        np.where(step < 0, np.nextafter(near, F(-np.inf)), near)).astype(F)
+    pick = (rng.random(n) < 0.5) & (np.abs(near) <= A)
+    x = np.where(pick, near, x).astype(F)
+    exact = np.rint((x / S).astype(F))
+    r0 = (F(1) / S).astype(F)
+    for dirn in (-1, 0, 1):
+        r = r0 if dirn == 0 else np.nextafter(r0, F(np.inf) if dirn > 0 else F(-np.inf)).astype(F)
+        q, slow = fast_quantize(x, S, r)
+        np.testing.assert_array_equal(q, exact)
+        assert slow[pick].mean() > 0.5          # the guard does fire near the boundaries
+        assert slow[~pick].mean() < 1e-3        # and almost never elsewhere
+    assert np.abs(exact).max() <= 127           # the clamp of the reference never binds
