@@ -111,15 +111,15 @@ __device__ __forceinline__ int q8_value(float x, float s) {
 // equals rint(fl(x/s)) unless y lies within that distance of a half-integer
 // (the only places where the two can round differently), i.e. unless
 // |y - rint(y)| >= 0.5 - margin; there, and for non-finite y (s denormal or
-// tiny), the correctly rounded division is taken.  The margin used,
-// |y|*2^-20, is four times the error bound.  No clamp is needed: s is
-// amax/127 rounded, so |x/s| < 127.5 for every x of the group.
+// tiny), the correctly rounded division is taken.  No clamp is needed: s is
+// amax/127 rounded, so |x/s| < 127.5 for every x of the group, and |y| < 128
+// makes 4 ulp(y) <= 2^-15; the margin used, 2^-13, is four times that.
 __device__ __forceinline__ float q8_recip(float s) { return __builtin_amdgcn_rcpf(s); }
 
 __device__ __forceinline__ int q8_value_fast(float x, float s, float r) {
     const float y = x * r;
     float q = rintf(y);
-    if (__builtin_expect(!(fabsf(y - q) < __builtin_fmaf(-fabsf(y), 0x1p-20f, 0.5f)), 0)) q = rintf(x / s);
+    if (__builtin_expect(!(fabsf(y - q) < 0.5f - 0x1p-13f), 0)) q = rintf(x / s);
     return (int)q;
 }
 

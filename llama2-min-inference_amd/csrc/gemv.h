@@ -539,6 +539,11 @@ __global__ __launch_bounds__(gemv_waves(NS) * L2Q_WAVE) void k_gemv(GemvArgs a) 
     constexpr bool SPLIT = ACTL && BITS == 4;
     static_assert(PR % 2 == 0 || EPI == kStore, "pair epilogues need an even unit");
     static_assert(EPI == kStore || PRO == kNorm, "fused epilogues run after the norm prologue");
+    // Read every kernel argument into SGPRs here, before any of them is used:
+    // the scalar loads then share one round trip to the argument buffer
+    // instead of costing one each at their first uses.
+    asm volatile("" ::"s"(a.rows), "s"(a.cols), "s"(a.w), "s"(a.ws), "s"(a.x_in), "s"(a.emb), "s"(a.resid),
+                 "s"(a.norm_w), "s"(a.xq), "s"(a.xs), "s"(a.meta), "s"(a.out), "s"(gridDim.x));
     extern __shared__ __attribute__((aligned(16))) float lds[];
     const int lane = threadIdx.x & (L2Q_WAVE - 1);
     const int wv = threadIdx.x / L2Q_WAVE;
@@ -572,7 +577,11 @@ __global__ __launch_bounds__(gemv_waves(NS) * L2Q_WAVE) void k_gemv(GemvArgs a) 
     const int nchunks = a.cols / 4;
     if (PRO != kPreq) {
         // unconditional loads (clamped chunk index; see load_lane_raw)
-        const float* src = (PRO == kNorm && a.emb) ? a.emb + (size_t)a.meta[0] * a.cols : a.x_in;
+        // meta (written by the host each step) is read only for the embedding
+        // row of the first layer: a scalar load from memory the other loads
+        // would otherwise wait behind
+        const float* src = a.x_in;
+        if (PRO == kNorm && a.emb) src = a.emb + (size_t)__builtin_nontemporal_load(a.meta) * a.cols;
         const float* rsrc = (PRO == kNorm && a.resid) ? a.resid : src;
 #pragma unroll
         for (int k = 0; k < kProChunks; k++) {
@@ -588,9 +597,7 @@ __global__ __launch_bounds__(gemv_waves(NS) * L2Q_WAVE) void k_gemv(GemvArgs a) 
     // prologue, so the epilogue never waits on a global load queued behind
     // the weight stream
     uint64_t etab_v = 0;
-    float rope_v = 0.0f;
     if (EPI == kSwiglu) etab_v = kExp2Tab[threadIdx.x & 31];
-    if (EPI == kRopeKV) rope_v = a.rope[(size_t)a.meta[1] * a.hs + min((int)threadIdx.x, a.hs - 1)];
     int raw[ACTL ? 1 : NS][32 / BITS];
     float sc[ACTL ? 1 : NS];
     constexpr int kCopyChunks = ACTL && PRO == kPreq ? (NS * 512 / BITS + THREADS - 1) / THREADS : 1;   // 16-byte xq chunks
@@ -637,6 +644,10 @@ __global__ __launch_bounds__(gemv_waves(NS) * L2Q_WAVE) void k_gemv(GemvArgs a) 
     const bool has_work = u0 < u1;   // wave-uniform
     load_unit(u0);
     __builtin_amdgcn_sched_barrier(0);
+    // the RoPE row of this position: its address needs meta, so it is
+    // issued after everything that does not
+    float rope_v = 0.0f;
+    if (EPI == kRopeKV) rope_v = a.rope[(size_t)a.meta[1] * a.hs + min((int)threadIdx.x, a.hs - 1)];
 
     // 3. prologue (workgroup-wide) while the weights stream in
     if (EPI == kSwiglu && threadIdx.x < 32) etab[threadIdx.x] = etab_v;

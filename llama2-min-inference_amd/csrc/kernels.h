@@ -255,70 +255,157 @@ __host__ __device__ constexpr size_t attn_lds_bytes(int hs) {
 // Attention in the reference's exact order (runq.c:367-391, softmax
 // :307-318), in two kernels:
 //
-// k_attn_scores: workgroup (head h, block of kScoreTile positions) stages
-//   the K rows in LDS with coalesced 128-bit loads, then one lane per
-//   position forms sum_i q_i*k_i over the head in index order (products
-//   rounded, added in order - GCC vectorises the reference loop that way;
-//   a remainder of head_size % 8 is fused), then / sqrtf(head_size).
-// k_attn_softmax_v: workgroup (head h, 32-wide slice of the head) takes
-//   the max of the head's scores, e_t = expf(s_t - max) with the
-//   host-identical exp_runq, the sum of e_t in position order (one lane),
-//   p_t = e_t / sum, and then one lane per output element accumulates
-//   fma(p_t, v_t[i], acc) in position order.  V is streamed through LDS
-//   in chunks of kVChunk positions by the whole workgroup (the next chunk's
-//   loads are in flight while the current chunk is folded), so the serial
-//   chains never wait on HBM.
-constexpr int kScoreTile = 64;
-constexpr int kVSlice = 32;
-constexpr int kVChunk = 128;
-constexpr int kVPer = kVChunk * kVSlice / 4 / kAttnThreads;   // float4 per thread per chunk
-constexpr int kScorePer = 16;                                   // scores per thread -> n <= 4096
+// k_attn_scores: one workgroup per work item (head h, tile of kScoreTile
+//   positions), persistent over the items of the current position: the K
+//   rows of the tile are staged in LDS with coalesced 128-bit loads (all in
+//   flight at once), then one lane per position forms
+//   sum_i q_i*k_i over the head in index order
+//   (products rounded, added in order - GCC vectorises the reference loop
+//   that way; a remainder of head_size % 8 is fused), then / sqrtf(hs).
+// k_attn_softmax_v: workgroup (head h, kVDims output elements) takes the
+//   max of the head's scores, e_t = expf(s_t - max) with the host-identical
+//   exp_runq, the sum of e_t in position order (one lane), p_t = e_t / sum,
+//   and then one lane per output element accumulates fma(p_t, v_t[i], acc)
+//   in position order.  V is streamed through LDS in chunks of kVChunk
+//   positions, transposed to [element][position] so that each chain reads
+//   four positions per LDS load; both serial chains read their operands a
+//   block ahead of the FMAs, and the next V chunk's loads are in flight
+//   while the current chunk is folded.
+constexpr int kScoreTile = 16;
+constexpr int kScoreThreads = L2Q_WAVE;
+constexpr int kScoreGridMax = 1024;
+constexpr int kVDims = 16;
+constexpr int kVChunk = 256;
+constexpr int kVStride = kVChunk + 4;                              // LDS row of one element's chunk
+constexpr int kVPer = kVChunk * kVDims / 4 / kAttnThreads;         // float4 per thread per chunk
+constexpr int kScorePer = 16;                                      // scores per thread -> n <= 4096
 
 __host__ __device__ constexpr size_t attn_scores_lds_bytes(int hs) {
     return ((size_t)kScoreTile * (hs + 4) + hs) * sizeof(float);
 }
 __host__ __device__ constexpr size_t attn_v_lds_bytes(int max_t) {
-    return ((size_t)max_t + 4 + 2 * kVChunk * kVSlice + 8) * sizeof(float);
+    return ((size_t)(max_t + 7) / 4 * 4 + 2 * kVDims * kVStride + 8) * sizeof(float);
 }
 
-__global__ __launch_bounds__(kAttnThreads) void k_attn_scores(
+// q.k over a head in the reference's order: products rounded, added in
+// index order for the first hs & ~7 elements, the rest fused (k and q in
+// LDS, 16-byte aligned).  Straight-line blocks of 16 elements: the block's
+// LDS reads are issued together, then its 16 dependent adds.
+__device__ __forceinline__ float serial_dot(const float* kr, const float* qs, int hs) {
+#pragma clang fp contract(off)
+    const float4* k4 = reinterpret_cast<const float4*>(kr);
+    const float4* q4 = reinterpret_cast<const float4*>(qs);
+    const int nv = hs & ~7;
+    float score = 0.0f;
+    int i = 0;
+#pragma unroll 2
+    for (; i + 16 <= nv; i += 16) {
+        float4 K[4], Q[4];
+#pragma unroll
+        for (int u = 0; u < 4; u++) { K[u] = k4[i / 4 + u]; Q[u] = q4[i / 4 + u]; }
+#pragma unroll
+        for (int u = 0; u < 4; u++) {
+            score = score + Q[u].x * K[u].x;
+            score = score + Q[u].y * K[u].y;
+            score = score + Q[u].z * K[u].z;
+            score = score + Q[u].w * K[u].w;
+        }
+    }
+    for (; i < nv; i += 4) {
+        const float4 k = k4[i / 4], q = q4[i / 4];
+        score = score + q.x * k.x;
+        score = score + q.y * k.y;
+        score = score + q.z * k.z;
+        score = score + q.w * k.w;
+    }
+    for (; i < hs; i++) score = __builtin_fmaf(qs[i], kr[i], score);
+    return score;
+}
+
+__global__ __launch_bounds__(kScoreThreads) void k_attn_scores(
     const float* __restrict__ q, const float* __restrict__ kcache, float* __restrict__ scores,
-    const int* __restrict__ meta, int pos_arg, int kv_mul, int hs, int max_t) {
+    const int* __restrict__ meta, int pos_arg, int kv_mul, int n_heads, int hs, int max_t) {
 #pragma clang fp contract(off)
     extern __shared__ __attribute__((aligned(16))) float sm[];
     const int hsp = hs + 4;
     float* kt = sm;                       // [kScoreTile][hsp]
     float* qs = kt + kScoreTile * hsp;    // [hs]
-    const int h = blockIdx.x;
+    const int tid = threadIdx.x;
     const int pos = meta_pos(meta, pos_arg);
     const int n = pos + 1;
-    const int t0 = blockIdx.y * kScoreTile;
-    if (t0 >= n) return;                  // uniform: the grid covers max_t
-    const int nt = min(kScoreTile, n - t0);
+    const int ntile = (n + kScoreTile - 1) / kScoreTile;
     const int f4 = hs / 4;
-    const float* kbase = kcache + ((size_t)(h / kv_mul) * max_t + t0) * hs;
-    for (int f = threadIdx.x; f < nt * f4; f += kAttnThreads) {
-        const int r = f / f4, c4 = f - r * f4;
-        *reinterpret_cast<float4*>(kt + r * hsp + 4 * c4) = *reinterpret_cast<const float4*>(kbase + (size_t)r * hs + 4 * c4);
-    }
-    for (int d = threadIdx.x; d < hs; d += kAttnThreads) qs[d] = q[(size_t)h * hs + d];
-    __syncthreads();
-    if (threadIdx.x < nt) {
-        const float* kr = kt + threadIdx.x * hsp;
-        const int nv = hs & ~7;
-        float score = 0.0f;
-        int i = 0;
-        for (; i < nv; i += 4) {
-            const float4 k4 = *reinterpret_cast<const float4*>(kr + i);
-            const float4 q4 = *reinterpret_cast<const float4*>(qs + i);
-            score = score + q4.x * k4.x;
-            score = score + q4.y * k4.y;
-            score = score + q4.z * k4.z;
-            score = score + q4.w * k4.w;
+    for (int item = blockIdx.x; item < n_heads * ntile; item += gridDim.x) {
+        const int h = item / ntile;
+        const int t0 = (item - h * ntile) * kScoreTile;
+        const int nt = min(kScoreTile, n - t0);
+        const float* kbase = kcache + ((size_t)(h / kv_mul) * max_t + t0) * hs;
+        // the tile's loads in batches of 8 float4 per lane, all of a batch in
+        // flight at once (one batch covers a 16 x 128 tile)
+        for (int b0 = 0; b0 < nt * f4; b0 += 8 * kScoreThreads) {
+            float4 kv[8];
+#pragma unroll
+            for (int k = 0; k < 8; k++) {
+                const int f = min(b0 + tid + kScoreThreads * k, nt * f4 - 1);
+                const int r = f / f4, c4 = f - r * f4;
+                kv[k] = *reinterpret_cast<const float4*>(kbase + (size_t)r * hs + 4 * c4);
+            }
+#pragma unroll
+            for (int k = 0; k < 8; k++) {
+                const int f = b0 + tid + kScoreThreads * k;
+                if (f < nt * f4) {
+                    const int r = f / f4, c4 = f - r * f4;
+                    *reinterpret_cast<float4*>(kt + r * hsp + 4 * c4) = kv[k];
+                }
+            }
         }
-        for (; i < hs; i++) score = __builtin_fmaf(qs[i], kr[i], score);
-        scores[(size_t)h * max_t + t0 + threadIdx.x] = score / sqrtf((float)hs);
+        for (int d = tid; d < hs; d += kScoreThreads) qs[d] = q[(size_t)h * hs + d];
+        __syncthreads();
+        if (tid < nt) scores[(size_t)h * max_t + t0 + tid] = serial_dot(kt + tid * hsp, qs, hs) / sqrtf((float)hs);
+        __syncthreads();   // the next item restages the tile
     }
+}
+
+// Sequential sum of p[0..n) (p 16-byte aligned in LDS), non-fused adds in
+// index order, in straight-line blocks of 16 (reads first, then the adds).
+__device__ __forceinline__ float serial_sum(const float* p, int n) {
+#pragma clang fp contract(off)
+    const float4* p4 = reinterpret_cast<const float4*>(p);
+    float sum = 0.0f;
+    int t = 0;
+#pragma unroll 2
+    for (; t + 16 <= n; t += 16) {
+        float4 v[4];
+#pragma unroll
+        for (int u = 0; u < 4; u++) v[u] = p4[t / 4 + u];
+#pragma unroll
+        for (int u = 0; u < 4; u++) { sum = sum + v[u].x; sum = sum + v[u].y; sum = sum + v[u].z; sum = sum + v[u].w; }
+    }
+    for (; t < n; t++) sum = sum + p[t];
+    return sum;
+}
+
+// acc = fma(p[t], v[t], acc) for t = 0..n-1 in order (both 16-byte aligned
+// in LDS), in straight-line blocks of 16.
+__device__ __forceinline__ float serial_pv(const float* p, const float* v, int n, float acc) {
+    const float4* p4 = reinterpret_cast<const float4*>(p);
+    const float4* v4 = reinterpret_cast<const float4*>(v);
+    int t = 0;
+#pragma unroll 2
+    for (; t + 16 <= n; t += 16) {
+        float4 P[4], V[4];
+#pragma unroll
+        for (int u = 0; u < 4; u++) { P[u] = p4[t / 4 + u]; V[u] = v4[t / 4 + u]; }
+#pragma unroll
+        for (int u = 0; u < 4; u++) {
+            acc = __builtin_fmaf(P[u].x, V[u].x, acc);
+            acc = __builtin_fmaf(P[u].y, V[u].y, acc);
+            acc = __builtin_fmaf(P[u].z, V[u].z, acc);
+            acc = __builtin_fmaf(P[u].w, V[u].w, acc);
+        }
+    }
+    for (; t < n; t++) acc = __builtin_fmaf(p[t], v[t], acc);
+    return acc;
 }
 
 __global__ __launch_bounds__(kAttnThreads) void k_attn_softmax_v(
@@ -327,13 +414,13 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn_softmax_v(
 #pragma clang fp contract(off)
     extern __shared__ __attribute__((aligned(16))) float smem[];
     float* p = smem;                                     // [max_t] probabilities
-    float* vb = smem + ((max_t + 3) & ~3);               // [2][kVChunk][kVSlice]
-    float* red = vb + 2 * kVChunk * kVSlice;             // [4] wave maxima, [4] sum
-    const int h = blockIdx.x, d0 = blockIdx.y * kVSlice;
+    float* vt = smem + (max_t + 7) / 4 * 4;              // [2][kVDims][kVStride]
+    float* red = vt + 2 * kVDims * kVStride;             // [4] wave maxima, [4] sum
+    const int h = blockIdx.x, d0 = blockIdx.y * kVDims;
     const int tid = threadIdx.x, lane = tid & (L2Q_WAVE - 1), wv = tid / L2Q_WAVE;
     const int pos = meta_pos(meta, pos_arg);
     const int n = pos + 1;
-    const int width = min(kVSlice, hs - d0);
+    const int width = min(kVDims, hs - d0);
     const float* sc = scores + (size_t)h * max_t;
     const float* vbase = vcache + (size_t)(h / kv_mul) * max_t * hs + d0;
     const int nchunks = (n + kVChunk - 1) / kVChunk;
@@ -350,16 +437,23 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn_softmax_v(
 #pragma unroll
         for (int k = 0; k < kVPer; k++) {
             const int e = tid + kAttnThreads * k;                 // float4 index in the chunk
-            const int r = e / (kVSlice / 4), c4 = e % (kVSlice / 4);
+            const int r = e / (kVDims / 4), c4 = e % (kVDims / 4);
             const int t = c * kVChunk + r;
             vr[k] = (t < n && 4 * c4 < width) ? *reinterpret_cast<const float4*>(vbase + (size_t)t * hs + 4 * c4)
                                               : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
         }
     };
-    auto store_chunk = [&](int buf) {
-        float* dst = vb + buf * kVChunk * kVSlice;
+    auto store_chunk = [&](int buf) {   // transposed: vt[buf][element][position]
+        float* dst = vt + buf * kVDims * kVStride;
 #pragma unroll
-        for (int k = 0; k < kVPer; k++) reinterpret_cast<float4*>(dst)[tid + kAttnThreads * k] = vr[k];
+        for (int k = 0; k < kVPer; k++) {
+            const int e = tid + kAttnThreads * k;
+            const int r = e / (kVDims / 4), c4 = e % (kVDims / 4);
+            dst[(4 * c4 + 0) * kVStride + r] = vr[k].x;
+            dst[(4 * c4 + 1) * kVStride + r] = vr[k].y;
+            dst[(4 * c4 + 2) * kVStride + r] = vr[k].z;
+            dst[(4 * c4 + 3) * kVStride + r] = vr[k].w;
+        }
     };
     load_chunk(0);
 
@@ -367,35 +461,28 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn_softmax_v(
     float m = -INFINITY;
 #pragma unroll
     for (int k = 0; k < kScorePer; k++) m = fmaxf(m, s[k]);
-    m = wave_max(m);
+    m = group_max<L2Q_WAVE>(m);
     if (lane == 0) red[wv] = m;
     __syncthreads();
     m = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+    float e[kScorePer];
 #pragma unroll
     for (int k = 0; k < kScorePer; k++) {
         const int t = tid + kAttnThreads * k;
-        if (t < n) p[t] = exp_runq(s[k] - m);
+        e[k] = 0.0f;
+        if (kAttnThreads * k < n && t < n) {   // the first test is uniform: skips whole rounds
+            e[k] = exp_runq(s[k] - m);
+            p[t] = e[k];
+        }
     }
     __syncthreads();
-    if (tid == 0) {
-        float sum = 0.0f;
-        int t = 0;
-        for (; t + 8 <= n; t += 8) {
-            float e[8];
-#pragma unroll
-            for (int u = 0; u < 8; u++) e[u] = p[t + u];
-#pragma unroll
-            for (int u = 0; u < 8; u++) sum += e[u];
-        }
-        for (; t < n; t++) sum += p[t];
-        red[4] = sum;
-    }
+    if (tid == 0) red[4] = serial_sum(p, n);
     __syncthreads();
     const float sum = red[4];
 #pragma unroll
     for (int k = 0; k < kScorePer; k++) {
         const int t = tid + kAttnThreads * k;
-        if (t < n) p[t] = p[t] / sum;
+        if (kAttnThreads * k < n && t < n) p[t] = e[k] / sum;
     }
     store_chunk(0);
     __syncthreads();
@@ -406,17 +493,7 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn_softmax_v(
         if (c + 1 < nchunks) load_chunk(c + 1);
         if (wv == 0 && lane < width) {
             const int tb = c * kVChunk;
-            const int nt = min(kVChunk, n - tb);
-            const float* src = vb + (c & 1) * kVChunk * kVSlice + lane;
-            int j = 0;
-            for (; j + 8 <= nt; j += 8) {
-                float pv[8], vv[8];
-#pragma unroll
-                for (int u = 0; u < 8; u++) { pv[u] = p[tb + j + u]; vv[u] = src[(j + u) * kVSlice]; }
-#pragma unroll
-                for (int u = 0; u < 8; u++) acc = __builtin_fmaf(pv[u], vv[u], acc);
-            }
-            for (; j < nt; j++) acc = __builtin_fmaf(p[tb + j], src[j * kVSlice], acc);
+            acc = serial_pv(p + tb, vt + (c & 1) * kVDims * kVStride + lane * kVStride, min(kVChunk, n - tb), acc);
         }
         if (c + 1 < nchunks) store_chunk((c + 1) & 1);
         __syncthreads();

@@ -239,13 +239,15 @@ int launch_attention_exact(const float* q, const float* kcache, const float* vca
         return L2Q_ERR_ARG;
     }
     const int kv_mul = n_heads / n_kv_heads;
-    // the graph covers every position the cache can hold; blocks past pos exit
-    const int tiles = meta ? (max_t + kScoreTile - 1) / kScoreTile : (pos + kScoreTile) / kScoreTile;
-    hipLaunchKernelGGL(k_attn_scores, dim3(n_heads, tiles), dim3(kAttnThreads), attn_scores_lds_bytes(hs), st, q,
-                       kcache, scores, meta, pos, kv_mul, hs, max_t);
+    // persistent score waves over (head, tile) items; a captured graph covers
+    // every position the cache can hold, items past pos are not visited
+    const int items = n_heads * ((meta ? max_t : pos + 1) + kScoreTile - 1) / kScoreTile;
+    const int grid = items < kScoreGridMax ? items : kScoreGridMax;
+    hipLaunchKernelGGL(k_attn_scores, dim3(grid), dim3(kScoreThreads), attn_scores_lds_bytes(hs), st, q, kcache,
+                       scores, meta, pos, kv_mul, n_heads, hs, max_t);
     int rc = check_launch("attention_scores");
     if (rc) return rc;
-    hipLaunchKernelGGL(k_attn_softmax_v, dim3(n_heads, (hs + kVSlice - 1) / kVSlice), dim3(kAttnThreads),
+    hipLaunchKernelGGL(k_attn_softmax_v, dim3(n_heads, (hs + kVDims - 1) / kVDims), dim3(kAttnThreads),
                        attn_v_lds_bytes(max_t), st, scores, vcache, out, meta, pos, kv_mul, hs, max_t);
     return check_launch("attention_softmax_v");
 }

@@ -1,6 +1,6 @@
 """The GPU quantizer's division-free path (device.h q8_value_fast), restated
 in numpy float32 on the CPU: y = x * rcp(s), q = rint(y), and the correctly
-rounded x / s wherever |y - q| >= 0.5 - |y| * 2^-20.  It must equal the
+rounded x / s wherever |y - q| >= 0.5 - 2^-13.  It must equal the
 reference's rint(x / s) (runq.c:117-139) on every input, including inputs
 a few ulps from the rounding boundaries (k + 1/2) * s, with rcp modelled as
 1 ulp off in either direction.  The GPU kernel itself is checked against the
@@ -13,8 +13,7 @@ F = np.float32
 def fast_quantize(x, s, r):
     y = (x * r).astype(F)
     q = np.rint(y).astype(F)
-    thr = (F(0.5) - np.abs(y).astype(np.float64) * 2.0 ** -20).astype(F)   # one rounding, as the fma
-    slow = ~(np.abs((y - q).astype(F)) < thr)
+    slow = ~(np.abs((y - q).astype(F)) < F(0.5) - F(2.0 ** -13))
     return np.where(slow, np.rint((x / s).astype(F)), q), slow
 
 
@@ -40,5 +39,5 @@ def test_fast_quantizer_equals_division():
         q, slow = fast_quantize(x, S, r)
         np.testing.assert_array_equal(q, exact)
         assert slow[pick].mean() > 0.5          # the guard does fire near the boundaries
-        assert slow[~pick].mean() < 1e-3        # and almost never elsewhere
+        assert slow[~pick].mean() < 2e-3        # and almost never elsewhere
     assert np.abs(exact).max() <= 127           # the clamp of the reference never binds
