@@ -21,6 +21,9 @@ constexpr int kAttnMaxHs = 256;      // largest head size
 typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 
 // 128-bit weight load.
+#ifndef L2Q_INPUT_FIRST
+#define L2Q_INPUT_FIRST 1
+#endif
 #ifndef L2Q_WEIGHT_NT
 #define L2Q_WEIGHT_NT 1
 #endif

@@ -124,8 +124,10 @@ __host__ __device__ constexpr int sumsq_stride(int n) { return ((n + 15) / 16 + 
 // LDS layout: [fold: waves x (terms, scales) x F x nbp floats]
 //             [act_q: cols int8, padded to 32 B][act_s: nb floats, padded to 4]
 //             [vt: the residual sum, transposed for the norm chains (kNorm): 16 x sumsq_stride(cols) floats]
-//             [misc: 4 floats | exp table: 32 doubles | RoPE row of the position: up to 256 floats]
-constexpr int kGemvMiscFloats = 4 + 64 + 256;
+//             [misc: 4 floats | exp table: 32 doubles]
+constexpr int kGemvMiscFloats = 4 + 64;
+// RoPE values held per lane by the kRopeKV epilogue (head size <= 256)
+constexpr int kRopeRegs = kAttnMaxHs / L2Q_WAVE;
 __host__ __device__ constexpr size_t gemv_fold_floats(int nb, int waves) {
     return (size_t)waves * 2 * gemv_fold_rows(nb, waves) * gemv_nbp(nb);
 }
@@ -469,49 +471,57 @@ __device__ __forceinline__ void prologue_compute(const GemvArgs& a, float4 (&xin
     __syncthreads();
 }
 
-// Ordered fold of one row: sum_b fma(ws_b, t_b, sum) for b = 0..nb-1, the
-// terms and scales read from LDS 16 groups ahead of the FMA chain.
+// Ordered fold of one row: sum_b fma(ws_b, t_b, sum) for b = 0..nb-1.  The
+// terms and scales stream from LDS through a ring of R blocks of 4 groups,
+// each block loaded R-1 blocks ahead of the FMA chain, so the chain never
+// waits on LDS and no registers are copied between iterations.  Loads run
+// up to R blocks past the row (into the next row's area, or the activation
+// area after the last one: always inside the workgroup's LDS); what they
+// read is never folded.
+template <int R = 6>
 __device__ __forceinline__ float fold_row(const float* tp, const float* sp, int nb) {
-    float sum = 0.0f;
     const float4* t4 = reinterpret_cast<const float4*>(tp);
     const float4* s4 = reinterpret_cast<const float4*>(sp);
-    const int n4 = nb >> 2;
+    const int nfull = nb >> 2;             // whole blocks of 4 groups
+    const int rem = nb & 3;                // groups in a trailing partial block
+    float4 T[R], S[R];
+#pragma unroll
+    for (int j = 0; j < R; j++) {
+        T[j] = t4[j];
+        S[j] = s4[j];
+    }
+    float sum = 0.0f;
     int b = 0;
-    if (n4 >= 4) {
-        float4 t[4], s[4];
+    for (; b + R <= nfull; b += R) {
 #pragma unroll
-        for (int u = 0; u < 4; u++) { t[u] = t4[u]; s[u] = s4[u]; }
-        for (; b + 8 <= n4; b += 4) {
-            float4 tn[4], sn[4];
-#pragma unroll
-            for (int u = 0; u < 4; u++) { tn[u] = t4[b + 4 + u]; sn[u] = s4[b + 4 + u]; }
-#pragma unroll
-            for (int u = 0; u < 4; u++) {
-                sum = __builtin_fmaf(s[u].x, t[u].x, sum);
-                sum = __builtin_fmaf(s[u].y, t[u].y, sum);
-                sum = __builtin_fmaf(s[u].z, t[u].z, sum);
-                sum = __builtin_fmaf(s[u].w, t[u].w, sum);
-            }
-#pragma unroll
-            for (int u = 0; u < 4; u++) { t[u] = tn[u]; s[u] = sn[u]; }
+        for (int j = 0; j < R; j++) {
+            sum = __builtin_fmaf(S[j].x, T[j].x, sum);
+            sum = __builtin_fmaf(S[j].y, T[j].y, sum);
+            sum = __builtin_fmaf(S[j].z, T[j].z, sum);
+            sum = __builtin_fmaf(S[j].w, T[j].w, sum);
+            // keep the reload after the block's last use, so the slot's
+            // registers are reused rather than copied
+            __builtin_amdgcn_sched_barrier(0);
+            T[j] = t4[b + j + R];
+            S[j] = s4[b + j + R];
+            __builtin_amdgcn_sched_barrier(0);
         }
+    }
+    // slot j now holds block b + j: fewer than R whole blocks remain, then
+    // possibly one partial block
 #pragma unroll
-        for (int u = 0; u < 4; u++) {
-            sum = __builtin_fmaf(s[u].x, t[u].x, sum);
-            sum = __builtin_fmaf(s[u].y, t[u].y, sum);
-            sum = __builtin_fmaf(s[u].z, t[u].z, sum);
-            sum = __builtin_fmaf(s[u].w, t[u].w, sum);
+    for (int j = 0; j < R; j++) {
+        if (b + j < nfull) {
+            sum = __builtin_fmaf(S[j].x, T[j].x, sum);
+            sum = __builtin_fmaf(S[j].y, T[j].y, sum);
+            sum = __builtin_fmaf(S[j].z, T[j].z, sum);
+            sum = __builtin_fmaf(S[j].w, T[j].w, sum);
+        } else if (b + j == nfull && rem) {
+            sum = __builtin_fmaf(S[j].x, T[j].x, sum);
+            if (rem > 1) sum = __builtin_fmaf(S[j].y, T[j].y, sum);
+            if (rem > 2) sum = __builtin_fmaf(S[j].z, T[j].z, sum);
         }
-        b += 4;
     }
-    for (; b < n4; b++) {
-        const float4 t = t4[b], s = s4[b];
-        sum = __builtin_fmaf(s.x, t.x, sum);
-        sum = __builtin_fmaf(s.y, t.y, sum);
-        sum = __builtin_fmaf(s.z, t.z, sum);
-        sum = __builtin_fmaf(s.w, t.w, sum);
-    }
-    for (int g = n4 * 4; g < nb; g++) sum = __builtin_fmaf(sp[g], tp[g], sum);
     return sum;
 }
 
@@ -558,7 +568,6 @@ __global__ __launch_bounds__(gemv_waves(NS) * L2Q_WAVE) void k_gemv(GemvArgs a) 
     float* vs = act_s + (nb + 3) / 4 * 4;
     float* misc = vs + (PRO == kNorm ? 16 * sumsq_stride(a.cols) : 0);
     uint64_t* etab = reinterpret_cast<uint64_t*>(misc + 4);   // exp table (kSwiglu)
-    float* rope_l = misc + 4 + 64;                             // RoPE row of the position (kRopeKV)
     const int rowbytes = a.cols * BITS / 8;
     const uint8_t* wbase = static_cast<const uint8_t*>(a.w);
     const bool leader = (lane % C::P) == 0;
@@ -598,6 +607,10 @@ __global__ __launch_bounds__(gemv_waves(NS) * L2Q_WAVE) void k_gemv(GemvArgs a) 
     // the weight stream
     uint64_t etab_v = 0;
     if (EPI == kSwiglu) etab_v = kExp2Tab[threadIdx.x & 31];
+    // the position, for the RoPE row: loaded ahead of the weights, so that
+    // addressing the row waits for nothing behind it
+    int pos = 0;
+    if (EPI == kRopeKV) pos = a.meta[1];
     int raw[ACTL ? 1 : NS][32 / BITS];
     float sc[ACTL ? 1 : NS];
     constexpr int kCopyChunks = ACTL && PRO == kPreq ? (NS * 512 / BITS + THREADS - 1) / THREADS : 1;   // 16-byte xq chunks
@@ -616,6 +629,12 @@ __global__ __launch_bounds__(gemv_waves(NS) * L2Q_WAVE) void k_gemv(GemvArgs a) 
             for (int k = 0; k < kXsChunks; k++) xsv[k] = a.xs[min((int)threadIdx.x + THREADS * k, nb - 1)];
         }
     }
+#if L2Q_INPUT_FIRST
+    // a computing prologue: let its inputs arrive before this grid's weight
+    // requests queue in front of them (measured: faster in the decode step;
+    // pre-quantized inputs are better left to arrive with the weights)
+    if (PRO != kPreq) __builtin_amdgcn_s_waitcnt(0x0F70);   // vmcnt(0)
+#endif
     __builtin_amdgcn_sched_barrier(0);
 
     // 2. weight loads: every load is issued unconditionally (addresses past
@@ -646,12 +665,19 @@ __global__ __launch_bounds__(gemv_waves(NS) * L2Q_WAVE) void k_gemv(GemvArgs a) 
     __builtin_amdgcn_sched_barrier(0);
     // the RoPE row of this position: its address needs meta, so it is
     // issued after everything that does not
-    float rope_v = 0.0f;
-    if (EPI == kRopeKV) rope_v = a.rope[(size_t)a.meta[1] * a.hs + min((int)threadIdx.x, a.hs - 1)];
+    // the RoPE row of the position, kRopeRegs values per lane (element
+    // lane + 64k in register k), gathered by the fold's epilogue
+    float rope_r[kRopeRegs] = {};
+    if (EPI == kRopeKV) {
+#pragma unroll
+        for (int k = 0; k < kRopeRegs; k++) rope_r[k] = a.rope[(size_t)pos * a.hs + min(lane + 64 * k, a.hs - 1)];
+    }
 
     // 3. prologue (workgroup-wide) while the weights stream in
-    if (EPI == kSwiglu && threadIdx.x < 32) etab[threadIdx.x] = etab_v;
-    if (EPI == kRopeKV && (int)threadIdx.x < a.hs) rope_l[threadIdx.x] = rope_v;
+    // every thread stores its entry (duplicates write the same value): a
+    // store under a thread condition lets the compiler sink the table load
+    // behind the weight loads, where waiting for it waits for them
+    if (EPI == kSwiglu) etab[threadIdx.x & 31] = etab_v;
     if (PRO != kPreq) {
         prologue_compute<G, PRO, kProChunks, kResChunks, SPLIT, THREADS>(a, xin, res, nw, act_q, act_s, vs, misc, nchunks);
         if constexpr (!ACTL) load_lane_raw<BITS, G, NS>(raw, sc, act_q, act_s, a.cols, lane);
@@ -730,21 +756,27 @@ __global__ __launch_bounds__(gemv_waves(NS) * L2Q_WAVE) void k_gemv(GemvArgs a) 
         } else if (EPI == kRopeKV) {
             // rows come in (even, odd) pairs held by lanes (0,1), (2,3), ...
             const float other = dpp_f<kDppXor1>(sum);
+            // (cos, sin) of this lane's pair, gathered from the RoPE
+            // registers by every lane (a permute reads any lane's value)
+            const int e = row < a.dim ? row : row - a.dim;
+            const int hd = (e & ~1) % a.hs;
+            float c = 0.0f, s = 0.0f;
+#pragma unroll
+            for (int k = 0; k < kRopeRegs; k++) {
+                const float ck = __shfl(rope_r[k], hd & 63);
+                const float sk = __shfl(rope_r[k], (hd + 1) & 63);
+                if ((hd >> 6) == k) { c = ck; s = sk; }
+            }
             if (mine && row < a.rows) {
-                const int pos = a.meta[1];
                 const bool odd = row & 1;
                 const float v0 = odd ? other : sum, v1 = odd ? sum : other;
                 if (row < a.dim + a.kv_dim) {            // q or k: rotate
-                    const int e = row < a.dim ? row : row - a.dim;
-                    const int hd = (e & ~1) % a.hs;
-                    const float c = rope_l[hd];
-                    const float s = rope_l[hd + 1];
                     const float r = odd ? __builtin_fmaf(v0, s, v1 * c) : __builtin_fmaf(v0, c, -(v1 * s));
                     if (row < a.dim) a.out[row] = r;
                     else a.kcache[((size_t)(e / a.hs) * a.max_t + pos) * a.hs + (e % a.hs)] = r;
                 } else {                                  // v: appended as is
-                    const int e = row - a.dim - a.kv_dim;
-                    a.vcache[((size_t)(e / a.hs) * a.max_t + pos) * a.hs + (e % a.hs)] = sum;
+                    const int ev = row - a.dim - a.kv_dim;
+                    a.vcache[((size_t)(ev / a.hs) * a.max_t + pos) * a.hs + (ev % a.hs)] = sum;
                 }
             }
         } else {   // kSwiglu: (w1, w3) pairs on lanes (0,1), (2,3), ...

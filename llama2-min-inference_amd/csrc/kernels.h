@@ -280,45 +280,55 @@ constexpr int kVStride = kVChunk + 4;                              // LDS row of
 constexpr int kVPer = kVChunk * kVDims / 4 / kAttnThreads;         // float4 per thread per chunk
 constexpr int kScorePer = 16;                                      // scores per thread -> n <= 4096
 
+// (+ kRingSlack floats: the serial chains' ring reads run up to 24 floats
+// past their arrays)
+constexpr int kRingSlack = 32;
 __host__ __device__ constexpr size_t attn_scores_lds_bytes(int hs) {
-    return ((size_t)kScoreTile * (hs + 4) + hs) * sizeof(float);
+    return ((size_t)kScoreTile * (hs + 4) + hs + kRingSlack) * sizeof(float);
 }
 __host__ __device__ constexpr size_t attn_v_lds_bytes(int max_t) {
-    return ((size_t)(max_t + 7) / 4 * 4 + 2 * kVDims * kVStride + 8) * sizeof(float);
+    return ((size_t)(max_t + 7) / 4 * 4 + 2 * kVDims * kVStride + 8 + kRingSlack) * sizeof(float);
 }
 
 // q.k over a head in the reference's order: products rounded, added in
 // index order for the first hs & ~7 elements, the rest fused (k and q in
-// LDS, 16-byte aligned).  Straight-line blocks of 16 elements: the block's
-// LDS reads are issued together, then its 16 dependent adds.
+// LDS, 16-byte aligned).  k streams through a ring of R float4 blocks, each
+// loaded R-1 blocks ahead of the adds; loads may run up to R blocks past
+// the row (inside the workgroup's LDS), never added.
+template <int R = 6>
 __device__ __forceinline__ float serial_dot(const float* kr, const float* qs, int hs) {
 #pragma clang fp contract(off)
     const float4* k4 = reinterpret_cast<const float4*>(kr);
     const float4* q4 = reinterpret_cast<const float4*>(qs);
-    const int nv = hs & ~7;
+    const int nv = (hs & ~7) >> 2;   // float4 blocks added unfused
+    float4 K[R], Q[R];
+#pragma unroll
+    for (int j = 0; j < R; j++) { K[j] = k4[j]; Q[j] = q4[j]; }
     float score = 0.0f;
-    int i = 0;
-#pragma unroll 2
-    for (; i + 16 <= nv; i += 16) {
-        float4 K[4], Q[4];
+    int b = 0;
+    for (; b + R <= nv; b += R) {
 #pragma unroll
-        for (int u = 0; u < 4; u++) { K[u] = k4[i / 4 + u]; Q[u] = q4[i / 4 + u]; }
-#pragma unroll
-        for (int u = 0; u < 4; u++) {
-            score = score + Q[u].x * K[u].x;
-            score = score + Q[u].y * K[u].y;
-            score = score + Q[u].z * K[u].z;
-            score = score + Q[u].w * K[u].w;
+        for (int j = 0; j < R; j++) {
+            score = score + Q[j].x * K[j].x;
+            score = score + Q[j].y * K[j].y;
+            score = score + Q[j].z * K[j].z;
+            score = score + Q[j].w * K[j].w;
+            __builtin_amdgcn_sched_barrier(0);
+            K[j] = k4[b + j + R];
+            Q[j] = q4[b + j + R];
+            __builtin_amdgcn_sched_barrier(0);
         }
     }
-    for (; i < nv; i += 4) {
-        const float4 k = k4[i / 4], q = q4[i / 4];
-        score = score + q.x * k.x;
-        score = score + q.y * k.y;
-        score = score + q.z * k.z;
-        score = score + q.w * k.w;
+#pragma unroll
+    for (int j = 0; j < R; j++) {
+        if (b + j < nv) {
+            score = score + Q[j].x * K[j].x;
+            score = score + Q[j].y * K[j].y;
+            score = score + Q[j].z * K[j].z;
+            score = score + Q[j].w * K[j].w;
+        }
     }
-    for (; i < hs; i++) score = __builtin_fmaf(qs[i], kr[i], score);
+    for (int i = nv * 4; i < hs; i++) score = __builtin_fmaf(qs[i], kr[i], score);
     return score;
 }
 
@@ -367,44 +377,69 @@ __global__ __launch_bounds__(kScoreThreads) void k_attn_scores(
 }
 
 // Sequential sum of p[0..n) (p 16-byte aligned in LDS), non-fused adds in
-// index order, in straight-line blocks of 16 (reads first, then the adds).
+// index order.  p streams through a ring of R float4 blocks loaded R-1
+// blocks ahead of the adds (reads may run R blocks past p[n), inside the
+// workgroup's LDS, never added).
+template <int R = 6>
 __device__ __forceinline__ float serial_sum(const float* p, int n) {
 #pragma clang fp contract(off)
     const float4* p4 = reinterpret_cast<const float4*>(p);
+    const int nb = n >> 2;
+    float4 P[R];
+#pragma unroll
+    for (int j = 0; j < R; j++) P[j] = p4[j];
     float sum = 0.0f;
-    int t = 0;
-#pragma unroll 2
-    for (; t + 16 <= n; t += 16) {
-        float4 v[4];
+    int b = 0;
+    for (; b + R <= nb; b += R) {
 #pragma unroll
-        for (int u = 0; u < 4; u++) v[u] = p4[t / 4 + u];
-#pragma unroll
-        for (int u = 0; u < 4; u++) { sum = sum + v[u].x; sum = sum + v[u].y; sum = sum + v[u].z; sum = sum + v[u].w; }
+        for (int j = 0; j < R; j++) {
+            sum = sum + P[j].x; sum = sum + P[j].y; sum = sum + P[j].z; sum = sum + P[j].w;
+            __builtin_amdgcn_sched_barrier(0);
+            P[j] = p4[b + j + R];
+            __builtin_amdgcn_sched_barrier(0);
+        }
     }
-    for (; t < n; t++) sum = sum + p[t];
+#pragma unroll
+    for (int j = 0; j < R; j++)
+        if (b + j < nb) { sum = sum + P[j].x; sum = sum + P[j].y; sum = sum + P[j].z; sum = sum + P[j].w; }
+    for (int t = nb * 4; t < n; t++) sum = sum + p[t];
     return sum;
 }
 
 // acc = fma(p[t], v[t], acc) for t = 0..n-1 in order (both 16-byte aligned
-// in LDS), in straight-line blocks of 16.
+// in LDS), through a ring of R float4 blocks of each (as serial_sum).
+template <int R = 6>
 __device__ __forceinline__ float serial_pv(const float* p, const float* v, int n, float acc) {
     const float4* p4 = reinterpret_cast<const float4*>(p);
     const float4* v4 = reinterpret_cast<const float4*>(v);
-    int t = 0;
-#pragma unroll 2
-    for (; t + 16 <= n; t += 16) {
-        float4 P[4], V[4];
+    const int nb = n >> 2;
+    float4 P[R], V[R];
 #pragma unroll
-        for (int u = 0; u < 4; u++) { P[u] = p4[t / 4 + u]; V[u] = v4[t / 4 + u]; }
+    for (int j = 0; j < R; j++) { P[j] = p4[j]; V[j] = v4[j]; }
+    int b = 0;
+    for (; b + R <= nb; b += R) {
 #pragma unroll
-        for (int u = 0; u < 4; u++) {
-            acc = __builtin_fmaf(P[u].x, V[u].x, acc);
-            acc = __builtin_fmaf(P[u].y, V[u].y, acc);
-            acc = __builtin_fmaf(P[u].z, V[u].z, acc);
-            acc = __builtin_fmaf(P[u].w, V[u].w, acc);
+        for (int j = 0; j < R; j++) {
+            acc = __builtin_fmaf(P[j].x, V[j].x, acc);
+            acc = __builtin_fmaf(P[j].y, V[j].y, acc);
+            acc = __builtin_fmaf(P[j].z, V[j].z, acc);
+            acc = __builtin_fmaf(P[j].w, V[j].w, acc);
+            __builtin_amdgcn_sched_barrier(0);
+            P[j] = p4[b + j + R];
+            V[j] = v4[b + j + R];
+            __builtin_amdgcn_sched_barrier(0);
         }
     }
-    for (; t < n; t++) acc = __builtin_fmaf(p[t], v[t], acc);
+#pragma unroll
+    for (int j = 0; j < R; j++) {
+        if (b + j < nb) {
+            acc = __builtin_fmaf(P[j].x, V[j].x, acc);
+            acc = __builtin_fmaf(P[j].y, V[j].y, acc);
+            acc = __builtin_fmaf(P[j].z, V[j].z, acc);
+            acc = __builtin_fmaf(P[j].w, V[j].w, acc);
+        }
+    }
+    for (int t = nb * 4; t < n; t++) acc = __builtin_fmaf(p[t], v[t], acc);
     return acc;
 }
 
