@@ -98,6 +98,15 @@ int l2q_engine_create(const l2q_config* cfg, const void* weights,
                       size_t weights_bytes, int wbits, int group,
                       int max_steps, l2q_engine** out);
 
+/* Engine options (l2q_engine_create_ex). */
+#define L2Q_ENGINE_KV_INT8 1   /* int8 KV cache (l2q_kv8_append / l2q_attention_kv8
+                                  semantics), the reference's -DINT8_KV=1 build */
+
+/* l2q_engine_create with option flags (0 gives l2q_engine_create). */
+int l2q_engine_create_ex(const l2q_config* cfg, const void* weights,
+                         size_t weights_bytes, int wbits, int group,
+                         int max_steps, int flags, l2q_engine** out);
+
 /* One decode step: embed `token`, run every layer at position `pos`
  * (appending its K/V), final norm and classifier.  If `logits` is not NULL
  * the vocab_size fp32 logits are copied into it (host memory).  Synchronous.
@@ -206,6 +215,31 @@ int l2q_attention(const float* q, const float* kcache, const float* vcache,
 int l2q_attention_split(const float* q, const float* kcache, const float* vcache,
                         float* out, int pos, int n_heads, int n_kv_heads,
                         int head_size, int max_t, void* stream);
+
+/* ---- int8 KV cache (v5-cuda-fused/run.cu:41-48, built there with
+ * -DINT8_KV=1) ----
+ * Layout: kcache8 / vcache8 [n_kv_heads][max_t][head_size] int8, one fp32
+ * scale per (kv head, position): kscale / vscale [n_kv_heads][max_t].
+ * head_size % 16 == 0, head_size <= 256. */
+
+/* Append position `pos`: k (n_kv_heads*head_size floats, rotated here with
+ * `rope` when it is not NULL, as l2q_rope_kv_append rotates) and v are
+ * quantized per kv head: s = amax/127 (1e-8 when 0), q = clamp(rint(x/s),
+ * -127, 127).  Replaces kv_quant_kernel (v5-cuda-fused/run.cu:204-249). */
+int l2q_kv8_append(const float* k, const float* v, int8_t* kcache8, int8_t* vcache8,
+                   float* kscale, float* vscale, const float* rope, int pos,
+                   int n_kv_heads, int head_size, int max_t, void* stream);
+
+/* Attention over positions 0..pos of an int8 cache: score_t = (q_h.k8_t) /
+ * sqrtf(hs) * kscale_t, softmax, out = sum_t p_t * vscale_t * v8_t.  Float
+ * results within 1e-5 relative of the same formula in double (the
+ * reference's own float order is a warp reduction, so no order is
+ * canonical).  Replaces attention_cache_kernel (v5-cuda-fused/run.cu:
+ * 350-410), which also quantizes its output; here the output stays fp32
+ * and the next GEMV's prologue quantizes it.  max_t <= 8192. */
+int l2q_attention_kv8(const float* q, const int8_t* kcache8, const int8_t* vcache8,
+                      const float* kscale, const float* vscale, float* out, int pos,
+                      int n_heads, int n_kv_heads, int head_size, int max_t, void* stream);
 
 /* expf exactly as the host C library computes it (the exp used by the
  * attention softmax and SwiGLU above), elementwise over n floats.  Exposed

@@ -41,6 +41,7 @@
 struct l2q_engine {
     l2q_config cfg;
     int wbits, G, max_t, kv_dim, hs, S;
+    int flags;               // L2Q_ENGINE_* options
     int device;
     hipStream_t stream = nullptr;
     hipGraph_t graph = nullptr, graph_am = nullptr;
@@ -57,6 +58,9 @@ struct l2q_engine {
     // state
     float *xa, *xb, *q, *att, *wo_out, *hb, *ffn_out, *logits;
     float *kcache, *vcache, *rope, *scores;
+    int8_t *k8, *v8;         // L2Q_ENGINE_KV_INT8: [L][n_kv][max_t][hs]
+    float *ks, *vs;          //   scales [L][n_kv][max_t]
+    float* kvf;              //   the position's rotated k and v rows [2][kv_dim]
     int *meta, *am;
     int* h_meta = nullptr;   // pinned {token, pos} slots
     int h_meta_slots = 0;
@@ -111,10 +115,23 @@ int enqueue_step(l2q_engine* e, hipStream_t st, float* dbg_x, float* dbg_tmp, bo
         qa.meta = e->meta;
         qa.dim = d; qa.kv_dim = kv; qa.hs = e->hs; qa.max_t = e->max_t;
         qa.kcache = kc; qa.vcache = vc; qa.rope = e->rope;
+        const bool kv8 = e->flags & L2Q_ENGINE_KV_INT8;
+        if (kv8) {   // k, v rows to the staging row, then quantized into the int8 cache
+            qa.kcache = e->kvf; qa.vcache = e->kvf + kv; qa.max_t = 1; qa.kv_stage = 1;
+        }
         if ((rc = launch_gemv_fused(bits, G, kNorm, kRopeKV, qa, st))) return rc;
         if (dbg_x && l == 0) HIPCHK(hipMemcpyAsync(dbg_x, e->xb, d * sizeof(float), hipMemcpyDeviceToHost, st), "copy x");
-        rc = launch_attention_exact(e->q, kc, vc, e->att, e->scores, e->S, e->meta, 0, c.n_heads, c.n_kv_heads,
-                                    e->hs, e->max_t, st);
+        if (kv8) {
+            const size_t co = (size_t)l * kv * e->max_t, so = (size_t)l * c.n_kv_heads * e->max_t;
+            rc = launch_kv8_append(e->kvf, e->kvf + kv, e->k8 + co, e->v8 + co, e->ks + so, e->vs + so, nullptr,
+                                   e->meta, 0, c.n_kv_heads, e->hs, e->max_t, st);
+            if (!rc)
+                rc = launch_attention_kv8(e->q, e->k8 + co, e->v8 + co, e->ks + so, e->vs + so, e->att, e->scores,
+                                          e->meta, 0, c.n_heads, c.n_kv_heads, e->hs, e->max_t, st);
+        } else {
+            rc = launch_attention_exact(e->q, kc, vc, e->att, e->scores, e->S, e->meta, 0, c.n_heads,
+                                        c.n_kv_heads, e->hs, e->max_t, st);
+        }
         if (rc) return rc;
         // wo: quantize the attention output in the prologue
         GemvArgs oa{};
@@ -289,8 +306,12 @@ int build(l2q_engine* e, const void* weights, size_t weights_bytes) {
     const size_t o_xa = sa.take(d * 4), o_xb = sa.take(d * 4), o_q = sa.take(d * 4), o_att = sa.take(d * 4);
     const size_t o_wo = sa.take(d * 4), o_hb = sa.take(h * 4), o_ffn = sa.take(d * 4);
     const size_t o_logits = sa.take(V * 4);
-    const size_t kvfloats = L * kv * (size_t)e->max_t;
+    const bool kv8 = e->flags & L2Q_ENGINE_KV_INT8;
+    const size_t kvfloats = kv8 ? 0 : L * kv * (size_t)e->max_t;
     const size_t o_kc = sa.take(kvfloats * 4), o_vc = sa.take(kvfloats * 4);
+    const size_t kv8n = kv8 ? L * kv * (size_t)e->max_t : 0, kv8s = kv8 ? L * (size_t)c.n_kv_heads * e->max_t : 0;
+    const size_t o_k8 = sa.take(kv8n), o_v8 = sa.take(kv8n), o_ks = sa.take(kv8s * 4), o_vs = sa.take(kv8s * 4);
+    const size_t o_kvf = sa.take(kv8 ? 2 * kv * 4 : 0);
     const size_t o_rope = sa.take((size_t)e->max_t * e->hs * 4);
     const size_t o_sc = sa.take((size_t)c.n_heads * e->max_t * 4);
     const size_t o_meta = sa.take(2 * sizeof(int)), o_am = sa.take(sizeof(int));
@@ -302,6 +323,8 @@ int build(l2q_engine* e, const void* weights, size_t weights_bytes) {
     e->logits = (float*)(S_ + o_logits);
     e->kcache = (float*)(S_ + o_kc); e->vcache = (float*)(S_ + o_vc); e->rope = (float*)(S_ + o_rope);
     e->scores = (float*)(S_ + o_sc);
+    e->k8 = (int8_t*)(S_ + o_k8); e->v8 = (int8_t*)(S_ + o_v8);
+    e->ks = (float*)(S_ + o_ks); e->vs = (float*)(S_ + o_vs); e->kvf = (float*)(S_ + o_kvf);
     e->meta = (int*)(S_ + o_meta); e->am = (int*)(S_ + o_am);
     // zero-fill the state (outside any graph) so unused cache rows are defined
     HIPCHK(hipMemsetAsync(e->sarena, 0, e->sbytes, e->stream), "hipMemset(state)");
@@ -346,6 +369,11 @@ extern "C" {
 
 int l2q_engine_create(const l2q_config* cfg, const void* weights, size_t weights_bytes, int wbits, int group,
                       int max_steps, l2q_engine** out) {
+    return l2q_engine_create_ex(cfg, weights, weights_bytes, wbits, group, max_steps, 0, out);
+}
+
+int l2q_engine_create_ex(const l2q_config* cfg, const void* weights, size_t weights_bytes, int wbits, int group,
+                         int max_steps, int flags, l2q_engine** out) {
     if (!cfg || !weights || !out) { set_error("engine: null argument"); return L2Q_ERR_ARG; }
     *out = nullptr;
     const l2q_config& c = *cfg;
@@ -362,8 +390,16 @@ int l2q_engine_create(const l2q_config* cfg, const void* weights, size_t weights
                   c.n_heads, group, wbits);
         return L2Q_ERR_ARG;
     }
+    const int steps = max_steps <= 0 || max_steps > c.seq_len ? c.seq_len : max_steps;
+    if ((flags & ~L2Q_ENGINE_KV_INT8) ||
+        ((flags & L2Q_ENGINE_KV_INT8) && !kv8_shape_ok(c.n_heads, c.n_kv_heads, hs, steps))) {
+        set_error("engine: unsupported flags %d for this shape (int8 KV needs head_size %% 16 == 0, <= 8192 steps)",
+                  flags);
+        return L2Q_ERR_ARG;
+    }
     l2q_engine* e = new (std::nothrow) l2q_engine();
     if (!e) { set_error("engine: out of host memory"); return L2Q_ERR_NOMEM; }
+    e->flags = flags;
     e->cfg = c;
     e->wbits = wbits;
     e->G = group;

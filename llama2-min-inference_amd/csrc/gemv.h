@@ -74,6 +74,7 @@ struct GemvArgs {
     float* kcache;
     float* vcache;
     const float* rope;
+    int kv_stage;            // 1: k/v rows written at position 0 (a staging row, max_t 1)
 };
 
 
@@ -767,16 +768,17 @@ __global__ __launch_bounds__(gemv_waves(NS) * L2Q_WAVE) void k_gemv(GemvArgs a) 
                 const float sk = __shfl(rope_r[k], (hd + 1) & 63);
                 if ((hd >> 6) == k) { c = ck; s = sk; }
             }
+            const int cpos = a.kv_stage ? 0 : pos;
             if (mine && row < a.rows) {
                 const bool odd = row & 1;
                 const float v0 = odd ? other : sum, v1 = odd ? sum : other;
                 if (row < a.dim + a.kv_dim) {            // q or k: rotate
                     const float r = odd ? __builtin_fmaf(v0, s, v1 * c) : __builtin_fmaf(v0, c, -(v1 * s));
                     if (row < a.dim) a.out[row] = r;
-                    else a.kcache[((size_t)(e / a.hs) * a.max_t + pos) * a.hs + (e % a.hs)] = r;
+                    else a.kcache[((size_t)(e / a.hs) * a.max_t + cpos) * a.hs + (e % a.hs)] = r;
                 } else {                                  // v: appended as is
                     const int ev = row - a.dim - a.kv_dim;
-                    a.vcache[((size_t)(ev / a.hs) * a.max_t + pos) * a.hs + (ev % a.hs)] = sum;
+                    a.vcache[((size_t)(ev / a.hs) * a.max_t + cpos) * a.hs + (ev % a.hs)] = sum;
                 }
             }
         } else {   // kSwiglu: (w1, w3) pairs on lanes (0,1), (2,3), ...

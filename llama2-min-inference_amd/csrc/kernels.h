@@ -536,6 +536,155 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn_softmax_v(
     if (wv == 0 && lane < width) out[(size_t)h * hs + d0 + lane] = acc;
 }
 
+// ---------------------------------------------------------------------------
+// int8 KV cache (v5-cuda-fused/run.cu:41-48, INT8_KV): k8 / v8 laid out
+// [n_kv][max_t][hs] int8 with one fp32 scale per (kv head, position),
+// ks / vs [n_kv][max_t].
+
+// Row `pos` of kv head blockIdx.x, k (blockIdx.y == 0, rotated first when a
+// RoPE table is given) or v: amax, s = amax/127 (1e-8 when 0), q =
+// clamp(rint(v/s), -127, 127) with the IEEE quotient
+// (v5-cuda-fused/run.cu:204-249).  One wave; element pairs (2p, 2p+1) on
+// lane p mod 64.
+constexpr int kKv8Pairs = kAttnMaxHs / 2 / L2Q_WAVE;   // pairs per lane (hs <= 256)
+__global__ __launch_bounds__(L2Q_WAVE) void k_kv8_append(
+    const float* __restrict__ k, const float* __restrict__ v, int8_t* __restrict__ k8, int8_t* __restrict__ v8,
+    float* __restrict__ ks, float* __restrict__ vs, const float* __restrict__ rope, const int* __restrict__ meta,
+    int pos_arg, int hs, int max_t) {
+    const int g = blockIdx.x, isv = blockIdx.y, lane = threadIdx.x;
+    const int pos = meta_pos(meta, pos_arg);
+    const float* src = (isv ? v : k) + (size_t)g * hs;
+    float2 val[kKv8Pairs];
+    float amax = 0.0f;
+#pragma unroll
+    for (int i = 0; i < kKv8Pairs; i++) {
+        const int p = lane + L2Q_WAVE * i;
+        val[i] = make_float2(0.0f, 0.0f);
+        if (2 * p < hs) {
+            float2 x = reinterpret_cast<const float2*>(src)[p];
+            if (!isv && rope) {   // the fp32 path's rotation (RoPE table of the position)
+                const float c = rope[(size_t)pos * hs + 2 * p], s = rope[(size_t)pos * hs + 2 * p + 1];
+                x = make_float2(__builtin_fmaf(x.x, c, -(x.y * s)), __builtin_fmaf(x.x, s, x.y * c));
+            }
+            val[i] = x;
+            amax = fmaxf(amax, fmaxf(fabsf(x.x), fabsf(x.y)));
+        }
+    }
+    amax = group_max<L2Q_WAVE>(amax);
+    float sc = amax / 127.0f;
+    if (sc == 0.0f) sc = 1e-8f;
+    int8_t* dst = (isv ? v8 : k8) + ((size_t)g * max_t + pos) * hs;
+#pragma unroll
+    for (int i = 0; i < kKv8Pairs; i++) {
+        const int p = lane + L2Q_WAVE * i;
+        if (2 * p < hs) {
+            const int q0 = q8_value(val[i].x, sc), q1 = q8_value(val[i].y, sc);
+            *reinterpret_cast<uint16_t*>(dst + 2 * p) = (uint16_t)((q0 & 0xff) | ((q1 & 0xff) << 8));
+        }
+    }
+    if (lane == 0) (isv ? vs : ks)[(size_t)g * max_t + pos] = sc;
+}
+
+// Scores over the int8 cache (v5-cuda-fused/run.cu:362-371): score_t =
+// (q . k8_t) / sqrt(hs) * ks_t.  Four lanes per position, each summing the
+// 4-element chunks c = 4*sub + 16*i with FMAs, then a two-step butterfly;
+// 64 positions per workgroup item.  Needs hs % 16 == 0.
+constexpr int kA8Pos = 64;
+constexpr int kA8GridMax = 2048;
+__device__ __forceinline__ float sbyte(int w, int b) { return (float)((w << (24 - 8 * b)) >> 24); }
+__global__ __launch_bounds__(kAttnThreads) void k_attn8_scores(
+    const float* __restrict__ q, const int8_t* __restrict__ k8, const float* __restrict__ ks,
+    float* __restrict__ scores, const int* __restrict__ meta, int pos_arg, int kv_mul, int n_heads, int hs,
+    int max_t) {
+    const int tid = threadIdx.x, sub = tid & 3;
+    const int pos = meta_pos(meta, pos_arg);
+    const int n = pos + 1;
+    const int ntile = (n + kA8Pos - 1) / kA8Pos;
+    const float rs = sqrtf((float)hs);
+    for (int item = blockIdx.x; item < n_heads * ntile; item += gridDim.x) {
+        const int h = item / ntile;
+        const int t = (item - h * ntile) * kA8Pos + tid / 4;
+        const int hk = h / kv_mul;
+        const int tc = min(t, n - 1);
+        const int8_t* kr = k8 + ((size_t)hk * max_t + tc) * hs;
+        const float* qh = q + (size_t)h * hs;
+        float acc = 0.0f;
+        for (int c = 4 * sub; c < hs; c += 16) {
+            const int w = *reinterpret_cast<const int*>(kr + c);
+            const float4 qq = *reinterpret_cast<const float4*>(qh + c);
+            acc = __builtin_fmaf(qq.x, sbyte(w, 0), acc);
+            acc = __builtin_fmaf(qq.y, sbyte(w, 1), acc);
+            acc = __builtin_fmaf(qq.z, sbyte(w, 2), acc);
+            acc = __builtin_fmaf(qq.w, sbyte(w, 3), acc);
+        }
+        acc += __shfl_xor(acc, 1);
+        acc += __shfl_xor(acc, 2);
+        if (sub == 0 && t < n) scores[(size_t)h * max_t + t] = acc / rs * ks[(size_t)hk * max_t + t];
+    }
+}
+
+// Softmax and p*V over the int8 cache (v5-cuda-fused/run.cu:373-398), one
+// workgroup per head: max and sum as block reductions, e_t * vs_t kept in
+// LDS, then thread (slice, g) accumulates elements 4g..4g+3 over positions
+// t = slice (mod slices); the slices are added in LDS in slice order and
+// divided by the sum.  Every reduction has a fixed order (restated by the
+// oracle's orc_attention_kv8_ordered), so results are reproducible bit for
+// bit.  Needs hs % 4 == 0.
+__host__ __device__ constexpr size_t attn8_v_lds_bytes(int max_t) {
+    return ((size_t)(max_t + 3) / 4 * 4 + 4 * kAttnThreads + 16) * sizeof(float);
+}
+__global__ __launch_bounds__(kAttnThreads) void k_attn8_softmax_v(
+    const float* __restrict__ scores, const int8_t* __restrict__ v8, const float* __restrict__ vs,
+    float* __restrict__ out, const int* __restrict__ meta, int pos_arg, int kv_mul, int hs, int max_t) {
+    extern __shared__ __attribute__((aligned(16))) float sm8[];
+    float* pe = sm8;                                   // [max_t] e_t * vs_t
+    float* part = pe + (max_t + 3) / 4 * 4;            // [slices][hs] partial sums
+    float* red = part + 4 * kAttnThreads;              // [8] block reductions
+    const int h = blockIdx.x, hk = h / kv_mul;
+    const int tid = threadIdx.x, lane = tid & (L2Q_WAVE - 1), wv = tid / L2Q_WAVE;
+    const int pos = meta_pos(meta, pos_arg);
+    const int n = pos + 1;
+    const float* sc = scores + (size_t)h * max_t;
+    float m = -INFINITY;
+    for (int t = tid; t < n; t += kAttnThreads) m = fmaxf(m, sc[t]);
+    m = group_max<L2Q_WAVE>(m);
+    if (lane == 0) red[wv] = m;
+    __syncthreads();
+    m = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+    float sum = 0.0f;
+    for (int t = tid; t < n; t += kAttnThreads) {
+        const float e = exp_runq(sc[t] - m);   // the host C library's expf, bit for bit
+        sum += e;
+        pe[t] = e * vs[(size_t)hk * max_t + t];
+    }
+    for (int o = 32; o > 0; o >>= 1) sum += __shfl_xor(sum, o);
+    if (lane == 0) red[4 + wv] = sum;
+    __syncthreads();
+    sum = (red[4] + red[5]) + (red[6] + red[7]);
+    const int groups = hs / 4, slices = kAttnThreads / groups;
+    const int gi = tid % groups, slice = tid / groups;
+    float4 acc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    if (slice < slices) {
+        const int8_t* vb = v8 + (size_t)hk * max_t * hs + 4 * gi;
+#pragma unroll 8
+        for (int t = slice; t < n; t += slices) {
+            const int w = *reinterpret_cast<const int*>(vb + (size_t)t * hs);
+            const float p = pe[t];
+            acc.x = __builtin_fmaf(p, sbyte(w, 0), acc.x);
+            acc.y = __builtin_fmaf(p, sbyte(w, 1), acc.y);
+            acc.z = __builtin_fmaf(p, sbyte(w, 2), acc.z);
+            acc.w = __builtin_fmaf(p, sbyte(w, 3), acc.w);
+        }
+        *reinterpret_cast<float4*>(part + (size_t)slice * hs + 4 * gi) = acc;
+    }
+    __syncthreads();
+    for (int d = tid; d < hs; d += kAttnThreads) {
+        float s = 0.0f;
+        for (int sl = 0; sl < slices; sl++) s += part[(size_t)sl * hs + d];
+        out[(size_t)h * hs + d] = s / sum;
+    }
+}
+
 // Merge the S partials of each head: out = sum_s e^(m_s-M) o_s / sum_s e^(m_s-M) l_s.
 __global__ __launch_bounds__(256) void k_attn_combine(const float* __restrict__ part_o,
                                                       const float* __restrict__ part_ml,

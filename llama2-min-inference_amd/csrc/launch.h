@@ -47,6 +47,15 @@ int launch_attention_exact(const float* q, const float* kcache, const float* vca
                            hipStream_t st);
 bool attention_exact_ok(int max_t);
 
+// int8 KV cache: append one position / attention over positions 0..pos.
+bool kv8_shape_ok(int n_heads, int n_kv_heads, int hs, int max_t);
+int launch_kv8_append(const float* k, const float* v, int8_t* k8, int8_t* v8, float* ks, float* vs,
+                      const float* rope, const int* meta, int pos, int n_kv_heads, int hs, int max_t,
+                      hipStream_t st);
+int launch_attention_kv8(const float* q, const int8_t* k8, const int8_t* v8, const float* ks, const float* vs,
+                         float* out, float* scores, const int* meta, int pos, int n_heads, int n_kv_heads, int hs,
+                         int max_t, hipStream_t st);
+
 // Score workgroups for n positions: ~128 positions each, at most 64.
 inline int score_splits(int n) {
     const int S = (n + 127) / 128;

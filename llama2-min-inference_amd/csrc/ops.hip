@@ -252,6 +252,43 @@ int launch_attention_exact(const float* q, const float* kcache, const float* vca
     return check_launch("attention_softmax_v");
 }
 
+bool kv8_shape_ok(int n_heads, int n_kv_heads, int hs, int max_t) {
+    return attention_shape_ok(n_heads, n_kv_heads, hs) && hs % 16 == 0 && max_t > 0 && max_t <= 8192;
+}
+
+int launch_kv8_append(const float* k, const float* v, int8_t* k8, int8_t* v8, float* ks, float* vs,
+                      const float* rope, const int* meta, int pos, int n_kv_heads, int hs, int max_t,
+                      hipStream_t st) {
+    if (!kv8_shape_ok(n_kv_heads, n_kv_heads, hs, max_t) || (!meta && (pos < 0 || pos >= max_t)) || !k || !v ||
+        !k8 || !v8 || !ks || !vs) {
+        set_error("kv8 append: bad arguments kv_heads=%d hs=%d pos=%d max_t=%d", n_kv_heads, hs, pos, max_t);
+        return L2Q_ERR_ARG;
+    }
+    hipLaunchKernelGGL(k_kv8_append, dim3(n_kv_heads, 2), dim3(L2Q_WAVE), 0, st, k, v, k8, v8, ks, vs, rope, meta,
+                       pos, hs, max_t);
+    return check_launch("kv8_append");
+}
+
+int launch_attention_kv8(const float* q, const int8_t* k8, const int8_t* v8, const float* ks, const float* vs,
+                         float* out, float* scores, const int* meta, int pos, int n_heads, int n_kv_heads, int hs,
+                         int max_t, hipStream_t st) {
+    if (!kv8_shape_ok(n_heads, n_kv_heads, hs, max_t) || (!meta && (pos < 0 || pos >= max_t))) {
+        set_error("attention kv8: bad shape heads=%d kv_heads=%d hs=%d pos=%d max_t=%d", n_heads, n_kv_heads, hs,
+                  pos, max_t);
+        return L2Q_ERR_ARG;
+    }
+    const int kv_mul = n_heads / n_kv_heads;
+    // a captured graph covers every position the cache can hold
+    const int items = n_heads * (((meta ? max_t : pos + 1) + kA8Pos - 1) / kA8Pos);
+    hipLaunchKernelGGL(k_attn8_scores, dim3(items < kA8GridMax ? items : kA8GridMax), dim3(kAttnThreads), 0, st, q,
+                       k8, ks, scores, meta, pos, kv_mul, n_heads, hs, max_t);
+    int rc = check_launch("attention_kv8_scores");
+    if (rc) return rc;
+    hipLaunchKernelGGL(k_attn8_softmax_v, dim3(n_heads), dim3(kAttnThreads), attn8_v_lds_bytes(max_t), st, scores,
+                       v8, vs, out, meta, pos, kv_mul, hs, max_t);
+    return check_launch("attention_kv8_softmax_v");
+}
+
 int launch_argmax(const float* v, int n, int* out, hipStream_t st) {
     if (n <= 0) { set_error("argmax: n=%d", n); return L2Q_ERR_ARG; }
     hipLaunchKernelGGL(k_argmax, dim3(1), dim3(1024), 0, st, v, n, out);
@@ -374,6 +411,27 @@ int l2q_attention(const float* q, const float* kcache, const float* vcache, floa
     if (rc) return rc;
     return launch_attention_exact(q, kcache, vcache, out, scratch, score_splits(pos + 1), nullptr, pos, n_heads,
                                   n_kv_heads, head_size, max_t, (hipStream_t)stream);
+}
+
+int l2q_kv8_append(const float* k, const float* v, int8_t* kcache8, int8_t* vcache8, float* kscale, float* vscale,
+                   const float* rope, int pos, int n_kv_heads, int head_size, int max_t, void* stream) {
+    return launch_kv8_append(k, v, kcache8, vcache8, kscale, vscale, rope, nullptr, pos, n_kv_heads, head_size, max_t,
+                             (hipStream_t)stream);
+}
+
+int l2q_attention_kv8(const float* q, const int8_t* kcache8, const int8_t* vcache8, const float* kscale,
+                      const float* vscale, float* out, int pos, int n_heads, int n_kv_heads, int head_size, int max_t,
+                      void* stream) {
+    if (!kv8_shape_ok(n_heads, n_kv_heads, head_size, max_t) || pos < 0 || pos >= max_t) {
+        set_error("attention kv8: bad shape heads=%d kv_heads=%d hs=%d pos=%d max_t=%d", n_heads, n_kv_heads,
+                  head_size, pos, max_t);
+        return L2Q_ERR_ARG;
+    }
+    float* scratch = nullptr;
+    int rc = attn_scratch((size_t)n_heads * max_t, &scratch);
+    if (rc) return rc;
+    return launch_attention_kv8(q, kcache8, vcache8, kscale, vscale, out, scratch, nullptr, pos, n_heads, n_kv_heads,
+                                head_size, max_t, (hipStream_t)stream);
 }
 
 int l2q_attention_split(const float* q, const float* kcache, const float* vcache, float* out, int pos, int n_heads,

@@ -142,6 +142,7 @@ static void usage(void) {
     fprintf(stderr, "  -z <string> optional path to custom tokenizer\n");
     fprintf(stderr, "  -m <string> mode: generate|chat, default: generate\n");
     fprintf(stderr, "  -y <string> (optional) system prompt in chat mode\n");
+    fprintf(stderr, "  -k <int>    KV cache element bits: 32 (default) or 8 (the reference's INT8_KV build)\n");
     exit(EXIT_FAILURE);
 }
 
@@ -154,6 +155,7 @@ int main(int argc, char** argv) {
     unsigned long long seed = 0;
     const char* mode = "generate";
     const char* system_prompt = NULL;
+    int kv_bits = 32;
 
     if (argc >= 2) ckpt = argv[1]; else usage();
     for (int i = 2; i < argc; i += 2) {
@@ -167,6 +169,7 @@ int main(int argc, char** argv) {
             case 'z': tok_path = argv[i + 1]; break;
             case 'm': mode = argv[i + 1]; break;
             case 'y': system_prompt = argv[i + 1]; break;
+            case 'k': kv_bits = atoi(argv[i + 1]); break;
             default: usage();
         }
     }
@@ -174,6 +177,7 @@ int main(int argc, char** argv) {
     if (temperature < 0.0f) temperature = 0.0f;
     if (topp < 0.0f || 1.0f < topp) topp = 0.9f;
     if (steps < 0) steps = 0;
+    if (kv_bits != 32 && kv_bits != 8) usage();
 
     char err[256];
     qll_file f;
@@ -182,8 +186,8 @@ int main(int argc, char** argv) {
     if (steps == 0 || steps > f.h.cfg.seq_len) steps = f.h.cfg.seq_len;
 
     l2q_engine* engine = NULL;
-    if (l2q_engine_create(&f.h.cfg, f.weights, f.weights_bytes, f.h.wbits, f.h.group, steps,
-                          &engine) != L2Q_OK)
+    if (l2q_engine_create_ex(&f.h.cfg, f.weights, f.weights_bytes, f.h.wbits, f.h.group, steps,
+                             kv_bits == 8 ? L2Q_ENGINE_KV_INT8 : 0, &engine) != L2Q_OK)
         die("engine init failed", l2q_last_error());
     qll_close(&f);   /* the engine holds device copies of every tensor */
 

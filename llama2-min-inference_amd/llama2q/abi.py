@@ -15,6 +15,7 @@ L2Q_ERR_HIP = -2
 L2Q_ERR_FORMAT = -3
 L2Q_ERR_NOMEM = -4
 L2Q_ERR_STATE = -5
+L2Q_ENGINE_KV_INT8 = 1
 
 
 class L2QError(RuntimeError):
@@ -38,6 +39,7 @@ SIGNATURES = {
     "l2q_last_error": (C.c_char_p, []),
     "l2q_device_count": (I, []),
     "l2q_engine_create": (I, [C.POINTER(Config), P, C.c_size_t, I, I, I, C.POINTER(P)]),
+    "l2q_engine_create_ex": (I, [C.POINTER(Config), P, C.c_size_t, I, I, I, I, C.POINTER(P)]),
     "l2q_engine_forward": (I, [P, I, I, P]),
     "l2q_engine_forward_argmax": (I, [P, I, I, C.POINTER(I)]),
     "l2q_engine_forward_debug": (I, [P, I, I, P, P]),
@@ -53,6 +55,8 @@ SIGNATURES = {
     "l2q_rope_kv_append": (I, [P, P, P, P, P, P, I, I, I, I, I, P]),
     "l2q_attention": (I, [P, P, P, P, I, I, I, I, I, P]),
     "l2q_attention_split": (I, [P, P, P, P, I, I, I, I, I, P]),
+    "l2q_kv8_append": (I, [P, P, P, P, P, P, P, I, I, I, I, P]),
+    "l2q_attention_kv8": (I, [P, P, P, P, P, P, I, I, I, I, I, P]),
     "l2q_expf": (I, [P, P, C.c_size_t, P]),
     "l2q_rope_table": (None, [P, I, I]),
 }

@@ -12,15 +12,16 @@ from .host import Checkpoint
 
 
 class Engine:
-    def __init__(self, ckpt: Checkpoint, max_steps: int = 0):
+    def __init__(self, ckpt: Checkpoint, max_steps: int = 0, kv8: bool = False):
+        """kv8: int8 KV cache (L2Q_ENGINE_KV_INT8, the reference's INT8_KV build)."""
         if ckpt.header.shared_weights:
             raise ValueError("shared weights not supported")   # runq.c:247-251
         self.cfg = ckpt.cfg
         self.vocab = self.cfg.vocab_size
         w = ckpt.weights
         h = C.c_void_p()
-        abi.call("l2q_engine_create", C.byref(self.cfg), w.ctypes.data, w.nbytes, ckpt.wbits, ckpt.group,
-                 max_steps, C.byref(h))
+        abi.call("l2q_engine_create_ex", C.byref(self.cfg), w.ctypes.data, w.nbytes, ckpt.wbits, ckpt.group,
+                 max_steps, abi.L2Q_ENGINE_KV_INT8 if kv8 else 0, C.byref(h))
         self._h = h
         self.max_steps = max_steps if 0 < max_steps <= self.cfg.seq_len else self.cfg.seq_len
         self._logits = np.empty(self.vocab, dtype=np.float32)

@@ -150,6 +150,9 @@ struct orc_model {
     const float* rms_final;
     orc_qmat wq, wk, wv, wo, w1, w2, w3, wcls;
     float *x, *xb, *xb2, *hb, *hb2, *q, *att, *logits, *kcache, *vcache;
+    int kv8;                          /* 1: int8 KV cache (orc_model_set_kv8) */
+    int8_t *k8, *v8;                  /* [L][max_t][kv_dim] */
+    float *ks, *vs;                   /* [L][max_t][n_kv_heads] */
     int8_t* xq;
     float *xs, *xt;
 };
@@ -207,6 +210,7 @@ void orc_model_free(orc_model* m) {
     if (!m) return;
     free(m->x); free(m->xb); free(m->xb2); free(m->hb); free(m->hb2); free(m->q);
     free(m->att); free(m->logits); free(m->kcache); free(m->vcache);
+    free(m->k8); free(m->v8); free(m->ks); free(m->vs);
     free(m->xq); free(m->xs); free(m->xt);
     free(m);
 }
@@ -275,6 +279,143 @@ void orc_attention(const float* q, const float* kc, const float* vc, float* out,
     }
 }
 
+/* One kv head's row of the int8 KV cache, v5-cuda-fused/run.cu:204-249
+ * (kv_quant_kernel): amax over the row, s = amax/127 (1e-8 when 0),
+ * q = clamp(rint(v/s), -127, 127) (__float2int_rn of the quotient). */
+void orc_kv_quant(const float* row, int hs, int8_t* q, float* s) {
+    float amax = 0.0f;
+    for (int i = 0; i < hs; i++) { float a = fabsf(row[i]); if (a > amax) amax = a; }
+    float sc = amax / 127.0f;
+    if (sc == 0.0f) sc = 1e-8f;
+    for (int i = 0; i < hs; i++) {
+        float r = rintf(row[i] / sc);
+        r = r > 127.0f ? 127.0f : (r < -127.0f ? -127.0f : r);
+        q[i] = (int8_t)r;
+    }
+    *s = sc;
+}
+
+/* Attention over the int8 cache, v5-cuda-fused/run.cu:350-410
+ * (attention_cache_kernel): score_t = (q . k8_t) / sqrt(hs) * ks_t,
+ * softmax over t <= pos, out = sum_t p_t * vs_t * v8_t.  Evaluated in double
+ * (the reference's float order is a warp reduction; this is the value every
+ * order approximates).  Row t of kv head g: kc + g*head_stride + t*t_stride;
+ * its scale: ks[t*s_t_stride + g*s_head_stride]. */
+void orc_attention_kv8(const float* q, const int8_t* kc, const int8_t* vc, const float* ks, const float* vs,
+                       float* out, int pos, int n_heads, int n_kv_heads, int hs, size_t t_stride,
+                       size_t head_stride, size_t s_t_stride, size_t s_head_stride) {
+    const int kv_mul = n_heads / n_kv_heads;
+    const double rs = sqrt((double)hs);
+    double* sc = (double*)malloc((size_t)(pos + 1) * sizeof(double));
+    double* acc = (double*)malloc((size_t)hs * sizeof(double));
+    for (int h = 0; h < n_heads; h++) {
+        const int g = h / kv_mul;
+        const float* qh = q + (size_t)h * hs;
+        double m = -INFINITY;
+        for (int t = 0; t <= pos; t++) {
+            const int8_t* kt = kc + (size_t)g * head_stride + (size_t)t * t_stride;
+            double d = 0.0;
+            for (int i = 0; i < hs; i++) d += (double)qh[i] * (double)kt[i];
+            sc[t] = d / rs * (double)ks[(size_t)t * s_t_stride + (size_t)g * s_head_stride];
+            if (sc[t] > m) m = sc[t];
+        }
+        double sum = 0.0;
+        for (int t = 0; t <= pos; t++) { sc[t] = exp(sc[t] - m); sum += sc[t]; }
+        for (int i = 0; i < hs; i++) acc[i] = 0.0;
+        for (int t = 0; t <= pos; t++) {
+            const int8_t* vt = vc + (size_t)g * head_stride + (size_t)t * t_stride;
+            const double w = sc[t] * (double)vs[(size_t)t * s_t_stride + (size_t)g * s_head_stride];
+            for (int i = 0; i < hs; i++) acc[i] += w * (double)vt[i];
+        }
+        for (int i = 0; i < hs; i++) out[(size_t)h * hs + i] = (float)(acc[i] / sum);
+    }
+    free(sc);
+    free(acc);
+}
+
+/* The same attention in the float order of this build's GPU kernels
+ * (k_attn8_scores / k_attn8_softmax_v), so that the int8-KV decode can be
+ * compared bit for bit; pinned to orc_attention_kv8 (double) by the tests.
+ *   score_t: four partial FMA chains, chain j over the 4-element chunks
+ *            c = 4j + 16i in order, combined as (a0+a1)+(a2+a3); then
+ *            (dot / sqrtf(hs)) * ks_t
+ *   sum:     256 partial sums (thread j: t = j, j+256, ...), each wave's 64
+ *            combined by the xor butterfly 32,16,...,1, the four waves as
+ *            (w0+w1)+(w2+w3); e_t = expf(score_t - max)
+ *   out[d]:  S = 256/(hs/4) slices, slice s: fma(e_t*vs_t, v8_t[d], acc)
+ *            over t = s, s+S, ...; out = (((0+p_0)+p_1)+...+p_{S-1}) / sum */
+static float butterfly64(float* v) {
+    for (int o = 32; o > 0; o >>= 1) {
+        float w[64];
+        for (int l = 0; l < 64; l++) w[l] = v[l] + v[l ^ o];
+        memcpy(v, w, sizeof w);
+    }
+    return v[0];
+}
+
+void orc_attention_kv8_ordered(const float* q, const int8_t* kc, const int8_t* vc, const float* ks,
+                               const float* vs, float* out, int pos, int n_heads, int n_kv_heads, int hs,
+                               size_t t_stride, size_t head_stride, size_t s_t_stride, size_t s_head_stride) {
+    const int kv_mul = n_heads / n_kv_heads, n = pos + 1;
+    const float rs = sqrtf((float)hs);
+    float* sc = (float*)malloc((size_t)n * sizeof(float));
+    float* pe = (float*)malloc((size_t)n * sizeof(float));
+    for (int h = 0; h < n_heads; h++) {
+        const int g = h / kv_mul;
+        const float* qh = q + (size_t)h * hs;
+        float m = -INFINITY;
+        for (int t = 0; t < n; t++) {
+            const int8_t* kt = kc + (size_t)g * head_stride + (size_t)t * t_stride;
+            float a[4];
+            for (int j = 0; j < 4; j++) {
+                a[j] = 0.0f;
+                for (int c = 4 * j; c < hs; c += 16)
+                    for (int e = 0; e < 4; e++) a[j] = fmaf(qh[c + e], (float)kt[c + e], a[j]);
+            }
+            const float dot = (a[0] + a[1]) + (a[2] + a[3]);
+            sc[t] = dot / rs * ks[(size_t)t * s_t_stride + (size_t)g * s_head_stride];
+            m = fmaxf(m, sc[t]);
+        }
+        float part[256], wsum[4];
+        for (int j = 0; j < 256; j++) {
+            part[j] = 0.0f;
+            for (int t = j; t < n; t += 256) {
+                const float e = expf(sc[t] - m);
+                part[j] = part[j] + e;
+                pe[t] = e * vs[(size_t)t * s_t_stride + (size_t)g * s_head_stride];
+            }
+        }
+        for (int w = 0; w < 4; w++) wsum[w] = butterfly64(part + 64 * w);
+        const float sum = (wsum[0] + wsum[1]) + (wsum[2] + wsum[3]);
+        const int groups = hs / 4, slices = 256 / groups;
+        for (int d = 0; d < hs; d++) {
+            float s = 0.0f;
+            for (int sl = 0; sl < slices; sl++) {
+                float acc = 0.0f;
+                for (int t = sl; t < n; t += slices)
+                    acc = fmaf(pe[t], (float)vc[(size_t)g * head_stride + (size_t)t * t_stride + d], acc);
+                s = s + acc;
+            }
+            out[(size_t)h * hs + d] = s / sum;
+        }
+    }
+    free(sc);
+    free(pe);
+}
+
+int orc_model_set_kv8(orc_model* m, int on) {
+    if (!on) { m->kv8 = 0; return 0; }
+    const size_t n = (size_t)m->n_layers * m->max_t * m->kv_dim;
+    const size_t ns = (size_t)m->n_layers * m->max_t * m->n_kv_heads;
+    if (!m->k8) {
+        m->k8 = calloc(n, 1); m->v8 = calloc(n, 1);
+        m->ks = calloc(ns, 4); m->vs = calloc(ns, 4);
+        if (!m->k8 || !m->v8 || !m->ks || !m->vs) return -1;
+    }
+    m->kv8 = 1;
+    return 0;
+}
+
 /* SwiGLU, runq.c:405-410: out = (h * (1/(1+expf(-h)))) * h2. */
 void orc_swiglu(float* out, const float* h, const float* h2, int n) {
     for (int i = 0; i < n; i++) {
@@ -305,8 +446,22 @@ const float* orc_forward(orc_model* m, int token, int pos, float* x_layers) {
 
         orc_rope(m->q, k, pos, dim, kv_dim, hs);
 
-        orc_attention(m->q, m->kcache + loff, m->vcache + loff, m->xb, pos, m->n_heads,
-                      m->n_kv_heads, hs, (size_t)kv_dim, (size_t)hs, m->att, m->max_t);
+        if (m->kv8) {
+            /* v5-cuda-fused/run.cu:627-631: the rotated k and the v row of
+             * this position go into the int8 cache, one scale per kv head */
+            const size_t soff = (size_t)l * m->max_t * m->n_kv_heads + (size_t)pos * m->n_kv_heads;
+            for (int g = 0; g < m->n_kv_heads; g++) {
+                orc_kv_quant(k + (size_t)g * hs, hs, m->k8 + loff + (size_t)pos * kv_dim + (size_t)g * hs, m->ks + soff + g);
+                orc_kv_quant(v + (size_t)g * hs, hs, m->v8 + loff + (size_t)pos * kv_dim + (size_t)g * hs, m->vs + soff + g);
+            }
+            const size_t sl = (size_t)l * m->max_t * m->n_kv_heads;
+            orc_attention_kv8_ordered(m->q, m->k8 + loff, m->v8 + loff, m->ks + sl, m->vs + sl, m->xb, pos,
+                                      m->n_heads, m->n_kv_heads, hs, (size_t)kv_dim, (size_t)hs,
+                                      (size_t)m->n_kv_heads, 1);
+        } else {
+            orc_attention(m->q, m->kcache + loff, m->vcache + loff, m->xb, pos, m->n_heads,
+                          m->n_kv_heads, hs, (size_t)kv_dim, (size_t)hs, m->att, m->max_t);
+        }
 
         orc_quantize_act(m->xb, dim, G, m->xq, m->xs, m->xt);
         matmul(m, m->xb2, m->wo, l, dim, dim);

@@ -16,6 +16,10 @@
  *   orc_softmax        runq.c:307-318
  *   orc_rope           runq.c:351-365
  *   orc_attention      runq.c:367-391
+ *   orc_kv_quant       v5-cuda-fused/run.cu:204-249 (int8 KV cache row)
+ *   orc_attention_kv8  v5-cuda-fused/run.cu:350-410 (attention over it; in
+ *                      double, the value every float order approximates)
+ *   orc_attention_kv8_ordered  the same in the GPU kernels' float order
  *   orc_swiglu         runq.c:405-410
  *   orc_forward        runq.c:320-421
  * Floating-point contraction follows a GCC -O3 -march=native build of
@@ -58,6 +62,23 @@ void orc_attention(const float* q, const float* kc, const float* vc, float* out,
                    int n_heads, int n_kv_heads, int hs, size_t t_stride, size_t head_stride,
                    float* att_scratch, int att_stride);
 
+/* One kv head's int8 cache row and its scale (v5-cuda-fused/run.cu:
+ * 204-249). */
+void orc_kv_quant(const float* row, int hs, int8_t* q, float* s);
+
+/* Attention over an int8 KV cache (v5-cuda-fused/run.cu:350-410), in
+ * double: row t of kv head g at kc + g*head_stride + t*t_stride, its scale
+ * at ks[t*s_t_stride + g*s_head_stride]. */
+void orc_attention_kv8(const float* q, const int8_t* kc, const int8_t* vc, const float* ks, const float* vs,
+                       float* out, int pos, int n_heads, int n_kv_heads, int hs, size_t t_stride,
+                       size_t head_stride, size_t s_t_stride, size_t s_head_stride);
+
+/* orc_attention_kv8 in the float order of this build's GPU kernels (see
+ * oracle.c), for bit-exact comparison; same arguments. */
+void orc_attention_kv8_ordered(const float* q, const int8_t* kc, const int8_t* vc, const float* ks,
+                               const float* vs, float* out, int pos, int n_heads, int n_kv_heads, int hs,
+                               size_t t_stride, size_t head_stride, size_t s_t_stride, size_t s_head_stride);
+
 /* SwiGLU (runq.c:405-410); out may alias h. */
 void orc_swiglu(float* out, const float* h, const float* h2, int n);
 
@@ -70,6 +91,12 @@ typedef struct orc_model orc_model;
 orc_model* orc_model_create(const int cfg[7], const void* weights, size_t bytes,
                             int wbits, int group, int max_t);
 void orc_model_free(orc_model* m);
+
+/* Switch the model to the int8 KV cache (v5-cuda-fused/run.cu:41-48,
+ * INT8_KV=1): each position's rotated k and v rows are stored through
+ * orc_kv_quant and attention runs through orc_attention_kv8.  Returns 0, or
+ * -1 when the caches cannot be allocated. */
+int orc_model_set_kv8(orc_model* m, int on);
 
 /* forward(token, pos) -> logits[vocab] (owned by the model).  If x_layers
  * is not NULL it receives the residual stream after the embedding and after

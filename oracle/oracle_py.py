@@ -49,6 +49,10 @@ def olib():
             "orc_attention": (None, [P, P, P, P, I, I, I, I, C.c_size_t, C.c_size_t, P, I]),
             "orc_swiglu": (None, [P, P, P, I]),
             "orc_expf_array": (None, [P, P, C.c_size_t]),
+            "orc_kv_quant": (None, [P, I, P, P]),
+            "orc_attention_kv8": (None, [P, P, P, P, P, P, I, I, I, I] + [C.c_size_t] * 4),
+            "orc_model_set_kv8": (I, [P, I]),
+            "orc_attention_kv8_ordered": (None, [P, P, P, P, P, P, I, I, I, I] + [C.c_size_t] * 4),
         }
         for n, (r, a) in sig.items():
             f = getattr(L, n)
@@ -122,6 +126,33 @@ def attention(q: np.ndarray, kcache: np.ndarray, vcache: np.ndarray, pos: int, n
     return out
 
 
+def kv_quant(row: np.ndarray):
+    """(int8 row, scale) of one kv head (v5-cuda-fused/run.cu:204-249)."""
+    row = np.ascontiguousarray(row, dtype=np.float32)
+    q = np.empty(row.size, dtype=np.int8)
+    s = np.empty(1, dtype=np.float32)
+    olib().orc_kv_quant(_p(row), row.size, _p(q), _p(s))
+    return q, np.float32(s[0])
+
+
+def attention_kv8(q: np.ndarray, k8: np.ndarray, v8: np.ndarray, ks: np.ndarray, vs: np.ndarray, pos: int,
+                  n_heads: int, n_kv_heads: int, head_size: int, ordered: bool = False) -> np.ndarray:
+    """v5-cuda-fused/run.cu:350-410 (in double, or with ordered=True in the
+    GPU kernels' float order) over int8 caches laid out
+    [n_kv_heads][max_t][head_size] with scales [n_kv_heads][max_t]."""
+    q = np.ascontiguousarray(q, dtype=np.float32)
+    k8 = np.ascontiguousarray(k8, dtype=np.int8)
+    v8 = np.ascontiguousarray(v8, dtype=np.int8)
+    ks = np.ascontiguousarray(ks, dtype=np.float32)
+    vs = np.ascontiguousarray(vs, dtype=np.float32)
+    max_t = k8.shape[1]
+    out = np.empty(n_heads * head_size, dtype=np.float32)
+    fn = olib().orc_attention_kv8_ordered if ordered else olib().orc_attention_kv8
+    fn(_p(q), _p(k8), _p(v8), _p(ks), _p(vs), _p(out), pos, n_heads, n_kv_heads, head_size,
+       head_size, max_t * head_size, 1, max_t)
+    return out
+
+
 def swiglu(h: np.ndarray, h2: np.ndarray) -> np.ndarray:
     h = np.ascontiguousarray(h, dtype=np.float32)
     h2 = np.ascontiguousarray(h2, dtype=np.float32)
@@ -141,7 +172,7 @@ def expf_host(x: np.ndarray) -> np.ndarray:
 class Oracle:
     """CPU restatement of forward() over a checkpoint image (host memory)."""
 
-    def __init__(self, cfg_list, weights: np.ndarray, wbits: int, group: int, max_t: int = 0):
+    def __init__(self, cfg_list, weights: np.ndarray, wbits: int, group: int, max_t: int = 0, kv8: bool = False):
         self.cfg = list(cfg_list)
         self.dim, self.n_layers, self.vocab = self.cfg[0], self.cfg[2], self.cfg[5]
         self._w = weights   # keep the buffer alive
@@ -149,6 +180,8 @@ class Oracle:
         self._m = olib().orc_model_create(arr, _p(weights), weights.nbytes, wbits, group, max_t)
         if not self._m:
             raise ValueError("oracle: weights image too short for the config")
+        if kv8 and olib().orc_model_set_kv8(self._m, 1) != 0:
+            raise MemoryError("oracle: int8 KV cache")
 
     def forward(self, token: int, pos: int, layers: bool = False):
         xl = np.empty((self.n_layers + 1, self.dim), dtype=np.float32) if layers else None
