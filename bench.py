@@ -94,6 +94,45 @@ def time_gemv(torch, abi, rows, cols, bits, group, min_bytes=1 << 30, reps=20):
     return ms, n
 
 
+def time_attention(torch, abi, host, ctx, kv8, reps=50, n_heads=32, hs=128, max_t=4096):
+    """Mean duration (ms) of one layer's decode attention at context ctx
+    (32 heads x 128, cache of 4096 positions), fp32 cache
+    in the reference's exact order, or the int8 cache; and its algorithmic
+    bytes (K and V read, q read, output written)."""
+    g = torch.Generator(device="cuda")
+    g.manual_seed(ctx)
+    q = torch.randn(n_heads * hs, device="cuda", generator=g)
+    out = torch.empty_like(q)
+    st = torch.cuda.current_stream()
+    if kv8:
+        k = torch.randint(-127, 128, (n_heads * max_t * hs,), dtype=torch.int8, device="cuda", generator=g)
+        v = torch.randint(-127, 128, (n_heads * max_t * hs,), dtype=torch.int8, device="cuda", generator=g)
+        ks = torch.rand(n_heads * max_t, device="cuda", generator=g) * 0.02
+        vs = torch.rand(n_heads * max_t, device="cuda", generator=g) * 0.02
+        args = (q.data_ptr(), k.data_ptr(), v.data_ptr(), ks.data_ptr(), vs.data_ptr(), out.data_ptr())
+        fn, nbytes = "l2q_attention_kv8", 2 * ctx * n_heads * (hs + 4)
+    else:
+        k = torch.randn(n_heads * max_t * hs, device="cuda", generator=g)
+        v = torch.randn(n_heads * max_t * hs, device="cuda", generator=g)
+        args = (q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr())
+        fn, nbytes = "l2q_attention", 2 * ctx * n_heads * hs * 4
+    nbytes += 2 * n_heads * hs * 4
+
+    def launch():
+        abi.call(fn, *args, ctx - 1, n_heads, n_heads, hs, max_t, st.cuda_stream)
+
+    for _ in range(3):
+        launch()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(st)
+    for _ in range(reps):
+        launch()
+    e1.record(st)
+    e1.synchronize()
+    return e0.elapsed_time(e1) / reps, nbytes
+
+
 def cpu_baseline(seconds_budget=20.0):
     """The reference runq.c (AVX-512 VNNI + OpenMP) on this host: 7B-shaped
     INT8 group-32 decode (its own format; the reference has no CPU INT4
@@ -135,6 +174,8 @@ def main():
     ap.add_argument("--prompt", type=int, default=128)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
+    ap.add_argument("--kv8-steps", type=int, default=64,
+                    help="greedy steps timed again with the int8 KV cache engine (0: skip)")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="first run a 256 MiB device copy (x4): a kernel of known traffic for scaling "
                          "rocprofv3 FETCH_SIZE / WRITE_SIZE readings")
@@ -162,9 +203,31 @@ def main():
     ck = host.synth_checkpoint(cfg, 4, group, seed=2024, q4_divisor=7.0)
     t_synth = time.time() - t0
     max_steps = args.prompt + args.warmup + args.steps
+    prompt = [int(v) for v in host.uniform_ints(args.prompt, 2024, 100, 3, cfg.vocab_size)]
+
+    # the same decode with the int8 KV cache (a secondary figure)
+    kv8 = None
+    if args.kv8_steps > 0:
+        e8 = Engine(ck, max_steps=args.prompt + args.warmup + args.kv8_steps, kv8=True)
+        for p in range(args.prompt - 1):
+            e8.step(prompt[p], p)
+        tok8, p8 = prompt[-1], args.prompt - 1
+        for _ in range(args.warmup):
+            tok8 = e8.forward_argmax(tok8, p8)
+            p8 += 1
+        torch.cuda.synchronize()
+        t8 = time.perf_counter()
+        for _ in range(args.kv8_steps):
+            tok8 = e8.forward_argmax(tok8, p8)
+            p8 += 1
+        torch.cuda.synchronize()
+        el8 = time.perf_counter() - t8
+        e8.close()
+        kv8 = {"tok_s": round(args.kv8_steps / el8, 2), "ms_per_step": round(el8 * 1e3 / args.kv8_steps, 4),
+               "steps": args.kv8_steps, "positions": [p8 - args.kv8_steps, p8 - 1]}
+
     eng = Engine(ck, max_steps=max_steps)
     del ck
-    prompt = [int(v) for v in host.uniform_ints(args.prompt, 2024, 100, 3, cfg.vocab_size)]
 
     # prompt forcing, then warmup greedy steps
     for pos in range(args.prompt - 1):
@@ -201,6 +264,15 @@ def main():
                    "frac": round(b / ms / 1e6 / HBM_PEAK_GBS, 4), "launches": n}
     dom = gemv["w13"]
     dom_bytes = gemv_bytes(*shapes["w13"], 4, group)
+
+    # one layer's attention at the BASELINE config-4 contexts, fp32 (exact
+    # order) and int8 caches
+    attention = {}
+    for ctx in (256, 1024, 2048, 4096):
+        for name, is8 in (("fp32", False), ("int8", True)):
+            ms, nbytes = time_attention(torch, abi, host, ctx, is8)
+            attention[f"{name}_ctx{ctx}"] = {"us": round(ms * 1e3, 2), "bytes": nbytes,
+                                             "GB/s": round(nbytes / ms / 1e6, 1)}
 
     traffic = None
     tpath = os.path.join(REPO, "profiles", "gemv_q4_g64_w13_traffic.txt")
@@ -239,6 +311,8 @@ def main():
         "step_effective_GBs": round(avg_bytes / (ms_per_step * 1e-3) / 1e9, 1),
         "device_replay_ms_per_step": round(dev_ms / args.steps, 4),
         "gemv": gemv,
+        "attention_c4": attention,
+        "kv8_decode": kv8,
         "synth_seconds": round(t_synth, 1),
     }
     print(json.dumps(line))
