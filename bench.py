@@ -94,11 +94,13 @@ def time_gemv(torch, abi, rows, cols, bits, group, min_bytes=1 << 30, reps=20):
     return ms, n
 
 
-def time_attention(torch, abi, host, ctx, kv8, reps=50, n_heads=32, hs=128, max_t=4096):
+def time_attention(torch, abi, host, ctx, mode, reps=50, n_heads=32, hs=128, max_t=4096):
     """Mean duration (ms) of one layer's decode attention at context ctx
-    (32 heads x 128, cache of 4096 positions), fp32 cache
-    in the reference's exact order, or the int8 cache; and its algorithmic
-    bytes (K and V read, q read, output written)."""
+    (32 heads x 128, cache of 4096 positions): mode
+    "exact" (fp32 cache, the reference's order), "split" (fp32 cache,
+    split-context, the config's 1e-5 tolerance) or "int8" (int8 cache); and
+    its algorithmic bytes (K and V read, q read, output written)."""
+    kv8 = mode == "int8"
     g = torch.Generator(device="cuda")
     g.manual_seed(ctx)
     q = torch.randn(n_heads * hs, device="cuda", generator=g)
@@ -115,7 +117,7 @@ def time_attention(torch, abi, host, ctx, kv8, reps=50, n_heads=32, hs=128, max_
         k = torch.randn(n_heads * max_t * hs, device="cuda", generator=g)
         v = torch.randn(n_heads * max_t * hs, device="cuda", generator=g)
         args = (q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr())
-        fn, nbytes = "l2q_attention", 2 * ctx * n_heads * hs * 4
+        fn, nbytes = "l2q_attention" if mode == "exact" else "l2q_attention_split", 2 * ctx * n_heads * hs * 4
     nbytes += 2 * n_heads * hs * 4
 
     def launch():
@@ -265,12 +267,12 @@ def main():
     dom = gemv["w13"]
     dom_bytes = gemv_bytes(*shapes["w13"], 4, group)
 
-    # one layer's attention at the BASELINE config-4 contexts, fp32 (exact
-    # order) and int8 caches
+    # one layer's attention at the BASELINE config-4 contexts: fp32 cache in
+    # the exact order and split over the context, int8 cache
     attention = {}
     for ctx in (256, 1024, 2048, 4096):
-        for name, is8 in (("fp32", False), ("int8", True)):
-            ms, nbytes = time_attention(torch, abi, host, ctx, is8)
+        for name in ("exact", "split", "int8"):
+            ms, nbytes = time_attention(torch, abi, host, ctx, name)
             attention[f"{name}_ctx{ctx}"] = {"us": round(ms * 1e3, 2), "bytes": nbytes,
                                              "GB/s": round(nbytes / ms / 1e6, 1)}
 

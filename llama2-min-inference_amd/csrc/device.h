@@ -15,7 +15,6 @@ namespace l2q {
 constexpr int kNormThreads = 1024;   // fused RMSNorm: one workgroup
 constexpr int kNormMaxPer = 8;       // elements per thread -> n <= 8192
 constexpr int kAttnThreads = 256;    // attention workgroup
-constexpr int kAttnTile = 64;        // positions per LDS-staged K tile
 constexpr int kAttnMaxHs = 256;      // largest head size
 
 typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));

@@ -145,31 +145,37 @@ __global__ __launch_bounds__(256) void k_rope_kv_append(
 
 // ---------------------------------------------------------------------------
 // Single-query attention, split over the context (runq.c:367-391 +
-// softmax :307-318).  Workgroup (head h, split s) covers positions
-// [s*C, min((s+1)*C, pos+1)) with C = ceil((pos+1)/S); it streams K in
-// LDS-staged tiles of 64 positions (coalesced 128-bit loads, padded rows),
-// scores one position per lane, keeps an online (max, sum) and accumulates
-// p*V with V read coalesced straight from the cache.  It leaves the
-// partial (m, l, o[hs]); k_attn_combine merges the S partials of a head.
+// softmax :307-318; the tolerance path of BASELINE config 4).  Workgroup
+// (head h, split s) covers positions [s*C, min((s+1)*C, pos+1)) with C =
+// ceil((pos+1)/S):
+//   scores   four lanes per position (lane sub sums the 4-element chunks
+//            4*sub + 16*i with FMAs, K read straight from the cache as
+//            float4, q held in registers), 64 positions per pass, all of a
+//            pass's loads in flight at once; scores to LDS;
+//   softmax  block max m and l = sum_t exp(s_t - m) over the split;
+//   p*V      thread (slice, g) accumulates elements 4g..4g+3 (float4 loads,
+//            a 512 B row per 32 threads) over positions t = slice (mod
+//            slices), four rows in flight; the slices are added in LDS.
+// It leaves the partial (m, l, o[hs]) with o unnormalised; k_attn_combine
+// merges the S partials of a head.
+__host__ __device__ constexpr size_t attn_lds_bytes(int C, int hs) {
+    return ((size_t)(C + 3) / 4 * 4 + 4 * kAttnThreads + 16) * sizeof(float);
+}
 
 __global__ __launch_bounds__(kAttnThreads) void k_attn_partial(
     const float* __restrict__ q, const float* __restrict__ kcache, const float* __restrict__ vcache,
     float* __restrict__ part_o, float* __restrict__ part_ml, const int* __restrict__ meta, int pos_arg,
     int n_heads, int kv_mul, int hs, int max_t) {
-    extern __shared__ float smem[];
-    const int hsp = hs + 4;                         // padded K row (keeps 16 B alignment)
-    float* kt = smem;                               // [kAttnTile][hsp]
-    float* qs = kt + kAttnTile * hsp;               // [hs]
-    float* sc = qs + hs;                            // [4][kAttnTile] partial scores
-    float* pt = sc + 4 * kAttnTile;                 // [kAttnTile] tile probabilities
-    float* ov = pt + kAttnTile;                     // [kAttnThreads] V partials
-    float* st = ov + kAttnThreads;                  // [4]: m, l, alpha
+    extern __shared__ __attribute__((aligned(16))) float smem[];
     const int h = blockIdx.x, s = blockIdx.y, S = gridDim.y;
-    const int tid = threadIdx.x, lane = tid & (L2Q_WAVE - 1), wv = tid / L2Q_WAVE;
+    const int tid = threadIdx.x, lane = tid & (L2Q_WAVE - 1), wv = tid / L2Q_WAVE, sub = tid & 3;
     const int pos = meta_pos(meta, pos_arg);
     const int n = pos + 1;
     const int C = (n + S - 1) / S;
-    const int t0 = s * C, t1 = min(n, t0 + C);
+    const int t0 = min(s * C, n), t1 = min(n, t0 + C);
+    float* sc = smem;                                   // [C] scores, then exp(s - m)
+    float* part = sc + (C + 3) / 4 * 4;                 // [slices][hs]
+    float* red = part + 4 * kAttnThreads;               // [8] block reductions
     float* po = part_o + ((size_t)h * S + s) * hs;
     float* pml = part_ml + ((size_t)h * S + s) * 2;
     if (t0 >= t1) {   // empty split (uniform across the workgroup)
@@ -180,75 +186,77 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn_partial(
     const int kvh = h / kv_mul;
     const float* kbase = kcache + (size_t)kvh * max_t * hs;
     const float* vbase = vcache + (size_t)kvh * max_t * hs;
-    for (int d = tid; d < hs; d += kAttnThreads) qs[d] = q[(size_t)h * hs + d];
-    if (tid == 0) { st[0] = -INFINITY; st[1] = 0.0f; }
-
+    const float* qh = q + (size_t)h * hs;
+    constexpr int kQChunks = kAttnMaxHs / 16;           // float4 chunks of q per lane (hs <= 256)
+    float4 qr[kQChunks];
+#pragma unroll
+    for (int i = 0; i < kQChunks; i++)
+        qr[i] = 16 * i + 4 * sub < hs ? *reinterpret_cast<const float4*>(qh + 16 * i + 4 * sub)
+                                      : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
     const float rs = sqrtf((float)hs);
-    const int dslice = hs / 4;                      // dims per wave in the score pass
-    const int nsl = kAttnThreads / hs;              // position slices in the V pass
-    const int vd = tid % hs, vsl = tid / hs;
-    const int f4 = hs / 4;
-    float o = 0.0f;
-
-    for (int tb = t0; tb < t1; tb += kAttnTile) {
-        const int nt = min(kAttnTile, t1 - tb);
-        __syncthreads();   // previous tile consumed; qs / st visible
-        // stage K[tb .. tb+nt) with 128-bit coalesced loads
-        for (int f = tid; f < nt * f4; f += kAttnThreads) {
-            const int r = f / f4, c4 = f - r * f4;
-            const float4 kv4 = *reinterpret_cast<const float4*>(kbase + (size_t)(tb + r) * hs + 4 * c4);
-            *reinterpret_cast<float4*>(kt + r * hsp + 4 * c4) = kv4;
-        }
-        __syncthreads();
-        // partial scores: lane = position, wave wv sums dims [wv*dslice, (wv+1)*dslice)
-        {
-            float acc = 0.0f;
-            if (lane < nt) {
-                const float* kr = kt + lane * hsp + wv * dslice;
-                const float* qq = qs + wv * dslice;
-                for (int d = 0; d < dslice; d++) acc = __builtin_fmaf(qq[d], kr[d], acc);
-            }
-            sc[wv * kAttnTile + lane] = acc;
-        }
-        __syncthreads();
-        // wave 0: scores, tile max, probabilities, running (m, l)
-        if (wv == 0) {
-            const bool in = lane < nt;
-            const float sj = in ? (sc[lane] + sc[kAttnTile + lane] + sc[2 * kAttnTile + lane] +
-                                   sc[3 * kAttnTile + lane]) / rs
-                                : -INFINITY;
-            const float m_old = st[0];
-            const float mn = fmaxf(m_old, wave_max(sj));
-            const float pj = in ? expf(sj - mn) : 0.0f;
-            pt[lane] = pj;
-            const float psum = wave_sum(pj);
-            if (lane == 0) {
-                const float alpha = expf(m_old - mn);   // 0 on the first tile
-                st[0] = mn;
-                st[1] = st[1] * alpha + psum;
-                st[2] = alpha;
+    for (int tb = t0; tb < t1; tb += kAttnThreads / 4) {
+        const int t = tb + tid / 4;
+        const float* kr = kbase + (size_t)min(t, t1 - 1) * hs;
+        float4 kk[kQChunks];
+#pragma unroll
+        for (int i = 0; i < kQChunks; i++)
+            kk[i] = 16 * i + 4 * sub < hs ? *reinterpret_cast<const float4*>(kr + 16 * i + 4 * sub)
+                                          : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        float acc = 0.0f;
+#pragma unroll
+        for (int i = 0; i < kQChunks; i++) {
+            if (16 * i < hs) {
+                acc = __builtin_fmaf(qr[i].x, kk[i].x, acc);
+                acc = __builtin_fmaf(qr[i].y, kk[i].y, acc);
+                acc = __builtin_fmaf(qr[i].z, kk[i].z, acc);
+                acc = __builtin_fmaf(qr[i].w, kk[i].w, acc);
             }
         }
-        __syncthreads();
-        o *= st[2];
-        if (vsl < nsl) {
-            for (int j = vsl; j < nt; j += nsl) o = __builtin_fmaf(pt[j], vbase[(size_t)(tb + j) * hs + vd], o);
-        }
+        acc += __shfl_xor(acc, 1);
+        acc += __shfl_xor(acc, 2);
+        if (sub == 0 && t < t1) sc[t - t0] = acc / rs;
     }
-    // reduce the position slices of the V accumulator
-    ov[tid] = o;
     __syncthreads();
-    if (tid < hs) {
-        float t = 0.0f;
-        for (int k = 0; k < nsl; k++) t += ov[k * hs + tid];
-        po[tid] = t;
+    const int m_n = t1 - t0;
+    float m = -INFINITY;
+    for (int j = tid; j < m_n; j += kAttnThreads) m = fmaxf(m, sc[j]);
+    m = wave_max(m);
+    if (lane == 0) red[wv] = m;
+    __syncthreads();
+    m = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+    float l = 0.0f;
+    for (int j = tid; j < m_n; j += kAttnThreads) {
+        const float e = expf(sc[j] - m);
+        sc[j] = e;
+        l += e;
     }
-    if (tid == 0) { pml[0] = st[0]; pml[1] = st[1]; }
-}
-
-// LDS bytes of k_attn_partial for a head size.
-__host__ __device__ constexpr size_t attn_lds_bytes(int hs) {
-    return (size_t)(kAttnTile * (hs + 4) + hs + 4 * kAttnTile + kAttnTile + kAttnThreads + 4) * sizeof(float);
+    l = wave_sum(l);
+    if (lane == 0) red[4 + wv] = l;
+    __syncthreads();
+    l = (red[4] + red[5]) + (red[6] + red[7]);
+    const int groups = hs / 4, slices = kAttnThreads / groups;
+    const int gi = tid % groups, slice = tid / groups;
+    float4 o = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    if (slice < slices) {
+        const float* vb = vbase + 4 * gi;
+#pragma unroll 4
+        for (int j = slice; j < m_n; j += slices) {
+            const float4 vv = *reinterpret_cast<const float4*>(vb + (size_t)(t0 + j) * hs);
+            const float p = sc[j];
+            o.x = __builtin_fmaf(p, vv.x, o.x);
+            o.y = __builtin_fmaf(p, vv.y, o.y);
+            o.z = __builtin_fmaf(p, vv.z, o.z);
+            o.w = __builtin_fmaf(p, vv.w, o.w);
+        }
+        *reinterpret_cast<float4*>(part + (size_t)slice * hs + 4 * gi) = o;
+    }
+    __syncthreads();
+    for (int d = tid; d < hs; d += kAttnThreads) {
+        float t = 0.0f;
+        for (int k = 0; k < slices; k++) t += part[(size_t)k * hs + d];
+        po[d] = t;
+    }
+    if (tid == 0) { pml[0] = m; pml[1] = l; }
 }
 
 // ---------------------------------------------------------------------------

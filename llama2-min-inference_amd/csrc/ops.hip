@@ -216,8 +216,14 @@ int launch_attention_split(const float* q, const float* kcache, const float* vca
                   pos, max_t);
         return L2Q_ERR_ARG;
     }
-    hipLaunchKernelGGL(k_attn_partial, dim3(n_heads, S), dim3(kAttnThreads), attn_lds_bytes(hs), st, q, kcache, vcache,
-                       part_o, part_ml, meta, pos, n_heads, n_heads / n_kv_heads, hs, max_t);
+    const int nmax = meta ? max_t : pos + 1;   // a captured graph covers every position
+    const size_t lds = attn_lds_bytes((nmax + S - 1) / S, hs);
+    if (lds > 65536) {
+        set_error("attention: %d positions per split exceed the LDS budget", (nmax + S - 1) / S);
+        return L2Q_ERR_ARG;
+    }
+    hipLaunchKernelGGL(k_attn_partial, dim3(n_heads, S), dim3(kAttnThreads), lds, st, q, kcache, vcache, part_o,
+                       part_ml, meta, pos, n_heads, n_heads / n_kv_heads, hs, max_t);
     int rc = check_launch("attention_partial");
     if (rc) return rc;
     hipLaunchKernelGGL(k_attn_combine, dim3(n_heads), dim3(hs < 256 ? hs : 256), 0, st, part_o, part_ml, out, S, hs);
@@ -303,9 +309,9 @@ int launch_unbias(const uint8_t* src, int8_t* dst, size_t n, hipStream_t st) {
 }
 
 // Split counts for a one-off attention call.
-static int attention_splits(int pos) {     // split-context path: ~32 positions per workgroup
-    int S = (pos + 1 + 31) / 32;
-    return S < 1 ? 1 : (S > 128 ? 128 : S);
+static int attention_splits(int pos) {     // split-context path: ~128 positions per workgroup
+    int S = (pos + 1 + 127) / 128;
+    return S < 1 ? 1 : (S > 512 ? 512 : S);
 }
 
 // Per-device scratch for the partials of l2q_attention (grown on demand).
