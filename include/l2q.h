@@ -98,6 +98,16 @@ int l2q_engine_create(const l2q_config* cfg, const void* weights,
                       size_t weights_bytes, int wbits, int group,
                       int max_steps, l2q_engine** out);
 
+/* Batched prefill: positions pos0..pos0+n-1 take tokens[0..n) through every
+ * layer together (chunks of up to 128 tokens; the weights stream once per
+ * chunk, group dots on int8 MFMA), leaving the KV cache exactly as n calls
+ * of l2q_engine_forward would; if logits is not NULL it receives the logits
+ * of the last position, bit-identical to l2q_engine_forward's.  Replaces the
+ * prompt-forcing loop of generate() (runq.c:695-700, v5-cuda-fused/run.cu:
+ * 969-974) and the batched forward of v2-cuda/run.cu:347-394. */
+int l2q_engine_prefill(l2q_engine* e, const int* tokens, int n, int pos0,
+                       float* logits);
+
 /* Engine options (l2q_engine_create_ex). */
 #define L2Q_ENGINE_KV_INT8 1   /* int8 KV cache (l2q_kv8_append / l2q_attention_kv8
                                   semantics), the reference's -DINT8_KV=1 build */
@@ -215,6 +225,16 @@ int l2q_attention(const float* q, const float* kcache, const float* vcache,
 int l2q_attention_split(const float* q, const float* kcache, const float* vcache,
                         float* out, int pos, int n_heads, int n_kv_heads,
                         int head_size, int max_t, void* stream);
+
+/* Batched GEMV of T activation vectors (a GEMM): out[t][r] = the row-r
+ * output of l2q_gemv_q8 / l2q_gemv_q4 for input t, bit for bit, for
+ * t < T.  xq [T][cols] int8 and xs [T][cols/group] as l2q_quantize_act
+ * writes them per vector; w, ws as for the GEMVs; out [T][rows].  Group
+ * dots on int8 MFMA.  Replaces launch_matmul with T > 1
+ * (v2-cuda/run.cu:131-162, 390-395). */
+int l2q_gemm_q(int wbits, float* out, const int8_t* xq, const float* xs,
+               const void* w, const float* ws, int rows, int cols, int group,
+               int T, void* stream);
 
 /* ---- int8 KV cache (v5-cuda-fused/run.cu:41-48, built there with
  * -DINT8_KV=1) ----

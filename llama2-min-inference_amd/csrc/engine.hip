@@ -65,6 +65,12 @@ struct l2q_engine {
     int* h_meta = nullptr;   // pinned {token, pos} slots
     int h_meta_slots = 0;
     int* h_am = nullptr;     // pinned argmax result
+    // batched prefill (allocated at the first l2q_engine_prefill): T tokens per chunk
+    char* pfarena = nullptr;
+    int pf_T = 0;
+    float *pf_xa, *pf_xb, *pf_qkv, *pf_att, *pf_wo, *pf_h13, *pf_ffn, *pf_scores, *pf_xs, *pf_xt;
+    int8_t *pf_xq, *pf_xqp;
+    int *pf_sq, *pf_tok;
 };
 
 using namespace l2q;
@@ -213,6 +219,7 @@ void release(l2q_engine* e) {
     if (e->stream) (void)hipStreamDestroy(e->stream);
     if (e->warena) (void)hipFree(e->warena);
     if (e->sarena) (void)hipFree(e->sarena);
+    if (e->pfarena) (void)hipFree(e->pfarena);
     if (e->h_meta) (void)hipHostFree(e->h_meta);
     if (e->h_am) (void)hipHostFree(e->h_am);
 }
@@ -363,9 +370,124 @@ int launch_step(l2q_engine* e, int token, int pos, hipGraphExec_t ex, int slot) 
     return L2Q_OK;
 }
 
+// Prefill buffers for chunks of up to pf_T tokens.
+int prefill_alloc(l2q_engine* e) {
+    if (e->pfarena) return L2Q_OK;
+    const l2q_config& c = e->cfg;
+    const size_t T = (size_t)(e->max_t < kPfMaxTokens ? e->max_t : kPfMaxTokens);
+    const size_t d = c.dim, h = c.hidden_dim, kv = e->kv_dim, qkv = d + 2 * kv;
+    const size_t kmax = d > h ? d : h, nbmax = kmax / e->G;
+    Arena a;
+    const size_t o_xa = a.take(T * d * 4), o_xb = a.take(T * d * 4), o_qkv = a.take(T * qkv * 4);
+    const size_t o_att = a.take(T * d * 4), o_wo = a.take(T * d * 4), o_h13 = a.take(T * 2 * h * 4);
+    const size_t o_ffn = a.take(T * d * 4), o_sc = a.take(T * c.n_heads * (size_t)e->max_t * 4);
+    const size_t o_xq = a.take(T * kmax), o_xqp = a.take(T * kmax);
+    const size_t o_xs = a.take(T * nbmax * 4), o_xt = a.take(T * nbmax * 4), o_sq = a.take(T * nbmax * 4);
+    const size_t o_tok = a.take(T * 4);
+    HIPCHK(hipMalloc(&e->pfarena, align_up(a.used, 256)), "hipMalloc(prefill)");
+    char* P = e->pfarena;
+    e->pf_xa = (float*)(P + o_xa); e->pf_xb = (float*)(P + o_xb); e->pf_qkv = (float*)(P + o_qkv);
+    e->pf_att = (float*)(P + o_att); e->pf_wo = (float*)(P + o_wo); e->pf_h13 = (float*)(P + o_h13);
+    e->pf_ffn = (float*)(P + o_ffn); e->pf_scores = (float*)(P + o_sc);
+    e->pf_xq = (int8_t*)(P + o_xq); e->pf_xqp = (int8_t*)(P + o_xqp);
+    e->pf_xs = (float*)(P + o_xs); e->pf_xt = (float*)(P + o_xt); e->pf_sq = (int*)(P + o_sq);
+    e->pf_tok = (int*)(P + o_tok);
+    e->pf_T = (int)T;
+    return L2Q_OK;
+}
+
+// T tokens at positions pos0.. through every layer at once: the same
+// operations as T decode steps (so the KV rows and the last position's
+// logits are bit-identical), with the weights streamed once per chunk.
+int prefill_chunk(l2q_engine* e, const int* tokens, int T, int pos0, bool want_logits) {
+    const l2q_config& c = e->cfg;
+    const int d = c.dim, h = c.hidden_dim, kv = e->kv_dim, G = e->G, bits = e->wbits;
+    const int qkv_rows = d + 2 * kv;
+    const size_t nbd = (size_t)d / G, nbh = (size_t)h / G;
+    hipStream_t st = e->stream;
+    int rc;
+    HIPCHK(hipMemcpyAsync(e->pf_tok, tokens, T * sizeof(int), hipMemcpyHostToDevice, st), "upload tokens");
+    if ((rc = launch_pf_embed(e->emb, e->pf_tok, e->pf_xa, d, T, st))) return rc;
+    auto gemm = [&](const uint8_t* w, const float* ws, int rows, int cols, float* out) {
+        int r = launch_pf_prep(bits, G, e->pf_xq, e->pf_xs, cols, T, e->pf_xqp, e->pf_sq, e->pf_xt, st);
+        if (!r) r = launch_pf_gemm(bits, G, w, ws, rows, cols, e->pf_xqp, e->pf_xs, e->pf_sq, e->pf_xt, T, out, rows, st);
+        return r;
+    };
+    for (int l = 0; l < c.n_layers; l++) {
+        float* kc = e->kcache + (size_t)l * kv * e->max_t;
+        float* vc = e->vcache + (size_t)l * kv * e->max_t;
+        // x = (l == 0 ? emb rows : xa + ffn) -> xb; RMSNorm; q, k, v; RoPE + append; attention
+        if ((rc = launch_rmsnorm_quant(e->pf_xa, nullptr, nullptr, l == 0 ? nullptr : e->pf_ffn, e->pf_xb,
+                                       e->rms_att + (size_t)l * d, d, G, e->pf_xq, e->pf_xs, st, T)))
+            return rc;
+        if ((rc = gemm(e->qkv_w + (size_t)l * qkv_rows * e->rowb_d, e->qkv_s + (size_t)l * qkv_rows * nbd, qkv_rows,
+                       d, e->pf_qkv)))
+            return rc;
+        if ((rc = launch_rope_kv_append(e->pf_qkv, e->pf_qkv + d, e->pf_qkv + d + kv, kc, vc, e->rope, nullptr,
+                                        pos0, d, kv, e->hs, e->max_t, st, T, qkv_rows)))
+            return rc;
+        if ((rc = launch_attention_exact(e->pf_qkv, kc, vc, e->pf_att, e->pf_scores, 0, nullptr, pos0, c.n_heads,
+                                         c.n_kv_heads, e->hs, e->max_t, st, T, qkv_rows)))
+            return rc;
+        // wo
+        if ((rc = launch_quantize(e->pf_att, T * d, G, e->pf_xq, e->pf_xs, st))) return rc;
+        if ((rc = gemm(e->wo_w + (size_t)l * d * e->rowb_d, e->wo_s + (size_t)l * d * nbd, d, d, e->pf_wo))) return rc;
+        // x = xb + wo -> xa; RMSNorm; SwiGLU(w1 x, w3 x); w2
+        if ((rc = launch_rmsnorm_quant(e->pf_xb, nullptr, nullptr, e->pf_wo, e->pf_xa, e->rms_ffn + (size_t)l * d, d,
+                                       G, e->pf_xq, e->pf_xs, st, T)))
+            return rc;
+        if ((rc = gemm(e->w13_w + (size_t)l * 2 * h * e->rowb_d, e->w13_s + (size_t)l * 2 * h * nbd, 2 * h, d,
+                       e->pf_h13)))
+            return rc;
+        if ((rc = launch_pf_swiglu_quant(e->pf_h13, h, T, G, e->pf_xq, e->pf_xs, st))) return rc;
+        if ((rc = gemm(e->w2_w + (size_t)l * d * e->rowb_h, e->w2_s + (size_t)l * d * nbh, d, h, e->pf_ffn))) return rc;
+    }
+    if (!want_logits) return L2Q_OK;
+    // the last position: final RMSNorm of xa + ffn, classifier
+    GemvArgs ca{};
+    ca.out = e->logits;
+    ca.w = e->wcls_w;
+    ca.ws = e->wcls_s;
+    ca.rows = c.vocab_size;
+    ca.cols = d;
+    ca.x_in = e->pf_xa + (size_t)(T - 1) * d;
+    ca.resid = e->pf_ffn + (size_t)(T - 1) * d;
+    ca.norm_w = e->rms_final;
+    ca.meta = e->meta;
+    return launch_gemv_fused(bits, G, kNorm, kStore, ca, st);
+}
+
 }  // namespace
 
 extern "C" {
+
+int l2q_engine_prefill(l2q_engine* e, const int* tokens, int n, int pos0, float* logits) {
+    if (!e || !tokens || n < 1) { set_error("engine: bad prefill arguments"); return L2Q_ERR_ARG; }
+    if (pos0 < 0 || pos0 + n > e->max_t) {
+        set_error("engine: prefill positions %d..%d outside the KV cache (max_steps %d)", pos0, pos0 + n - 1,
+                  e->max_t);
+        return L2Q_ERR_STATE;
+    }
+    for (int i = 0; i < n; i++)
+        if (tokens[i] < 0 || tokens[i] >= e->cfg.vocab_size) { set_error("engine: token %d out of range", tokens[i]); return L2Q_ERR_ARG; }
+    int rc;
+    if (e->flags & L2Q_ENGINE_KV_INT8) {   // int8 KV cache: the decode step per token (same results)
+        for (int i = 0; i < n; i++)
+            if ((rc = l2q_engine_forward(e, tokens[i], pos0 + i, i == n - 1 ? logits : nullptr))) return rc;
+        return L2Q_OK;
+    }
+    if ((rc = prefill_alloc(e))) return rc;
+    for (int i0 = 0; i0 < n; i0 += e->pf_T) {
+        const int T = n - i0 < e->pf_T ? n - i0 : e->pf_T;
+        if ((rc = prefill_chunk(e, tokens + i0, T, pos0 + i0, i0 + T == n))) return rc;
+    }
+    if (logits)
+        HIPCHK(hipMemcpyAsync(logits, e->logits, (size_t)e->cfg.vocab_size * 4, hipMemcpyDeviceToHost, e->stream),
+               "copy logits");
+    HIPCHK(hipStreamSynchronize(e->stream), "hipStreamSynchronize");
+    return L2Q_OK;
+}
+
 
 int l2q_engine_create(const l2q_config* cfg, const void* weights, size_t weights_bytes, int wbits, int group,
                       int max_steps, l2q_engine** out) {

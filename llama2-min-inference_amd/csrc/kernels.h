@@ -51,6 +51,15 @@ __global__ __launch_bounds__(kNormThreads) void k_rmsnorm_quant(
     __shared__ float vs[kNormThreads * kNormMaxPer];
     __shared__ float inv_s;
     const int tid = threadIdx.x;
+    // workgroup t normalises vector t of a batch (rows of n; one vector per launch on the decode path)
+    const size_t to = (size_t)blockIdx.x * n;
+    if (blockIdx.x) {
+        x += to;
+        if (resid) resid += to;
+        if (xout) xout += to;
+        xq += to;
+        xs += to / G;
+    }
     const float* src = emb ? emb + (size_t)meta[0] * n : x;
     float v[kNormMaxPer];
 #pragma unroll
@@ -116,14 +125,19 @@ __global__ __launch_bounds__(256) void k_swiglu_quant(const float* __restrict__ 
 // Rotation as a GCC -O3 -march=native build of the reference evaluates it:
 //   v0' = fma(v0, c, -(v1*s)),  v1' = fma(v0, s, v1*c).
 // Cache layout [n_kv_heads][max_t][head_size].
+// Workgroup row y handles token y of a batch at position pos + y, its q, k,
+// v rows `stride` floats after the previous token's (prefill).
 __global__ __launch_bounds__(256) void k_rope_kv_append(
     float* __restrict__ q, const float* __restrict__ k, const float* __restrict__ v,
     float* __restrict__ kcache, float* __restrict__ vcache, const float* __restrict__ rope,
-    const int* __restrict__ meta, int pos_arg, int dim, int kv_dim, int hs, int max_t) {
+    const int* __restrict__ meta, int pos_arg, int dim, int kv_dim, int hs, int max_t, int stride) {
     const int p = blockIdx.x * blockDim.x + threadIdx.x;
     const int i = 2 * p;
     if (i >= dim) return;
-    const int pos = meta_pos(meta, pos_arg);
+    const int pos = meta_pos(meta, pos_arg) + blockIdx.y;
+    q += (size_t)blockIdx.y * stride;
+    k += (size_t)blockIdx.y * stride;
+    v += (size_t)blockIdx.y * stride;
     const int hd = i % hs;
     const float c = rope[(size_t)pos * hs + hd];
     const float s = rope[(size_t)pos * hs + hd + 1];
@@ -340,16 +354,20 @@ __device__ __forceinline__ float serial_dot(const float* kr, const float* qs, in
     return score;
 }
 
+// Grid row y: query y of a batch at position pos + y, its q `q_stride`
+// floats after the previous query's, scores in its own [n_heads][max_t].
 __global__ __launch_bounds__(kScoreThreads) void k_attn_scores(
     const float* __restrict__ q, const float* __restrict__ kcache, float* __restrict__ scores,
-    const int* __restrict__ meta, int pos_arg, int kv_mul, int n_heads, int hs, int max_t) {
+    const int* __restrict__ meta, int pos_arg, int kv_mul, int n_heads, int hs, int max_t, int q_stride) {
 #pragma clang fp contract(off)
     extern __shared__ __attribute__((aligned(16))) float sm[];
     const int hsp = hs + 4;
     float* kt = sm;                       // [kScoreTile][hsp]
     float* qs = kt + kScoreTile * hsp;    // [hs]
     const int tid = threadIdx.x;
-    const int pos = meta_pos(meta, pos_arg);
+    const int pos = meta_pos(meta, pos_arg) + blockIdx.y;
+    q += (size_t)blockIdx.y * q_stride;
+    scores += (size_t)blockIdx.y * n_heads * max_t;
     const int n = pos + 1;
     const int ntile = (n + kScoreTile - 1) / kScoreTile;
     const int f4 = hs / 4;
@@ -451,6 +469,7 @@ __device__ __forceinline__ float serial_pv(const float* p, const float* v, int n
     return acc;
 }
 
+// Grid z: query z of a batch (position pos + z, scores and output of its own).
 __global__ __launch_bounds__(kAttnThreads) void k_attn_softmax_v(
     const float* __restrict__ scores, const float* __restrict__ vcache, float* __restrict__ out,
     const int* __restrict__ meta, int pos_arg, int kv_mul, int hs, int max_t) {
@@ -461,9 +480,11 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn_softmax_v(
     float* red = vt + 2 * kVDims * kVStride;             // [4] wave maxima, [4] sum
     const int h = blockIdx.x, d0 = blockIdx.y * kVDims;
     const int tid = threadIdx.x, lane = tid & (L2Q_WAVE - 1), wv = tid / L2Q_WAVE;
-    const int pos = meta_pos(meta, pos_arg);
+    const int pos = meta_pos(meta, pos_arg) + blockIdx.z;
     const int n = pos + 1;
     const int width = min(kVDims, hs - d0);
+    scores += (size_t)blockIdx.z * gridDim.x * max_t;
+    out += (size_t)blockIdx.z * gridDim.x * hs;
     const float* sc = scores + (size_t)h * max_t;
     const float* vbase = vcache + (size_t)(h / kv_mul) * max_t * hs + d0;
     const int nchunks = (n + kVChunk - 1) / kVChunk;

@@ -23,16 +23,18 @@ int launch_gemv(int bits, int group, const GemvArgs& a, hipStream_t st);   // kP
 int launch_quantize(const float* x, int n, int group, int8_t* xq, float* xs, hipStream_t st);
 
 // emb/meta: layer-0 form (x = emb[meta[0]]); otherwise x.
+// T > 1: T consecutive vectors of n (x, resid, xout, xq rows of n; xs rows of n/group).
 int launch_rmsnorm_quant(const float* x, const float* emb, const int* meta, const float* resid,
                          float* xout, const float* w, int n, int group, int8_t* xq, float* xs,
-                         hipStream_t st);
+                         hipStream_t st, int T = 1);
 
 int launch_swiglu_quant(const float* hb, const float* hb2, int n, int group, int8_t* xq, float* xs,
                         float* gout, hipStream_t st);
 
+// T > 1: tokens at positions pos..pos+T-1, their q/k/v rows `stride` floats apart.
 int launch_rope_kv_append(float* q, const float* k, const float* v, float* kcache, float* vcache,
                           const float* rope, const int* meta, int pos, int dim, int kv_dim, int hs,
-                          int max_t, hipStream_t st);
+                          int max_t, hipStream_t st, int T = 1, int stride = 0);
 
 // Split-context attention (tolerance path): S splits per head, partial
 // buffers of n_heads*S*hs and n_heads*S*2 floats.
@@ -42,9 +44,11 @@ int launch_attention_split(const float* q, const float* kcache, const float* vca
 
 // Attention in the reference's exact order: `scores` is n_heads*max_t
 // floats of scratch, S the number of score workgroups per head.
+// T > 1: queries at positions pos..pos+T-1 (causal), q rows `q_stride` floats
+// apart, outputs [T][n_heads*hs], scores [T][n_heads][max_t].
 int launch_attention_exact(const float* q, const float* kcache, const float* vcache, float* out, float* scores,
                            int S, const int* meta, int pos, int n_heads, int n_kv_heads, int hs, int max_t,
-                           hipStream_t st);
+                           hipStream_t st, int T = 1, int q_stride = 0);
 bool attention_exact_ok(int max_t);
 
 // int8 KV cache: append one position / attention over positions 0..pos.
@@ -61,6 +65,15 @@ inline int score_splits(int n) {
     const int S = (n + 127) / 128;
     return S < 1 ? 1 : (S > 64 ? 64 : S);
 }
+
+// Batched prefill (prefill.h): activation preparation and the exact-fold GEMM.
+constexpr int kPfMaxTokens = 128;    // tokens per prefill chunk
+int launch_pf_prep(int bits, int group, const int8_t* xq, const float* xs, int K, int T, int8_t* xqp, int* sq,
+                   float* xt, hipStream_t st);
+int launch_pf_gemm(int bits, int group, const void* w, const float* ws, int rows, int cols, const int8_t* xqp,
+                   const float* xs, const int* sq, const float* xt, int T, float* out, int ldo, hipStream_t st);
+int launch_pf_embed(const float* emb, const int* tokens, float* x, int dim, int T, hipStream_t st);
+int launch_pf_swiglu_quant(const float* h13, int n, int T, int group, int8_t* xq, float* xs, hipStream_t st);
 
 int launch_argmax(const float* v, int n, int* out, hipStream_t st);
 int launch_unbias(const uint8_t* src, int8_t* dst, size_t n, hipStream_t st);

@@ -6,6 +6,7 @@
 #include <string.h>
 
 #include "kernels.h"
+#include "prefill.h"
 #include "launch.h"
 
 namespace l2q {
@@ -169,15 +170,16 @@ int launch_quantize(const float* x, int n, int group, int8_t* xq, float* xs, hip
 }
 
 int launch_rmsnorm_quant(const float* x, const float* emb, const int* meta, const float* resid, float* xout,
-                         const float* w, int n, int group, int8_t* xq, float* xs, hipStream_t st) {
-    if (n <= 0 || n > kNormThreads * kNormMaxPer || (group != 32 && group != 64) || n % group) {
-        set_error("rmsnorm_quant: bad n=%d group=%d", n, group);
+                         const float* w, int n, int group, int8_t* xq, float* xs, hipStream_t st, int T) {
+    if (n <= 0 || n > kNormThreads * kNormMaxPer || (group != 32 && group != 64) || n % group || T < 1 ||
+        (T > 1 && emb)) {
+        set_error("rmsnorm_quant: bad n=%d group=%d T=%d", n, group, T);
         return L2Q_ERR_ARG;
     }
     if (group == 32)
-        hipLaunchKernelGGL(k_rmsnorm_quant<32>, dim3(1), dim3(kNormThreads), 0, st, x, emb, meta, resid, xout, w, n, xq, xs);
+        hipLaunchKernelGGL(k_rmsnorm_quant<32>, dim3(T), dim3(kNormThreads), 0, st, x, emb, meta, resid, xout, w, n, xq, xs);
     else
-        hipLaunchKernelGGL(k_rmsnorm_quant<64>, dim3(1), dim3(kNormThreads), 0, st, x, emb, meta, resid, xout, w, n, xq, xs);
+        hipLaunchKernelGGL(k_rmsnorm_quant<64>, dim3(T), dim3(kNormThreads), 0, st, x, emb, meta, resid, xout, w, n, xq, xs);
     return check_launch("rmsnorm_quant");
 }
 
@@ -191,14 +193,17 @@ int launch_swiglu_quant(const float* hb, const float* hb2, int n, int group, int
 }
 
 int launch_rope_kv_append(float* q, const float* k, const float* v, float* kcache, float* vcache, const float* rope,
-                          const int* meta, int pos, int dim, int kv_dim, int hs, int max_t, hipStream_t st) {
-    if (hs <= 0 || hs % 2 || dim % hs || kv_dim % hs || kv_dim > dim || max_t <= 0 || (!meta && (pos < 0 || pos >= max_t))) {
-        set_error("rope_kv_append: bad shape dim=%d kv_dim=%d hs=%d pos=%d max_t=%d", dim, kv_dim, hs, pos, max_t);
+                          const int* meta, int pos, int dim, int kv_dim, int hs, int max_t, hipStream_t st, int T,
+                          int stride) {
+    if (hs <= 0 || hs % 2 || dim % hs || kv_dim % hs || kv_dim > dim || max_t <= 0 || T < 1 ||
+        (!meta && (pos < 0 || pos + T > max_t)) || (meta && T > 1)) {
+        set_error("rope_kv_append: bad shape dim=%d kv_dim=%d hs=%d pos=%d T=%d max_t=%d", dim, kv_dim, hs, pos, T,
+                  max_t);
         return L2Q_ERR_ARG;
     }
     const int pairs = dim / 2;
-    hipLaunchKernelGGL(k_rope_kv_append, dim3((pairs + 255) / 256), dim3(256), 0, st, q, k, v, kcache, vcache, rope,
-                       meta, pos, dim, kv_dim, hs, max_t);
+    hipLaunchKernelGGL(k_rope_kv_append, dim3((pairs + 255) / 256, T), dim3(256), 0, st, q, k, v, kcache, vcache,
+                       rope, meta, pos, dim, kv_dim, hs, max_t, stride);
     return check_launch("rope_kv_append");
 }
 
@@ -236,10 +241,10 @@ bool attention_exact_ok(int max_t) {
 
 int launch_attention_exact(const float* q, const float* kcache, const float* vcache, float* out, float* scores,
                            int S, const int* meta, int pos, int n_heads, int n_kv_heads, int hs, int max_t,
-                           hipStream_t st) {
+                           hipStream_t st, int T, int q_stride) {
     (void)S;
-    if (!attention_shape_ok(n_heads, n_kv_heads, hs) || max_t <= 0 || !attention_exact_ok(max_t) ||
-        (!meta && (pos < 0 || pos >= max_t))) {
+    if (!attention_shape_ok(n_heads, n_kv_heads, hs) || max_t <= 0 || !attention_exact_ok(max_t) || T < 1 ||
+        (!meta && (pos < 0 || pos + T > max_t)) || (meta && T > 1)) {
         set_error("attention: bad shape heads=%d kv_heads=%d hs=%d pos=%d max_t=%d", n_heads, n_kv_heads, hs, pos,
                   max_t);
         return L2Q_ERR_ARG;
@@ -247,13 +252,13 @@ int launch_attention_exact(const float* q, const float* kcache, const float* vca
     const int kv_mul = n_heads / n_kv_heads;
     // persistent score waves over (head, tile) items; a captured graph covers
     // every position the cache can hold, items past pos are not visited
-    const int items = n_heads * ((meta ? max_t : pos + 1) + kScoreTile - 1) / kScoreTile;
+    const int items = n_heads * ((meta ? max_t : pos + T) + kScoreTile - 1) / kScoreTile;
     const int grid = items < kScoreGridMax ? items : kScoreGridMax;
-    hipLaunchKernelGGL(k_attn_scores, dim3(grid), dim3(kScoreThreads), attn_scores_lds_bytes(hs), st, q, kcache,
-                       scores, meta, pos, kv_mul, n_heads, hs, max_t);
+    hipLaunchKernelGGL(k_attn_scores, dim3(grid, T), dim3(kScoreThreads), attn_scores_lds_bytes(hs), st, q, kcache,
+                       scores, meta, pos, kv_mul, n_heads, hs, max_t, q_stride);
     int rc = check_launch("attention_scores");
     if (rc) return rc;
-    hipLaunchKernelGGL(k_attn_softmax_v, dim3(n_heads, (hs + kVDims - 1) / kVDims), dim3(kAttnThreads),
+    hipLaunchKernelGGL(k_attn_softmax_v, dim3(n_heads, (hs + kVDims - 1) / kVDims, T), dim3(kAttnThreads),
                        attn_v_lds_bytes(max_t), st, scores, vcache, out, meta, pos, kv_mul, hs, max_t);
     return check_launch("attention_softmax_v");
 }
@@ -293,6 +298,54 @@ int launch_attention_kv8(const float* q, const int8_t* k8, const int8_t* v8, con
     hipLaunchKernelGGL(k_attn8_softmax_v, dim3(n_heads), dim3(kAttnThreads), attn8_v_lds_bytes(max_t), st, scores,
                        v8, vs, out, meta, pos, kv_mul, hs, max_t);
     return check_launch("attention_kv8_softmax_v");
+}
+
+// ---------------------------------------------------------------------------
+// batched prefill
+
+int launch_pf_prep(int bits, int group, const int8_t* xq, const float* xs, int K, int T, int8_t* xqp, int* sq,
+                   float* xt, hipStream_t st) {
+    if (T < 1 || K <= 0 || (group != 32 && group != 64) || K % group || (bits != 4 && bits != 8)) {
+        set_error("prefill prep: bad K=%d T=%d group=%d bits=%d", K, T, group, bits);
+        return L2Q_ERR_ARG;
+    }
+    const int n = T * (K / group), blocks = (n + 255) / 256;
+    if (bits == 4 && group == 64) hipLaunchKernelGGL((k_pf_prep<4, 64>), dim3(blocks), dim3(256), 0, st, xq, xs, K, T, xqp, sq, xt);
+    if (bits == 4 && group == 32) hipLaunchKernelGGL((k_pf_prep<4, 32>), dim3(blocks), dim3(256), 0, st, xq, xs, K, T, xqp, sq, xt);
+    if (bits == 8 && group == 64) hipLaunchKernelGGL((k_pf_prep<8, 64>), dim3(blocks), dim3(256), 0, st, xq, xs, K, T, xqp, sq, xt);
+    if (bits == 8 && group == 32) hipLaunchKernelGGL((k_pf_prep<8, 32>), dim3(blocks), dim3(256), 0, st, xq, xs, K, T, xqp, sq, xt);
+    return check_launch("prefill_prep");
+}
+
+int launch_pf_gemm(int bits, int group, const void* w, const float* ws, int rows, int cols, const int8_t* xqp,
+                   const float* xs, const int* sq, const float* xt, int T, float* out, int ldo, hipStream_t st) {
+    if (T < 1 || rows < 1 || cols <= 0 || (group != 32 && group != 64) || cols % group || (bits != 4 && bits != 8) ||
+        cols % 8 || ldo < rows) {
+        set_error("prefill gemm: bad rows=%d cols=%d T=%d group=%d bits=%d", rows, cols, T, group, bits);
+        return L2Q_ERR_ARG;
+    }
+    const long long waves = (long long)((rows + kPfTile - 1) / kPfTile) * ((T + kPfTile - 1) / kPfTile);
+    const dim3 grid((unsigned)((waves + kPfWaves - 1) / kPfWaves)), block(kPfWaves * L2Q_WAVE);
+    const uint8_t* wb = static_cast<const uint8_t*>(w);
+    if (bits == 4 && group == 64) hipLaunchKernelGGL((k_pf_gemm<4, 64>), grid, block, 0, st, wb, ws, rows, cols, xqp, xs, sq, xt, T, out, ldo);
+    if (bits == 4 && group == 32) hipLaunchKernelGGL((k_pf_gemm<4, 32>), grid, block, 0, st, wb, ws, rows, cols, xqp, xs, sq, xt, T, out, ldo);
+    if (bits == 8 && group == 64) hipLaunchKernelGGL((k_pf_gemm<8, 64>), grid, block, 0, st, wb, ws, rows, cols, xqp, xs, sq, xt, T, out, ldo);
+    if (bits == 8 && group == 32) hipLaunchKernelGGL((k_pf_gemm<8, 32>), grid, block, 0, st, wb, ws, rows, cols, xqp, xs, sq, xt, T, out, ldo);
+    return check_launch("prefill_gemm");
+}
+
+int launch_pf_embed(const float* emb, const int* tokens, float* x, int dim, int T, hipStream_t st) {
+    hipLaunchKernelGGL(k_pf_embed, dim3((dim + 255) / 256, T), dim3(256), 0, st, emb, tokens, x, dim);
+    return check_launch("prefill_embed");
+}
+
+int launch_pf_swiglu_quant(const float* h13, int n, int T, int group, int8_t* xq, float* xs, hipStream_t st) {
+    if (n <= 0 || n % group || (group != 32 && group != 64)) { set_error("prefill swiglu: bad n=%d", n); return L2Q_ERR_ARG; }
+    const size_t total = (size_t)T * n;
+    const unsigned blocks = (unsigned)((total + 255) / 256);
+    if (group == 32) hipLaunchKernelGGL(k_pf_swiglu_quant<32>, dim3(blocks), dim3(256), 0, st, h13, n, T, xq, xs);
+    else hipLaunchKernelGGL(k_pf_swiglu_quant<64>, dim3(blocks), dim3(256), 0, st, h13, n, T, xq, xs);
+    return check_launch("prefill_swiglu_quant");
 }
 
 int launch_argmax(const float* v, int n, int* out, hipStream_t st) {
@@ -417,6 +470,27 @@ int l2q_attention(const float* q, const float* kcache, const float* vcache, floa
     if (rc) return rc;
     return launch_attention_exact(q, kcache, vcache, out, scratch, score_splits(pos + 1), nullptr, pos, n_heads,
                                   n_kv_heads, head_size, max_t, (hipStream_t)stream);
+}
+
+int l2q_gemm_q(int wbits, float* out, const int8_t* xq, const float* xs, const void* w, const float* ws, int rows,
+               int cols, int group, int T, void* stream) {
+    if ((wbits != 4 && wbits != 8) || (group != 32 && group != 64) || rows < 1 || T < 1 || cols <= 0 ||
+        cols % group || cols % 8 || !out || !xq || !xs || !w || !ws) {
+        set_error("gemm: bad arguments bits=%d rows=%d cols=%d group=%d T=%d", wbits, rows, cols, group, T);
+        return L2Q_ERR_ARG;
+    }
+    // scratch: permuted activations, then sum(q) and bias terms per group
+    const size_t nbt = (size_t)T * (cols / group);
+    const size_t words = ((size_t)T * cols + 3) / 4 + 2 * nbt;
+    float* scratch = nullptr;
+    int rc = attn_scratch(words, &scratch);
+    if (rc) return rc;
+    int8_t* xqp = reinterpret_cast<int8_t*>(scratch);
+    int* sq = reinterpret_cast<int*>(scratch + ((size_t)T * cols + 3) / 4);
+    float* xt = reinterpret_cast<float*>(sq + nbt);
+    hipStream_t st = (hipStream_t)stream;
+    if ((rc = launch_pf_prep(wbits, group, xq, xs, cols, T, xqp, sq, xt, st))) return rc;
+    return launch_pf_gemm(wbits, group, w, ws, rows, cols, xqp, xs, sq, xt, T, out, rows, st);
 }
 
 int l2q_kv8_append(const float* k, const float* v, int8_t* kcache8, int8_t* vcache8, float* kscale, float* vscale,

@@ -43,12 +43,14 @@ SIGNATURES = {
     "l2q_engine_forward": (I, [P, I, I, P]),
     "l2q_engine_forward_argmax": (I, [P, I, I, C.POINTER(I)]),
     "l2q_engine_forward_debug": (I, [P, I, I, P, P]),
+    "l2q_engine_prefill": (I, [P, P, I, I, P]),
     "l2q_engine_time_steps": (I, [P, P, I, I, C.POINTER(C.c_double)]),
     "l2q_engine_device_bytes": (C.c_size_t, [P]),
     "l2q_engine_destroy": (None, [P]),
     "l2q_quantize_act": (I, [P, I, I, P, P, P]),
     "l2q_gemv_q8": (I, [P, P, P, P, P, I, I, I, P, P]),
     "l2q_gemv_q4": (I, [P, P, P, P, P, I, I, I, P, P]),
+    "l2q_gemm_q": (I, [I, P, P, P, P, P, I, I, I, I, P]),
     "l2q_unbias_q8": (I, [P, P, C.c_size_t, P]),
     "l2q_rmsnorm_quant": (I, [P, P, P, P, I, I, P, P, P]),
     "l2q_swiglu_quant": (I, [P, P, I, I, P, P, P, P]),

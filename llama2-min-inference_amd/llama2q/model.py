@@ -31,6 +31,14 @@ class Engine:
         abi.call("l2q_engine_forward", self._h, token, pos, self._logits.ctypes.data)
         return self._logits.copy()
 
+    def prefill(self, tokens, pos0: int, logits: bool = True):
+        """Positions pos0.. take `tokens` in one batched pass; the logits of
+        the last position (or None)."""
+        t = np.ascontiguousarray(tokens, dtype=np.int32)
+        abi.call("l2q_engine_prefill", self._h, t.ctypes.data, t.size, pos0,
+                 self._logits.ctypes.data if logits else None)
+        return self._logits.copy() if logits else None
+
     def step(self, token: int, pos: int) -> None:
         """One step without fetching logits (prompt forcing)."""
         abi.call("l2q_engine_forward", self._h, token, pos, None)
