@@ -324,13 +324,25 @@ int launch_pf_gemm(int bits, int group, const void* w, const float* ws, int rows
         set_error("prefill gemm: bad rows=%d cols=%d T=%d group=%d bits=%d", rows, cols, T, group, bits);
         return L2Q_ERR_ARG;
     }
-    const long long waves = (long long)((rows + kPfTile - 1) / kPfTile) * ((T + kPfTile - 1) / kPfTile);
+    // token tiles per wave: as many as keep >= 2048 waves in the grid (weight
+    // reuse in registers vs parallelism)
+    const long long nrt = (rows + kPfTile - 1) / kPfTile, ntt = (T + kPfTile - 1) / kPfTile;
+    int NT = 1;
+    if (nrt * ((ntt + 3) / 4) >= 2048) NT = 4;
+    else if (nrt * ((ntt + 1) / 2) >= 2048) NT = 2;
+    const long long waves = nrt * ((ntt + NT - 1) / NT);
     const dim3 grid((unsigned)((waves + kPfWaves - 1) / kPfWaves)), block(kPfWaves * L2Q_WAVE);
     const uint8_t* wb = static_cast<const uint8_t*>(w);
-    if (bits == 4 && group == 64) hipLaunchKernelGGL((k_pf_gemm<4, 64>), grid, block, 0, st, wb, ws, rows, cols, xqp, xs, sq, xt, T, out, ldo);
-    if (bits == 4 && group == 32) hipLaunchKernelGGL((k_pf_gemm<4, 32>), grid, block, 0, st, wb, ws, rows, cols, xqp, xs, sq, xt, T, out, ldo);
-    if (bits == 8 && group == 64) hipLaunchKernelGGL((k_pf_gemm<8, 64>), grid, block, 0, st, wb, ws, rows, cols, xqp, xs, sq, xt, T, out, ldo);
-    if (bits == 8 && group == 32) hipLaunchKernelGGL((k_pf_gemm<8, 32>), grid, block, 0, st, wb, ws, rows, cols, xqp, xs, sq, xt, T, out, ldo);
+#define L2Q_PF_GEMM(B_, G_, N_) \
+    hipLaunchKernelGGL((k_pf_gemm<B_, G_, N_>), grid, block, 0, st, wb, ws, rows, cols, xqp, xs, sq, xt, T, out, ldo)
+#define L2Q_PF_GEMM_NT(B_, G_) \
+    do { if (NT == 4) L2Q_PF_GEMM(B_, G_, 4); else if (NT == 2) L2Q_PF_GEMM(B_, G_, 2); else L2Q_PF_GEMM(B_, G_, 1); } while (0)
+    if (bits == 4 && group == 64) L2Q_PF_GEMM_NT(4, 64);
+    if (bits == 4 && group == 32) L2Q_PF_GEMM_NT(4, 32);
+    if (bits == 8 && group == 64) L2Q_PF_GEMM_NT(8, 64);
+    if (bits == 8 && group == 32) L2Q_PF_GEMM_NT(8, 32);
+#undef L2Q_PF_GEMM_NT
+#undef L2Q_PF_GEMM
     return check_launch("prefill_gemm");
 }
 

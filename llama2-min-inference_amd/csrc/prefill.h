@@ -78,9 +78,21 @@ __device__ __forceinline__ void pf_load_a(const uint8_t* wrow, int b, int kq, in
 }
 
 // Batched GEMM with the exact ordered fold: out[t][r] for t < T, r < rows.
-// Wave (row tile, token tile); token tiles of a row tile are adjacent
-// waves, so they share the weight tile through L2.
-template <int BITS, int G>
+// Wave (row tile, token group of NT token tiles): the weight tile of a
+// group is loaded once for NT MFMAs; the operands of group b+1 are loaded
+// while group b is folded (two register sets, the loop unrolled by two so
+// neither set is copied).  Waves of one row tile are adjacent, so they share
+// the weight tile through L2.
+template <int BITS, int G, int NT>
+struct PfOperands {
+    int a[G / 16];
+    int bx[NT][G / 16];
+    float ws4[4];
+    float gxs[NT], gxt[NT];
+    int gsq[NT];
+};
+
+template <int BITS, int G, int NT>
 __global__ __launch_bounds__(kPfWaves * L2Q_WAVE) void k_pf_gemm(
     const uint8_t* __restrict__ w, const float* __restrict__ ws, int rows, int cols,
     const int8_t* __restrict__ xqp, const float* __restrict__ xs, const int* __restrict__ sq,
@@ -88,50 +100,79 @@ __global__ __launch_bounds__(kPfWaves * L2Q_WAVE) void k_pf_gemm(
     const int lane = threadIdx.x & (L2Q_WAVE - 1);
     const int gw = blockIdx.x * kPfWaves + threadIdx.x / L2Q_WAVE;
     const int ntt = (T + kPfTile - 1) / kPfTile;
+    const int ntg = (ntt + NT - 1) / NT;
     const int nrt = (rows + kPfTile - 1) / kPfTile;
-    if (gw >= nrt * ntt) return;   // wave-uniform: no barrier follows
-    const int rt = gw / ntt, tt = gw - rt * ntt;
+    if (gw >= nrt * ntg) return;   // wave-uniform: no barrier follows
+    const int rt = gw / ntg, tg = gw - rt * ntg;
     const int nb = cols / G;
     const int kq = lane / 16;
-    const int ra = min(rt * kPfTile + lane % 16, rows - 1);       // A row of this lane
-    const int tb = min(tt * kPfTile + lane % 16, T - 1);          // B token of this lane / D token
-    const uint8_t* wrow = w + (size_t)ra * cols * BITS / 8;
-    const int8_t* xrow = xqp + (size_t)tb * cols;
-    int rd[4];                                                    // D rows of this lane
-#pragma unroll
-    for (int i = 0; i < 4; i++) rd[i] = min(rt * kPfTile + 4 * kq + i, rows - 1);
-    float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
     constexpr int CH = G / 4;
-#pragma unroll 4
-    for (int b = 0; b < nb; b++) {
-        int a[G / 16];
-        pf_load_a<BITS, G>(wrow, b, kq, a);
-        const int* xp = reinterpret_cast<const int*>(xrow + (size_t)b * G + kq * CH);
-        v4i32 d4 = {0, 0, 0, 0};
-        if constexpr (G == 64) {
-            const v4i32 av = {a[0], a[1], a[2], a[3]};
-            const v4i32 bv = {xp[0], xp[1], xp[2], xp[3]};
-            d4 = __builtin_amdgcn_mfma_i32_16x16x64_i8(av, bv, d4, 0, 0, 0);
-        } else {
-            const long av = (long)(unsigned)a[0] | ((long)a[1] << 32);
-            const long bv = (long)(unsigned)xp[0] | ((long)xp[1] << 32);
-            d4 = __builtin_amdgcn_mfma_i32_16x16x32_i8(av, bv, d4, 0, 0, 0);
-        }
-        const size_t gi = (size_t)tb * nb + b;
-        const float gxs = xs[gi], gxt = xt[gi];
-        const int gsq = sq[gi];
+    const int ra = min(rt * kPfTile + lane % 16, rows - 1);       // A row of this lane
+    const uint8_t* wrow = w + (size_t)ra * cols * BITS / 8;
+    int tb[NT];                                                   // B / D token of this lane per tile
 #pragma unroll
-        for (int i = 0; i < 4; i++) {
-            const int d = BITS == 4 ? d4[i] >> 4 : d4[i];   // exact: the x16 dot is a multiple of 16
-            acc[i] = __builtin_fmaf(ws[(size_t)rd[i] * nb + b], group_term(gxs, gxt, d, gsq), acc[i]);
+    for (int j = 0; j < NT; j++) tb[j] = min((tg * NT + j) * kPfTile + lane % 16, T - 1);
+    size_t wsrow[4];                                              // D rows of this lane
+#pragma unroll
+    for (int i = 0; i < 4; i++) wsrow[i] = (size_t)min(rt * kPfTile + 4 * kq + i, rows - 1) * nb;
+
+    auto load = [&](int b, PfOperands<BITS, G, NT>& o) {
+        pf_load_a<BITS, G>(wrow, b, kq, o.a);
+#pragma unroll
+        for (int j = 0; j < NT; j++) {
+            const int* xp = reinterpret_cast<const int*>(xqp + (size_t)tb[j] * cols + (size_t)b * G + kq * CH);
+#pragma unroll
+            for (int v = 0; v < G / 16; v++) o.bx[j][v] = xp[v];
+            const size_t gi = (size_t)tb[j] * nb + b;
+            o.gxs[j] = xs[gi];
+            o.gxt[j] = xt[gi];
+            o.gsq[j] = sq[gi];
         }
+#pragma unroll
+        for (int i = 0; i < 4; i++) o.ws4[i] = ws[wsrow[i] + b];
+    };
+    float acc[NT][4];
+#pragma unroll
+    for (int j = 0; j < NT; j++)
+#pragma unroll
+        for (int i = 0; i < 4; i++) acc[j][i] = 0.0f;
+    auto fold = [&](const PfOperands<BITS, G, NT>& o) {
+#pragma unroll
+        for (int j = 0; j < NT; j++) {
+            v4i32 d4 = {0, 0, 0, 0};
+            if constexpr (G == 64) {
+                const v4i32 av = {o.a[0], o.a[1], o.a[2], o.a[3]};
+                const v4i32 bv = {o.bx[j][0], o.bx[j][1], o.bx[j][2], o.bx[j][3]};
+                d4 = __builtin_amdgcn_mfma_i32_16x16x64_i8(av, bv, d4, 0, 0, 0);
+            } else {
+                const long av = (long)(unsigned)o.a[0] | ((long)o.a[1] << 32);
+                const long bv = (long)(unsigned)o.bx[j][0] | ((long)o.bx[j][1] << 32);
+                d4 = __builtin_amdgcn_mfma_i32_16x16x32_i8(av, bv, d4, 0, 0, 0);
+            }
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const int d = BITS == 4 ? d4[i] >> 4 : d4[i];   // exact: the x16 dot is a multiple of 16
+                acc[j][i] = __builtin_fmaf(o.ws4[i], group_term(o.gxs[j], o.gxt[j], d, o.gsq[j]), acc[j][i]);
+            }
+        }
+    };
+    PfOperands<BITS, G, NT> s0, s1;
+    load(0, s0);
+    for (int b = 0; b < nb; b += 2) {
+        load(min(b + 1, nb - 1), s1);
+        fold(s0);
+        load(min(b + 2, nb - 1), s0);
+        if (b + 1 < nb) fold(s1);
     }
-    const int t = tt * kPfTile + lane % 16;
-    if (t < T) {
 #pragma unroll
-        for (int i = 0; i < 4; i++) {
-            const int r = rt * kPfTile + 4 * kq + i;
-            if (r < rows) out[(size_t)t * ldo + r] = acc[i];
+    for (int j = 0; j < NT; j++) {
+        const int t = (tg * NT + j) * kPfTile + lane % 16;
+        if (t < T) {
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const int r = rt * kPfTile + 4 * kq + i;
+                if (r < rows) out[(size_t)t * ldo + r] = acc[j][i];
+            }
         }
     }
 }

@@ -62,8 +62,23 @@ static void generate(decoder* d, l2q_tokenizer* tk, const char* prompt, int step
     int n = tok_encode(tk, prompt, 1, 0, toks);
     if (n < 1) die("something is wrong, expected at least 1 prompt token", NULL);
     long start = 0;
-    int token = toks[0], pos = 0, next;
-    while (pos < steps) {
+    int token = toks[0], pos = 0, next, pos_start = 0, done = 0;
+    /* the forced prompt positions in one batched pass (the same KV cache and
+     * text as forcing them one by one, runq.c:695-700), then the loop */
+    const int npf = n - 1 < steps ? n - 1 : steps;
+    if (npf > 1) {
+        if (l2q_engine_prefill(d->engine, toks, npf, 0, NULL) != L2Q_OK) die("prefill failed", l2q_last_error());
+        for (; pos < npf; pos++) {
+            next = toks[pos + 1];
+            if (next == 1) { done = 1; pos++; break; }
+            tok_print_piece(tok_decode(tk, token, next));
+            token = next;
+        }
+        fflush(stdout);
+        start = time_in_ms();
+        pos_start = pos;
+    }
+    while (!done && pos < steps) {
         int forced = pos < n - 1;
         next = step(d, token, pos, !forced);
         if (forced) next = toks[pos + 1];
@@ -72,12 +87,12 @@ static void generate(decoder* d, l2q_tokenizer* tk, const char* prompt, int step
         tok_print_piece(tok_decode(tk, token, next));
         fflush(stdout);
         token = next;
-        if (start == 0) start = time_in_ms();
+        if (start == 0) { start = time_in_ms(); pos_start = 1; }
     }
     printf("\n");
-    if (pos > 1) {
+    if (pos > pos_start && start != 0) {
         long end = time_in_ms();
-        fprintf(stderr, "achieved tok/s: %f\n", (pos - 1) / (double)(end - start) * 1000);
+        fprintf(stderr, "achieved tok/s: %f\n", (pos - pos_start) / (double)(end - start) * 1000);
     }
     free(toks);
 }

@@ -125,3 +125,30 @@ def test_int4_g64_7b_layers_debug(gpu_lib):
         np.testing.assert_array_equal(lg_g, lg_o)
         token = int(np.argmax(lg_o))
     eng.close()
+
+
+@pytest.mark.parametrize("prompt,steps", [("Once upon a time", 48), ("a", 20)])
+def test_runner_output_equals_reference_runq(gpu_lib, c1_q8, tmp_path, prompt, steps):
+    """The drop-in runner against the reference's own runq executable
+    (compiled from v1-int8-vnni/runq.c by oracle/Makefile) on the same
+    checkpoint, tokenizer and flags, greedy: identical generated text.  The
+    runner prefills the forced prompt positions in one batched pass; runq
+    forces them one by one."""
+    import subprocess
+    from conftest import PKG, REPO
+    runq = os.path.join(REPO, "oracle", "_ref", "runq")
+    if not os.path.exists(runq):
+        pytest.skip("oracle/_ref/runq not built")
+    model, tok = str(tmp_path / "m.bin"), str(tmp_path / "tok.bin")
+    c1_q8.save(model)
+    pieces, scores = host.synth_tokenizer_pieces(32000)
+    host.write_tokenizer(tok, pieces, scores)
+    args = [model, "-z", tok, "-n", str(steps), "-t", "0", "-i", prompt]
+    ref = subprocess.run([runq] + args, capture_output=True, text=True, timeout=300,
+                         env={**os.environ, "OMP_NUM_THREADS": "4"})
+    got = subprocess.run([os.path.join(PKG, "build", "llama2q_run")] + args, capture_output=True, text=True,
+                         timeout=300)
+    assert ref.returncode == 0, ref.stderr
+    assert got.returncode == 0, got.stderr
+    assert got.stdout == ref.stdout
+    assert "achieved tok/s" in got.stderr
