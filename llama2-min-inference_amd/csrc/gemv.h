@@ -79,7 +79,10 @@ struct GemvArgs {
 
 
 constexpr int kSweepBytes = 16 * L2Q_WAVE;   // one 128-bit load per lane
-constexpr int kGemvUnit = 2;                 // rows per unit (PR): (even, odd) pairs for the epilogues
+// Rows per unit (PR): (even, odd) pairs for the pair epilogues; single rows
+// for plain stores of long rows (>= 5 sweeps), whose two-row unit would
+// crowd the registers and leave a wave one unit with nothing to overlap.
+__host__ __device__ constexpr int gemv_unit_rows(int NS, int EPI) { return EPI == 0 && NS >= 5 ? 1 : 2; }
 
 __host__ __device__ constexpr int gemv_sweeps(int bits, int cols) { return (cols * bits / 8 + kSweepBytes - 1) / kSweepBytes; }
 
@@ -543,7 +546,7 @@ template <int BITS, int G, int NS, int PRO, int EPI, int PR>
 __global__ __launch_bounds__(gemv_waves(NS) * L2Q_WAVE) void k_gemv(GemvArgs a) {
     constexpr int WAVES = gemv_waves(NS);
     constexpr int THREADS = WAVES * L2Q_WAVE;
-    static_assert(PR == 2, "fold batches hold whole units of two rows");
+    static_assert(PR == gemv_unit_rows(NS, EPI), "unit size");
     using C = Chunk<BITS, G>;
     constexpr int NSS = gemv_scale_sweeps(BITS, G, NS);
     constexpr bool ACTL = gemv_act_lds(NS);           // activations read from LDS per chunk

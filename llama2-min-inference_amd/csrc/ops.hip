@@ -68,7 +68,7 @@ constexpr size_t kGemvMaxLds = 160 * 1024;   // gfx950 LDS per workgroup
 
 template <int BITS, int G, int NS, int PRO, int EPI>
 static int go_gemv(const GemvArgs& a, hipStream_t st) {
-    constexpr int PR = kGemvUnit;
+    constexpr int PR = gemv_unit_rows(NS, EPI);
     const size_t lds = gemv_lds_bytes(PRO, a.cols, G, BITS, PR);
     constexpr int W = gemv_waves(NS);
     const void* fn = reinterpret_cast<const void*>(&k_gemv<BITS, G, NS, PRO, EPI, PR>);
@@ -131,7 +131,7 @@ int launch_gemv_fused(int bits, int group, int pro, int epi, const GemvArgs& a, 
     }
     if (pro != kPreq && !a.x_in && !(pro == kNorm && a.emb)) { set_error("gemv: null prologue input"); return L2Q_ERR_ARG; }
     if (pro == kNorm && (!a.norm_w || (a.emb && !a.meta))) { set_error("gemv: null norm weight / meta"); return L2Q_ERR_ARG; }
-    if (gemv_lds_bytes(pro, a.cols, group, bits, kGemvUnit) > kGemvMaxLds) {
+    if (gemv_lds_bytes(pro, a.cols, group, bits, 2) > kGemvMaxLds) {
         set_error("gemv: cols=%d needs too much LDS", a.cols);
         return L2Q_ERR_ARG;
     }
