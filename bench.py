@@ -117,19 +117,28 @@ def time_attention(torch, abi, host, ctx, mode, reps=50, n_heads=32, hs=128, max
         k = torch.randn(n_heads * max_t * hs, device="cuda", generator=g)
         v = torch.randn(n_heads * max_t * hs, device="cuda", generator=g)
         args = (q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr())
-        fn, nbytes = "l2q_attention" if mode == "exact" else "l2q_attention_split", 2 * ctx * n_heads * hs * 4
+        fn, nbytes = "l2q_attention_ex" if mode == "exact" else "l2q_attention_split", 2 * ctx * n_heads * hs * 4
     nbytes += 2 * n_heads * hs * 4
+    # exact: the engine's K layout and choice of kernels
+    extra = (abi.L2Q_ATTN_K_INTERLEAVED,) if mode == "exact" else ()
 
     def launch():
-        abi.call(fn, *args, ctx - 1, n_heads, n_heads, hs, max_t, st.cuda_stream)
+        abi.call(fn, *args, ctx - 1, n_heads, n_heads, hs, max_t, *extra, torch.cuda.current_stream().cuda_stream)
 
     for _ in range(3):
         launch()
     torch.cuda.synchronize()
+    # the launches are replayed from a captured graph: a short attention
+    # takes less time than one launch through ctypes
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        for _ in range(reps):
+            launch()
+    graph.replay()
+    torch.cuda.synchronize()
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     e0.record(st)
-    for _ in range(reps):
-        launch()
+    graph.replay()
     e1.record(st)
     e1.synchronize()
     return e0.elapsed_time(e1) / reps, nbytes

@@ -218,6 +218,22 @@ int l2q_attention(const float* q, const float* kcache, const float* vcache,
                   float* out, int pos, int n_heads, int n_kv_heads,
                   int head_size, int max_t, void* stream);
 
+/* l2q_attention with options (no reference counterpart: the engine's own
+ * cache layout and the choice of kernels, for tests and measurements).
+ * L2Q_ATTN_K_INTERLEAVED: kcache in the engine's column-interleaved layout
+ * [n_kv_heads][head_size/4][max_t][4] (float4 column f of consecutive
+ * positions contiguous) instead of [n_kv_heads][max_t][head_size].
+ * L2Q_ATTN_ONE_KERNEL / L2Q_ATTN_TWO_KERNELS force the single-kernel form
+ * (head sizes 48, 64, 128) or the scores + softmax/p*V pair; by default the
+ * single kernel serves contexts up to a measured threshold.  Every form
+ * gives the same bits. */
+#define L2Q_ATTN_K_INTERLEAVED 1
+#define L2Q_ATTN_ONE_KERNEL 2
+#define L2Q_ATTN_TWO_KERNELS 4
+int l2q_attention_ex(const float* q, const float* kcache, const float* vcache,
+                     float* out, int pos, int n_heads, int n_kv_heads,
+                     int head_size, int max_t, int flags, void* stream);
+
 /* The same attention split over the context (flash-decoding: per-split
  * online softmax, then a merge), for throughput; float results agree with
  * l2q_attention to ~1e-6 relative, not bit for bit.

@@ -167,4 +167,13 @@ __device__ __forceinline__ int dot8_q4_x16(unsigned w, int xe, int xo, int c) {
     return dot4(hi, xo, dot4(lo, xe, c));
 }
 
+// Index of element i of head g's key at position t in an fp32 K cache:
+// row layout [n_kv][max_t][hs] (the op ABI's) or the engine's
+// column-interleaved layout [n_kv][hs/4][max_t][4], in which float4 column
+// f of consecutive positions is contiguous, so a wave that reads one
+// position per lane reads one coalesced KiB per column.
+__host__ __device__ inline size_t k_index(int il, int g, int t, int i, int hs, int max_t) {
+    return il ? (((size_t)g * (hs >> 2) + (i >> 2)) * max_t + t) * 4 + (i & 3) : ((size_t)g * max_t + t) * hs + i;
+}
+
 }  // namespace l2q

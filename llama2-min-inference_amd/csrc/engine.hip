@@ -9,14 +9,18 @@
 //   w2_w/s     [L][d][...]
 //   wcls_w/s   [V][...]
 //   INT8 weights are stored signed (the file's +128 bias removed at load).
-//   kcache/vcache fp32 [L][n_kv_heads][max_t][hs]
+//   vcache     fp32 [L][n_kv_heads][max_t][hs]
+//   kcache     fp32 [L][n_kv_heads][hs/4][max_t][4]: float4 columns of consecutive
+//              positions contiguous (k_index), so the attention, one position per
+//              lane, reads K with coalesced loads
 // Concatenating wq|wk|wv and interleaving w1/w3 turns 5 GEMV launches per
 // layer into 2 with 12288- and 22016-row grids at the 7B shape, and lets the
 // SwiGLU run in the GEMV's epilogue.
 //
-// A layer is six launches (runq.c:335-415):
+// A layer is five launches (runq.c:335-415):
 //   QKV   residual add + RMSNorm + quantize prologue, RoPE + KV append epilogue
-//   attention scores, attention softmax + p*V        (exact order, two kernels)
+//   attention scores, softmax, p*V in the exact order: one kernel up to
+//         attention_fused_max() positions, two (scores; softmax + p*V) beyond
 //   wo    quantize prologue
 //   W13   residual add + RMSNorm + quantize prologue, SwiGLU epilogue
 //   W2    quantize prologue
@@ -44,8 +48,10 @@ struct l2q_engine {
     int flags;               // L2Q_ENGINE_* options
     int device;
     hipStream_t stream = nullptr;
-    hipGraph_t graph = nullptr, graph_am = nullptr;
-    hipGraphExec_t exec = nullptr, exec_am = nullptr;
+    // captured steps [argmax][long context]: the long-context graphs (two-kernel
+    // attention) exist only when the cache outgrows attention_fused_max()
+    hipGraph_t graph[2][2] = {};
+    hipGraphExec_t exec[2][2] = {};
     hipEvent_t ev0 = nullptr, ev1 = nullptr;
     char* warena = nullptr;
     char* sarena = nullptr;
@@ -97,7 +103,7 @@ struct Arena {
 // Enqueue one decode step on `st` (captured or eager).  If `dbg_x` is set
 // (eager diagnostic mode) the residual stream after the embedding and after
 // each layer is copied to it.
-int enqueue_step(l2q_engine* e, hipStream_t st, float* dbg_x, float* dbg_tmp, bool argmax) {
+int enqueue_step(l2q_engine* e, hipStream_t st, float* dbg_x, float* dbg_tmp, bool argmax, bool fused) {
     const l2q_config& c = e->cfg;
     const int d = c.dim, h = c.hidden_dim, kv = e->kv_dim, G = e->G, bits = e->wbits;
     const int qkv_rows = d + 2 * kv;
@@ -122,6 +128,7 @@ int enqueue_step(l2q_engine* e, hipStream_t st, float* dbg_x, float* dbg_tmp, bo
         qa.dim = d; qa.kv_dim = kv; qa.hs = e->hs; qa.max_t = e->max_t;
         qa.kcache = kc; qa.vcache = vc; qa.rope = e->rope;
         const bool kv8 = e->flags & L2Q_ENGINE_KV_INT8;
+        qa.k_il = kv8 ? 0 : 1;
         if (kv8) {   // k, v rows to the staging row, then quantized into the int8 cache
             qa.kcache = e->kvf; qa.vcache = e->kvf + kv; qa.max_t = 1; qa.kv_stage = 1;
         }
@@ -136,7 +143,7 @@ int enqueue_step(l2q_engine* e, hipStream_t st, float* dbg_x, float* dbg_tmp, bo
                                           e->meta, 0, c.n_heads, c.n_kv_heads, e->hs, e->max_t, st);
         } else {
             rc = launch_attention_exact(e->q, kc, vc, e->att, e->scores, e->S, e->meta, 0, c.n_heads,
-                                        c.n_kv_heads, e->hs, e->max_t, st);
+                                        c.n_kv_heads, e->hs, e->max_t, st, 1, 0, fused ? 1 : 0, 1);
         }
         if (rc) return rc;
         // wo: quantize the attention output in the prologue
@@ -194,9 +201,9 @@ int enqueue_step(l2q_engine* e, hipStream_t st, float* dbg_x, float* dbg_tmp, bo
     return L2Q_OK;
 }
 
-int capture(l2q_engine* e, bool argmax, hipGraph_t* g, hipGraphExec_t* ex) {
+int capture(l2q_engine* e, bool argmax, bool fused, hipGraph_t* g, hipGraphExec_t* ex) {
     HIPCHK(hipStreamBeginCapture(e->stream, hipStreamCaptureModeThreadLocal), "hipStreamBeginCapture");
-    int rc = enqueue_step(e, e->stream, nullptr, nullptr, argmax);
+    int rc = enqueue_step(e, e->stream, nullptr, nullptr, argmax, fused);
     hipGraph_t graph = nullptr;
     hipError_t ee = hipStreamEndCapture(e->stream, &graph);
     if (rc) {
@@ -210,10 +217,11 @@ int capture(l2q_engine* e, bool argmax, hipGraph_t* g, hipGraphExec_t* ex) {
 }
 
 void release(l2q_engine* e) {
-    if (e->exec) (void)hipGraphExecDestroy(e->exec);
-    if (e->exec_am) (void)hipGraphExecDestroy(e->exec_am);
-    if (e->graph) (void)hipGraphDestroy(e->graph);
-    if (e->graph_am) (void)hipGraphDestroy(e->graph_am);
+    for (int a = 0; a < 2; a++)
+        for (int l = 0; l < 2; l++) {
+            if (e->exec[a][l]) (void)hipGraphExecDestroy(e->exec[a][l]);
+            if (e->graph[a][l]) (void)hipGraphDestroy(e->graph[a][l]);
+        }
     if (e->ev0) (void)hipEventDestroy(e->ev0);
     if (e->ev1) (void)hipEventDestroy(e->ev1);
     if (e->stream) (void)hipStreamDestroy(e->stream);
@@ -346,8 +354,13 @@ int build(l2q_engine* e, const void* weights, size_t weights_bytes) {
     HIPCHK(hipHostMalloc((void**)&e->h_am, sizeof(int), hipHostMallocDefault), "hipHostMalloc");
     HIPCHK(hipEventCreate(&e->ev0), "hipEventCreate");
     HIPCHK(hipEventCreate(&e->ev1), "hipEventCreate");
-    if ((rc = capture(e, false, &e->graph, &e->exec))) return rc;
-    if ((rc = capture(e, true, &e->graph_am, &e->exec_am))) return rc;
+    // short contexts: one-kernel attention where the head size has it
+    const bool fused = attention_fused_ok(e->hs) && !(e->flags & L2Q_ENGINE_KV_INT8);
+    const bool need_long = !fused || e->max_t > attention_fused_max();
+    for (int a = 0; a < 2; a++) {
+        if (fused && (rc = capture(e, a, true, &e->graph[a][0], &e->exec[a][0]))) return rc;
+        if (need_long && (rc = capture(e, a, false, &e->graph[a][1], &e->exec[a][1]))) return rc;
+    }
     return L2Q_OK;
 }
 
@@ -359,6 +372,13 @@ int check_step(l2q_engine* e, int token, int pos) {
         return L2Q_ERR_STATE;
     }
     return L2Q_OK;
+}
+
+// The captured step for this position: the one-kernel attention graph up to
+// attention_fused_max() positions, the two-kernel one beyond.
+hipGraphExec_t step_graph(const l2q_engine* e, bool argmax, int pos) {
+    hipGraphExec_t const* g = e->exec[argmax ? 1 : 0];
+    return g[0] && (!g[1] || pos + 1 <= attention_fused_max()) ? g[0] : g[1];
 }
 
 int launch_step(l2q_engine* e, int token, int pos, hipGraphExec_t ex, int slot) {
@@ -424,10 +444,10 @@ int prefill_chunk(l2q_engine* e, const int* tokens, int T, int pos0, bool want_l
                        d, e->pf_qkv)))
             return rc;
         if ((rc = launch_rope_kv_append(e->pf_qkv, e->pf_qkv + d, e->pf_qkv + d + kv, kc, vc, e->rope, nullptr,
-                                        pos0, d, kv, e->hs, e->max_t, st, T, qkv_rows)))
+                                        pos0, d, kv, e->hs, e->max_t, st, T, qkv_rows, 1)))
             return rc;
         if ((rc = launch_attention_exact(e->pf_qkv, kc, vc, e->pf_att, e->pf_scores, 0, nullptr, pos0, c.n_heads,
-                                         c.n_kv_heads, e->hs, e->max_t, st, T, qkv_rows)))
+                                         c.n_kv_heads, e->hs, e->max_t, st, T, qkv_rows, -1, 1)))
             return rc;
         // wo
         if ((rc = launch_quantize(e->pf_att, T * d, G, e->pf_xq, e->pf_xs, st))) return rc;
@@ -544,7 +564,7 @@ int l2q_engine_create_ex(const l2q_config* cfg, const void* weights, size_t weig
 int l2q_engine_forward(l2q_engine* e, int token, int pos, float* logits) {
     int rc = check_step(e, token, pos);
     if (rc) return rc;
-    if ((rc = launch_step(e, token, pos, e->exec, 0))) return rc;
+    if ((rc = launch_step(e, token, pos, step_graph(e, false, pos), 0))) return rc;
     if (logits)
         HIPCHK(hipMemcpyAsync(logits, e->logits, (size_t)e->cfg.vocab_size * 4, hipMemcpyDeviceToHost, e->stream),
                "copy logits");
@@ -556,7 +576,7 @@ int l2q_engine_forward_argmax(l2q_engine* e, int token, int pos, int* next) {
     int rc = check_step(e, token, pos);
     if (rc) return rc;
     if (!next) { set_error("engine: null output"); return L2Q_ERR_ARG; }
-    if ((rc = launch_step(e, token, pos, e->exec_am, 0))) return rc;
+    if ((rc = launch_step(e, token, pos, step_graph(e, true, pos), 0))) return rc;
     HIPCHK(hipMemcpyAsync(e->h_am, e->am, sizeof(int), hipMemcpyDeviceToHost, e->stream), "copy argmax");
     HIPCHK(hipStreamSynchronize(e->stream), "hipStreamSynchronize");
     *next = *e->h_am;
@@ -571,7 +591,8 @@ int l2q_engine_forward_debug(l2q_engine* e, int token, int pos, float* x_layers,
     e->h_meta[1] = pos;
     HIPCHK(hipMemcpyAsync(e->meta, e->h_meta, 2 * sizeof(int), hipMemcpyHostToDevice, e->stream), "upload meta");
     std::vector<float> tmp(e->cfg.dim);
-    if ((rc = enqueue_step(e, e->stream, x_layers, tmp.data(), false))) return rc;
+    if ((rc = enqueue_step(e, e->stream, x_layers, tmp.data(), false, step_graph(e, false, pos) == e->exec[0][0])))
+        return rc;
     if (logits)
         HIPCHK(hipMemcpyAsync(logits, e->logits, (size_t)e->cfg.vocab_size * 4, hipMemcpyDeviceToHost, e->stream),
                "copy logits");
@@ -593,7 +614,7 @@ int l2q_engine_time_steps(l2q_engine* e, const int* tokens, int pos0, int n_step
     }
     HIPCHK(hipEventRecord(e->ev0, e->stream), "hipEventRecord");
     for (int i = 0; i < n_steps; i++) {
-        int rc = launch_step(e, tokens[i], pos0 + i, e->exec, i);
+        int rc = launch_step(e, tokens[i], pos0 + i, step_graph(e, false, pos0 + i), i);
         if (rc) return rc;
     }
     HIPCHK(hipEventRecord(e->ev1, e->stream), "hipEventRecord");

@@ -75,6 +75,7 @@ struct GemvArgs {
     float* vcache;
     const float* rope;
     int kv_stage;            // 1: k/v rows written at position 0 (a staging row, max_t 1)
+    int k_il;                // K cache layout (see k_index)
 };
 
 
@@ -778,7 +779,7 @@ __global__ __launch_bounds__(gemv_waves(NS) * L2Q_WAVE) void k_gemv(GemvArgs a) 
                 if (row < a.dim + a.kv_dim) {            // q or k: rotate
                     const float r = odd ? __builtin_fmaf(v0, s, v1 * c) : __builtin_fmaf(v0, c, -(v1 * s));
                     if (row < a.dim) a.out[row] = r;
-                    else a.kcache[((size_t)(e / a.hs) * a.max_t + cpos) * a.hs + (e % a.hs)] = r;
+                    else a.kcache[k_index(a.k_il, e / a.hs, cpos, e % a.hs, a.hs, a.max_t)] = r;
                 } else {                                  // v: appended as is
                     const int ev = row - a.dim - a.kv_dim;
                     a.vcache[((size_t)(ev / a.hs) * a.max_t + cpos) * a.hs + (ev % a.hs)] = sum;

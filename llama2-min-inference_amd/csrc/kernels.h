@@ -124,13 +124,13 @@ __global__ __launch_bounds__(256) void k_swiglu_quant(const float* __restrict__ 
 // The (cos, sin) come from the host-built table (bit-identical to libm).
 // Rotation as a GCC -O3 -march=native build of the reference evaluates it:
 //   v0' = fma(v0, c, -(v1*s)),  v1' = fma(v0, s, v1*c).
-// Cache layout [n_kv_heads][max_t][head_size].
+// Cache layout [n_kv_heads][max_t][head_size] (V; K as k_index with k_il).
 // Workgroup row y handles token y of a batch at position pos + y, its q, k,
 // v rows `stride` floats after the previous token's (prefill).
 __global__ __launch_bounds__(256) void k_rope_kv_append(
     float* __restrict__ q, const float* __restrict__ k, const float* __restrict__ v,
     float* __restrict__ kcache, float* __restrict__ vcache, const float* __restrict__ rope,
-    const int* __restrict__ meta, int pos_arg, int dim, int kv_dim, int hs, int max_t, int stride) {
+    const int* __restrict__ meta, int pos_arg, int dim, int kv_dim, int hs, int max_t, int stride, int k_il) {
     const int p = blockIdx.x * blockDim.x + threadIdx.x;
     const int i = 2 * p;
     if (i >= dim) return;
@@ -149,9 +149,10 @@ __global__ __launch_bounds__(256) void k_rope_kv_append(
     if (i < kv_dim) {
         const int h = i / hs;
         const size_t off = ((size_t)h * max_t + pos) * hs + hd;
+        const size_t ko = k_index(k_il, h, pos, hd, hs, max_t);   // hd even: hd, hd + 1 share a float4
         const float k0 = k[i], k1 = k[i + 1];
-        kcache[off] = __builtin_fmaf(k0, c, -(k1 * s));
-        kcache[off + 1] = __builtin_fmaf(k0, s, k1 * c);
+        kcache[ko] = __builtin_fmaf(k0, c, -(k1 * s));
+        kcache[ko + 1] = __builtin_fmaf(k0, s, k1 * c);
         vcache[off] = v[i];
         vcache[off + 1] = v[i + 1];
     }
@@ -358,7 +359,7 @@ __device__ __forceinline__ float serial_dot(const float* kr, const float* qs, in
 // floats after the previous query's, scores in its own [n_heads][max_t].
 __global__ __launch_bounds__(kScoreThreads) void k_attn_scores(
     const float* __restrict__ q, const float* __restrict__ kcache, float* __restrict__ scores,
-    const int* __restrict__ meta, int pos_arg, int kv_mul, int n_heads, int hs, int max_t, int q_stride) {
+    const int* __restrict__ meta, int pos_arg, int kv_mul, int n_heads, int hs, int max_t, int q_stride, int k_il) {
 #pragma clang fp contract(off)
     extern __shared__ __attribute__((aligned(16))) float sm[];
     const int hsp = hs + 4;
@@ -375,22 +376,28 @@ __global__ __launch_bounds__(kScoreThreads) void k_attn_scores(
         const int h = item / ntile;
         const int t0 = (item - h * ntile) * kScoreTile;
         const int nt = min(kScoreTile, n - t0);
-        const float* kbase = kcache + ((size_t)(h / kv_mul) * max_t + t0) * hs;
+        const int g = h / kv_mul;
         // the tile's loads in batches of 8 float4 per lane, all of a batch in
-        // flight at once (one batch covers a 16 x 128 tile)
+        // flight at once (one batch covers a 16 x 128 tile); consecutive
+        // lanes read consecutive float4 of the cache in either layout
+        auto tile_rc = [&](int f, int& r, int& c4) {
+            if (k_il) { c4 = f / nt; r = f - c4 * nt; }
+            else { r = f / f4; c4 = f - r * f4; }
+        };
         for (int b0 = 0; b0 < nt * f4; b0 += 8 * kScoreThreads) {
             float4 kv[8];
 #pragma unroll
             for (int k = 0; k < 8; k++) {
-                const int f = min(b0 + tid + kScoreThreads * k, nt * f4 - 1);
-                const int r = f / f4, c4 = f - r * f4;
-                kv[k] = *reinterpret_cast<const float4*>(kbase + (size_t)r * hs + 4 * c4);
+                int r, c4;
+                tile_rc(min(b0 + tid + kScoreThreads * k, nt * f4 - 1), r, c4);
+                kv[k] = *reinterpret_cast<const float4*>(kcache + k_index(k_il, g, t0 + r, 4 * c4, hs, max_t));
             }
 #pragma unroll
             for (int k = 0; k < 8; k++) {
                 const int f = b0 + tid + kScoreThreads * k;
                 if (f < nt * f4) {
-                    const int r = f / f4, c4 = f - r * f4;
+                    int r, c4;
+                    tile_rc(f, r, c4);
                     *reinterpret_cast<float4*>(kt + r * hsp + 4 * c4) = kv[k];
                 }
             }
@@ -563,6 +570,156 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn_softmax_v(
         __syncthreads();
     }
     if (wv == 0 && lane < width) out[(size_t)h * hs + d0 + lane] = acc;
+}
+
+// ---------------------------------------------------------------------------
+// Single-query attention in the reference's exact order in ONE kernel
+// (runq.c:367-391, softmax :307-318): the same operations as k_attn_scores
+// + k_attn_softmax_v, bit for bit, without the second launch and the scores'
+// round trip through memory.  Workgroup (head h, slice of kVDims output
+// elements); its 8 waves
+//   scores   one position per thread per round of kAfThreads positions:
+//            the K row straight from the cache into registers (HS/4
+//            float4), q broadcast from LDS, products rounded and added in
+//            index order, / sqrtf(HS); scores kept in registers;
+//   softmax  workgroup max, e_t = exp_runq(s_t - max), the sum of e_t in
+//            position order (one lane, serial_sum), p_t = e_t / sum;
+//   p*V      one lane per output element of the slice, fma(p_t, v_t[i],
+//            acc) in position order (serial_pv) over chunks of kAfChunk
+//            positions, transposed into LDS; the next chunk's loads are in
+//            flight while the current one is folded.
+// Every slice recomputes its head's scores (the K rows come from L2 after
+// the first); the slices of a head are numbered so that they run on one
+// XCD (workgroup id = slice * n_heads + h, ids dealt round-robin over 8
+// XCDs) when n_heads is a multiple of 8.
+constexpr int kAfThreads = 512;
+constexpr int kAfChunk = 512;                                   // V positions per LDS chunk
+constexpr int kAfStride = kAfChunk + 4;                         // LDS row of one element's chunk
+constexpr int kAfVPer = kAfChunk * kVDims / 4 / kAfThreads;     // float4 per thread per chunk
+constexpr int kAfRounds = kScorePer * kAttnThreads / kAfThreads;  // positions per thread (n <= 4096)
+constexpr int kAfDefaultMax = kScorePer * kAttnThreads;         // see attention_fused_max
+__host__ __device__ constexpr size_t attn_fused_lds_bytes(int max_t, int hs) {
+    return ((size_t)(hs + 3) / 4 * 4 + (size_t)(max_t + 3) / 4 * 4 + kRingSlack + 2 * kVDims * kAfStride +
+            kRingSlack + 16) * sizeof(float);
+}
+template <int HS, int KIL>
+__global__ __launch_bounds__(kAfThreads) void k_attn_fused(
+    const float* __restrict__ q, const float* __restrict__ kcache, const float* __restrict__ vcache,
+    float* __restrict__ out, const int* __restrict__ meta, int pos_arg, int kv_mul, int n_heads, int max_t) {
+#pragma clang fp contract(off)
+    static_assert(HS % kVDims == 0 && HS % 8 == 0, "head size");
+    constexpr int F4 = HS / 4;
+    extern __shared__ __attribute__((aligned(16))) float smem[];
+    float* qs = smem;                                        // [HS]
+    float* p = qs + (HS + 3) / 4 * 4;                        // [max_t] scores, e_t, then p_t
+    float* vt = p + (max_t + 3) / 4 * 4 + kRingSlack;        // [2][kVDims][kAfStride]
+    float* red = vt + 2 * kVDims * kAfStride + kRingSlack;   // [8] wave maxima, [8] sum
+    const int h = blockIdx.x % n_heads, d0 = (blockIdx.x / n_heads) * kVDims;
+    const int tid = threadIdx.x, lane = tid & (L2Q_WAVE - 1), wv = tid / L2Q_WAVE;
+    const int n = meta_pos(meta, pos_arg) + 1;
+    const float4* kbase = reinterpret_cast<const float4*>(kcache + (size_t)(h / kv_mul) * max_t * HS);
+    const float* vbase = vcache + (size_t)(h / kv_mul) * max_t * HS + d0;
+    const int nchunks = (n + kAfChunk - 1) / kAfChunk;
+
+    // loads in the order they are needed (they complete in order): q, the
+    // first round's K rows, the first V chunk
+    if (tid < F4) reinterpret_cast<float4*>(qs)[tid] = reinterpret_cast<const float4*>(q + (size_t)h * HS)[tid];
+    float4 kr[F4];
+    auto load_k = [&](int t) {   // column-interleaved: one coalesced KiB per column and wave
+        t = min(t, n - 1);
+#pragma unroll
+        for (int f = 0; f < F4; f++) kr[f] = KIL ? kbase[(size_t)f * max_t + t] : kbase[(size_t)t * F4 + f];
+    };
+    load_k(tid);
+    float4 vr[kAfVPer];
+    auto load_chunk = [&](int c) {
+#pragma unroll
+        for (int k = 0; k < kAfVPer; k++) {
+            const int e = tid + kAfThreads * k;                  // float4 index in the chunk
+            const int r = e / (kVDims / 4), c4 = e % (kVDims / 4);
+            const int t = c * kAfChunk + r;
+            vr[k] = t < n ? *reinterpret_cast<const float4*>(vbase + (size_t)t * HS + 4 * c4)
+                          : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        }
+    };
+    auto store_chunk = [&](int buf) {   // transposed: vt[buf][element][position]
+        float* dst = vt + buf * kVDims * kAfStride;
+#pragma unroll
+        for (int k = 0; k < kAfVPer; k++) {
+            const int e = tid + kAfThreads * k;
+            const int r = e / (kVDims / 4), c4 = e % (kVDims / 4);
+            dst[(4 * c4 + 0) * kAfStride + r] = vr[k].x;
+            dst[(4 * c4 + 1) * kAfStride + r] = vr[k].y;
+            dst[(4 * c4 + 2) * kAfStride + r] = vr[k].z;
+            dst[(4 * c4 + 3) * kAfStride + r] = vr[k].w;
+        }
+    };
+    load_chunk(0);
+    __syncthreads();   // qs
+
+    // scores: round r covers positions r*kAfThreads + tid
+    float s[kAfRounds];
+    float m = -INFINITY;
+    const float4* q4 = reinterpret_cast<const float4*>(qs);
+#pragma unroll
+    for (int r = 0; r < kAfRounds; r++) {
+        s[r] = -INFINITY;
+        if (kAfThreads * r >= n) continue;   // uniform
+        const int t = kAfThreads * r + tid;
+        if (r > 0) load_k(t);
+        float score = 0.0f;
+#pragma unroll
+        for (int f = 0; f < F4; f++) {
+            const float4 qv = q4[f];
+            score = score + qv.x * kr[f].x;
+            score = score + qv.y * kr[f].y;
+            score = score + qv.z * kr[f].z;
+            score = score + qv.w * kr[f].w;
+        }
+        if (t < n) {
+            s[r] = score / sqrtf((float)HS);
+            m = fmaxf(m, s[r]);
+        }
+    }
+    m = group_max<L2Q_WAVE>(m);
+    if (lane == 0) red[wv] = m;
+    __syncthreads();
+    m = red[0];
+#pragma unroll
+    for (int w = 1; w < kAfThreads / L2Q_WAVE; w++) m = fmaxf(m, red[w]);
+    float e[kAfRounds];
+#pragma unroll
+    for (int r = 0; r < kAfRounds; r++) {
+        const int t = kAfThreads * r + tid;
+        e[r] = 0.0f;
+        if (kAfThreads * r < n && t < n) {
+            e[r] = exp_runq(s[r] - m);
+            p[t] = e[r];
+        }
+    }
+    store_chunk(0);
+    __syncthreads();
+    if (tid == 0) red[8] = serial_sum(p, n);
+    __syncthreads();
+    const float sum = red[8];
+#pragma unroll
+    for (int r = 0; r < kAfRounds; r++) {
+        const int t = kAfThreads * r + tid;
+        if (kAfThreads * r < n && t < n) p[t] = e[r] / sum;
+    }
+    __syncthreads();
+
+    float acc = 0.0f;
+    for (int c = 0; c < nchunks; c++) {
+        if (c + 1 < nchunks) load_chunk(c + 1);
+        if (wv == 0 && lane < kVDims) {
+            const int tb = c * kAfChunk;
+            acc = serial_pv(p + tb, vt + (c & 1) * kVDims * kAfStride + lane * kAfStride, min(kAfChunk, n - tb), acc);
+        }
+        if (c + 1 < nchunks) store_chunk((c + 1) & 1);
+        __syncthreads();
+    }
+    if (wv == 0 && lane < kVDims) out[(size_t)h * HS + d0 + lane] = acc;
 }
 
 // ---------------------------------------------------------------------------

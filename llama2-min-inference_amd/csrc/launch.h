@@ -34,7 +34,7 @@ int launch_swiglu_quant(const float* hb, const float* hb2, int n, int group, int
 // T > 1: tokens at positions pos..pos+T-1, their q/k/v rows `stride` floats apart.
 int launch_rope_kv_append(float* q, const float* k, const float* v, float* kcache, float* vcache,
                           const float* rope, const int* meta, int pos, int dim, int kv_dim, int hs,
-                          int max_t, hipStream_t st, int T = 1, int stride = 0);
+                          int max_t, hipStream_t st, int T = 1, int stride = 0, int k_il = 0);
 
 // Split-context attention (tolerance path): S splits per head, partial
 // buffers of n_heads*S*hs and n_heads*S*2 floats.
@@ -46,10 +46,19 @@ int launch_attention_split(const float* q, const float* kcache, const float* vca
 // floats of scratch, S the number of score workgroups per head.
 // T > 1: queries at positions pos..pos+T-1 (causal), q rows `q_stride` floats
 // apart, outputs [T][n_heads*hs], scores [T][n_heads][max_t].
+// k_il: the K cache's layout (see k_index).
+// A single query (T == 1) runs as one kernel (k_attn_fused, same operations)
+// when `fused` is 1, or when it is -1, meta is NULL, the head size has a
+// fused form and pos + 1 <= attention_fused_max(); otherwise as two.
 int launch_attention_exact(const float* q, const float* kcache, const float* vcache, float* out, float* scores,
                            int S, const int* meta, int pos, int n_heads, int n_kv_heads, int hs, int max_t,
-                           hipStream_t st, int T = 1, int q_stride = 0);
+                           hipStream_t st, int T = 1, int q_stride = 0, int fused = -1, int k_il = 0);
 bool attention_exact_ok(int max_t);
+bool attention_fused_ok(int hs);
+// Longest context served by the one-kernel form: every context the exact
+// path takes (measured faster than the pair at 64..4096 positions with the
+// engine's K layout; L2Q_ATTN_FUSED_MAX lowers it, for measurements).
+int attention_fused_max();
 
 // int8 KV cache: append one position / attention over positions 0..pos.
 bool kv8_shape_ok(int n_heads, int n_kv_heads, int hs, int max_t);

@@ -3,6 +3,7 @@
 #include <math.h>
 #include <stdarg.h>
 #include <stdio.h>
+#include <stdlib.h>
 #include <string.h>
 
 #include "kernels.h"
@@ -194,8 +195,8 @@ int launch_swiglu_quant(const float* hb, const float* hb2, int n, int group, int
 
 int launch_rope_kv_append(float* q, const float* k, const float* v, float* kcache, float* vcache, const float* rope,
                           const int* meta, int pos, int dim, int kv_dim, int hs, int max_t, hipStream_t st, int T,
-                          int stride) {
-    if (hs <= 0 || hs % 2 || dim % hs || kv_dim % hs || kv_dim > dim || max_t <= 0 || T < 1 ||
+                          int stride, int k_il) {
+    if (hs <= 0 || hs % 2 || (k_il && hs % 4) || dim % hs || kv_dim % hs || kv_dim > dim || max_t <= 0 || T < 1 ||
         (!meta && (pos < 0 || pos + T > max_t)) || (meta && T > 1)) {
         set_error("rope_kv_append: bad shape dim=%d kv_dim=%d hs=%d pos=%d T=%d max_t=%d", dim, kv_dim, hs, pos, T,
                   max_t);
@@ -203,7 +204,7 @@ int launch_rope_kv_append(float* q, const float* k, const float* v, float* kcach
     }
     const int pairs = dim / 2;
     hipLaunchKernelGGL(k_rope_kv_append, dim3((pairs + 255) / 256, T), dim3(256), 0, st, q, k, v, kcache, vcache,
-                       rope, meta, pos, dim, kv_dim, hs, max_t, stride);
+                       rope, meta, pos, dim, kv_dim, hs, max_t, stride, k_il);
     return check_launch("rope_kv_append");
 }
 
@@ -235,13 +236,48 @@ int launch_attention_split(const float* q, const float* kcache, const float* vca
     return check_launch("attention_combine");
 }
 
+template <int HS, int KIL>
+static int go_attn_fused_l(const float* q, const float* kcache, const float* vcache, float* out, const int* meta,
+                           int pos, int kv_mul, int n_heads, int max_t, hipStream_t st) {
+    const size_t lds = attn_fused_lds_bytes(max_t, HS);
+    const void* fn = reinterpret_cast<const void*>(&k_attn_fused<HS, KIL>);
+    if (lds > 65536) {   // above the default dynamic-LDS limit: raise it once per kernel
+        static int raised = 0;
+        if (raised < (int)lds) {
+            hipError_t e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+            if (e != hipSuccess) return hip_fail(e, "attention: raising the LDS limit");
+            raised = (int)lds;
+        }
+    }
+    hipLaunchKernelGGL((k_attn_fused<HS, KIL>), dim3(n_heads * (HS / kVDims)), dim3(kAfThreads), lds, st, q, kcache,
+                       vcache, out, meta, pos, kv_mul, n_heads, max_t);
+    return check_launch("attention_fused");
+}
+
+template <int HS>
+static int go_attn_fused(const float* q, const float* kcache, const float* vcache, float* out, const int* meta,
+                         int pos, int kv_mul, int n_heads, int max_t, int k_il, hipStream_t st) {
+    return k_il ? go_attn_fused_l<HS, 1>(q, kcache, vcache, out, meta, pos, kv_mul, n_heads, max_t, st)
+                : go_attn_fused_l<HS, 0>(q, kcache, vcache, out, meta, pos, kv_mul, n_heads, max_t, st);
+}
+
+bool attention_fused_ok(int hs) { return hs == 48 || hs == 64 || hs == 128; }
+
+int attention_fused_max() {
+    static const int v = [] {
+        const char* s = getenv("L2Q_ATTN_FUSED_MAX");
+        return s ? atoi(s) : kAfDefaultMax;
+    }();
+    return v;
+}
+
 bool attention_exact_ok(int max_t) {
     return max_t <= kScorePer * kAttnThreads && attn_v_lds_bytes(max_t) <= 65536;
 }
 
 int launch_attention_exact(const float* q, const float* kcache, const float* vcache, float* out, float* scores,
                            int S, const int* meta, int pos, int n_heads, int n_kv_heads, int hs, int max_t,
-                           hipStream_t st, int T, int q_stride) {
+                           hipStream_t st, int T, int q_stride, int fused, int k_il) {
     (void)S;
     if (!attention_shape_ok(n_heads, n_kv_heads, hs) || max_t <= 0 || !attention_exact_ok(max_t) || T < 1 ||
         (!meta && (pos < 0 || pos + T > max_t)) || (meta && T > 1)) {
@@ -250,12 +286,21 @@ int launch_attention_exact(const float* q, const float* kcache, const float* vca
         return L2Q_ERR_ARG;
     }
     const int kv_mul = n_heads / n_kv_heads;
+    const bool one = T == 1 && attention_fused_ok(hs) &&
+                     (fused == 1 || (fused == -1 && !meta && pos + 1 <= attention_fused_max()));
+    if (one) {   // one query: the single-kernel form (same operations, same order)
+        switch (hs) {
+            case 48: return go_attn_fused<48>(q, kcache, vcache, out, meta, pos, kv_mul, n_heads, max_t, k_il, st);
+            case 64: return go_attn_fused<64>(q, kcache, vcache, out, meta, pos, kv_mul, n_heads, max_t, k_il, st);
+            case 128: return go_attn_fused<128>(q, kcache, vcache, out, meta, pos, kv_mul, n_heads, max_t, k_il, st);
+        }
+    }
     // persistent score waves over (head, tile) items; a captured graph covers
     // every position the cache can hold, items past pos are not visited
     const int items = n_heads * ((meta ? max_t : pos + T) + kScoreTile - 1) / kScoreTile;
     const int grid = items < kScoreGridMax ? items : kScoreGridMax;
     hipLaunchKernelGGL(k_attn_scores, dim3(grid, T), dim3(kScoreThreads), attn_scores_lds_bytes(hs), st, q, kcache,
-                       scores, meta, pos, kv_mul, n_heads, hs, max_t, q_stride);
+                       scores, meta, pos, kv_mul, n_heads, hs, max_t, q_stride, k_il);
     int rc = check_launch("attention_scores");
     if (rc) return rc;
     hipLaunchKernelGGL(k_attn_softmax_v, dim3(n_heads, (hs + kVDims - 1) / kVDims, T), dim3(kAttnThreads),
@@ -470,18 +515,27 @@ int l2q_rope_kv_append(float* q, const float* k, const float* v, float* kcache, 
                                  n_kv_heads * head_size, head_size, max_t, (hipStream_t)stream);
 }
 
-int l2q_attention(const float* q, const float* kcache, const float* vcache, float* out, int pos, int n_heads,
-                  int n_kv_heads, int head_size, int max_t, void* stream) {
-    if (!attention_shape_ok(n_heads, n_kv_heads, head_size) || pos < 0 || pos >= max_t) {
-        set_error("attention: bad shape heads=%d kv_heads=%d hs=%d pos=%d max_t=%d", n_heads, n_kv_heads, head_size,
-                  pos, max_t);
+int l2q_attention_ex(const float* q, const float* kcache, const float* vcache, float* out, int pos, int n_heads,
+                     int n_kv_heads, int head_size, int max_t, int flags, void* stream) {
+    const int one = flags & L2Q_ATTN_ONE_KERNEL, two = flags & L2Q_ATTN_TWO_KERNELS;
+    if (!attention_shape_ok(n_heads, n_kv_heads, head_size) || pos < 0 || pos >= max_t ||
+        (flags & ~(L2Q_ATTN_K_INTERLEAVED | L2Q_ATTN_ONE_KERNEL | L2Q_ATTN_TWO_KERNELS)) || (one && two) ||
+        (one && !attention_fused_ok(head_size))) {
+        set_error("attention: bad shape or flags heads=%d kv_heads=%d hs=%d pos=%d max_t=%d flags=%d", n_heads,
+                  n_kv_heads, head_size, pos, max_t, flags);
         return L2Q_ERR_ARG;
     }
     float* scratch = nullptr;
     int rc = attn_scratch((size_t)n_heads * max_t, &scratch);
     if (rc) return rc;
     return launch_attention_exact(q, kcache, vcache, out, scratch, score_splits(pos + 1), nullptr, pos, n_heads,
-                                  n_kv_heads, head_size, max_t, (hipStream_t)stream);
+                                  n_kv_heads, head_size, max_t, (hipStream_t)stream, 1, 0, one ? 1 : two ? 0 : -1,
+                                  flags & L2Q_ATTN_K_INTERLEAVED ? 1 : 0);
+}
+
+int l2q_attention(const float* q, const float* kcache, const float* vcache, float* out, int pos, int n_heads,
+                  int n_kv_heads, int head_size, int max_t, void* stream) {
+    return l2q_attention_ex(q, kcache, vcache, out, pos, n_heads, n_kv_heads, head_size, max_t, 0, stream);
 }
 
 int l2q_gemm_q(int wbits, float* out, const int8_t* xq, const float* xs, const void* w, const float* ws, int rows,

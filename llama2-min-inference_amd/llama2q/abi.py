@@ -16,6 +16,9 @@ L2Q_ERR_FORMAT = -3
 L2Q_ERR_NOMEM = -4
 L2Q_ERR_STATE = -5
 L2Q_ENGINE_KV_INT8 = 1
+L2Q_ATTN_K_INTERLEAVED = 1
+L2Q_ATTN_ONE_KERNEL = 2
+L2Q_ATTN_TWO_KERNELS = 4
 
 
 class L2QError(RuntimeError):
@@ -56,6 +59,7 @@ SIGNATURES = {
     "l2q_swiglu_quant": (I, [P, P, I, I, P, P, P, P]),
     "l2q_rope_kv_append": (I, [P, P, P, P, P, P, I, I, I, I, I, P]),
     "l2q_attention": (I, [P, P, P, P, I, I, I, I, I, P]),
+    "l2q_attention_ex": (I, [P, P, P, P, I, I, I, I, I, I, P]),
     "l2q_attention_split": (I, [P, P, P, P, I, I, I, I, I, P]),
     "l2q_kv8_append": (I, [P, P, P, P, P, P, P, I, I, I, I, P]),
     "l2q_attention_kv8": (I, [P, P, P, P, P, P, I, I, I, I, I, P]),

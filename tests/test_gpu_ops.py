@@ -238,6 +238,33 @@ def test_attention_other_heads(gpu_lib, torch_cuda, n_heads, n_kv, hs, max_t, po
     np.testing.assert_array_equal(got[3], ref[3])
 
 
+@pytest.mark.parametrize("n_heads,n_kv,hs,max_t,ctx", [
+    (32, 32, 128, 4096, 1), (32, 32, 128, 4096, 65), (32, 32, 128, 4096, 513), (32, 32, 128, 4096, 769),
+    (32, 32, 128, 4096, 4096), (6, 6, 48, 256, 1), (6, 6, 48, 256, 256), (8, 2, 64, 512, 300),
+])
+def test_attention_forms_and_k_layouts(gpu_lib, torch_cuda, n_heads, n_kv, hs, max_t, ctx):
+    """The single-kernel and two-kernel forms, over the row-major and the
+    engine's column-interleaved K layout ([n_kv][hs/4][max_t][4]), all give
+    the oracle's bits (runq.c:367-391)."""
+    t = torch_cuda
+    print(f"attention forms heads={n_heads}/{n_kv} hs={hs} ctx={ctx}", flush=True)
+    pos = ctx - 1
+    kc = host.gauss(n_kv * max_t * hs, ctx, 1, 1.0).reshape(n_kv, max_t, hs)
+    vc = host.gauss(n_kv * max_t * hs, ctx, 2, 1.0).reshape(n_kv, max_t, hs)
+    q = host.gauss(n_heads * hs, ctx, 3, 1.0)
+    ref = O.attention(q, kc, vc, pos, n_heads, n_kv, hs)
+    kil = np.ascontiguousarray(kc.reshape(n_kv, max_t, hs // 4, 4).transpose(0, 2, 1, 3))
+    d_q, d_v = dev(t, q), dev(t, vc)
+    out = t.empty(n_heads * hs, dtype=t.float32, device="cuda")
+    for layout, kd in ((0, dev(t, kc)), (abi.L2Q_ATTN_K_INTERLEAVED, dev(t, kil))):
+        for form in (0, abi.L2Q_ATTN_ONE_KERNEL, abi.L2Q_ATTN_TWO_KERNELS):
+            out.fill_(np.nan)
+            abi.call("l2q_attention_ex", d_q.data_ptr(), kd.data_ptr(), d_v.data_ptr(), out.data_ptr(), pos, n_heads,
+                     n_kv, hs, max_t, layout | form, stream(t))
+            t.cuda.synchronize()
+            np.testing.assert_array_equal(out.cpu().numpy(), ref, err_msg=f"layout {layout} form {form}")
+
+
 def test_expf_identical_to_host_on_every_input(gpu_lib, torch_cuda):
     """The device exp used by softmax and SwiGLU equals the host C library's
     expf on all 2^32 float bit patterns (NaNs compared as NaN)."""
@@ -276,3 +303,9 @@ def test_bad_shapes_raise(gpu_lib, torch_cuda):
         abi.call("l2q_gemv_q8", p, p + 1, p, p, p, 16, 4096, 64, None, None)  # misaligned activations
     with pytest.raises(abi.L2QError):
         abi.call("l2q_attention", p, p, p, p, 10, 4, 4, 128, 8, None)         # pos >= max_t
+    with pytest.raises(abi.L2QError):
+        abi.call("l2q_attention_ex", p, p, p, p, 1, 4, 4, 96, 8, abi.L2Q_ATTN_ONE_KERNEL, None)   # no 96 form
+    with pytest.raises(abi.L2QError):
+        abi.call("l2q_attention_ex", p, p, p, p, 1, 4, 4, 128, 8, 6, None)     # both forms
+    with pytest.raises(abi.L2QError):
+        abi.call("l2q_attention_ex", p, p, p, p, 1, 4, 4, 128, 8, 8, None)     # unknown flag
