@@ -277,6 +277,11 @@ int l2q_attention_kv8(const float* q, const int8_t* kcache8, const int8_t* vcach
                       const float* kscale, const float* vscale, float* out, int pos,
                       int n_heads, int n_kv_heads, int head_size, int max_t, void* stream);
 
+/* Greedy argmax on the device: out[0] = the first index of the maximum of
+ * v[0..n), v 16-byte aligned (sample_argmax, runq.c:578-585; the engine's
+ * l2q_engine_forward_argmax runs it inside its step). */
+int l2q_argmax(const float* v, int n, int* out, void* stream);
+
 /* expf exactly as the host C library computes it (the exp used by the
  * attention softmax and SwiGLU above), elementwise over n floats.  Exposed
  * so its identity with the host's expf can be checked on every input. */

@@ -894,15 +894,40 @@ __global__ __launch_bounds__(256) void k_attn_combine(const float* __restrict__ 
 }
 
 // ---------------------------------------------------------------------------
-// Greedy argmax (runq.c:578-585: first index of the maximum).
-__global__ __launch_bounds__(1024) void k_argmax(const float* __restrict__ v, int n, int* __restrict__ out) {
-    __shared__ float bv[1024 / L2Q_WAVE];
-    __shared__ int bi[1024 / L2Q_WAVE];
+// Greedy argmax (runq.c:578-585: first index of the maximum).  One
+// workgroup; each thread takes float4 chunks t, t + 1024, ... (v 16-byte
+// aligned), the loads of eight chunks in flight at once, and scans its
+// elements in ascending index order, so its first maximum is kept; the
+// reduction prefers the smaller index on equal values.
+constexpr int kArgmaxThreads = 1024;
+__global__ __launch_bounds__(kArgmaxThreads) void k_argmax(const float* __restrict__ v, int n, int* __restrict__ out) {
+    __shared__ float bv[kArgmaxThreads / L2Q_WAVE];
+    __shared__ int bi[kArgmaxThreads / L2Q_WAVE];
     float best = -INFINITY;
     int idx = n;   // sentinel larger than every index
-    for (int i = threadIdx.x; i < n; i += blockDim.x) {
+    const int n4 = n / 4;
+    const float4* v4 = reinterpret_cast<const float4*>(v);
+    for (int base = 0; base < n4; base += 8 * kArgmaxThreads) {
+        float4 x[8];
+#pragma unroll
+        for (int k = 0; k < 8; k++) {
+            const int f = base + (int)threadIdx.x + kArgmaxThreads * k;
+            x[k] = v4[min(f, n4 - 1)];
+        }
+#pragma unroll
+        for (int k = 0; k < 8; k++) {
+            const int f = base + (int)threadIdx.x + kArgmaxThreads * k;
+            if (f < n4) {
+                if (x[k].x > best) { best = x[k].x; idx = 4 * f; }
+                if (x[k].y > best) { best = x[k].y; idx = 4 * f + 1; }
+                if (x[k].z > best) { best = x[k].z; idx = 4 * f + 2; }
+                if (x[k].w > best) { best = x[k].w; idx = 4 * f + 3; }
+            }
+        }
+    }
+    for (int i = 4 * n4 + (int)threadIdx.x; i < n; i += kArgmaxThreads) {
         const float x = v[i];
-        if (x > best) { best = x; idx = i; }   // ascending i: first max kept
+        if (x > best) { best = x; idx = i; }
     }
 #pragma unroll
     for (int o = 32; o > 0; o >>= 1) {

@@ -406,8 +406,11 @@ int launch_pf_swiglu_quant(const float* h13, int n, int T, int group, int8_t* xq
 }
 
 int launch_argmax(const float* v, int n, int* out, hipStream_t st) {
-    if (n <= 0) { set_error("argmax: n=%d", n); return L2Q_ERR_ARG; }
-    hipLaunchKernelGGL(k_argmax, dim3(1), dim3(1024), 0, st, v, n, out);
+    if (n <= 0 || !v || !out || reinterpret_cast<uintptr_t>(v) % 16) {
+        set_error("argmax: n=%d (v must be 16-byte aligned)", n);
+        return L2Q_ERR_ARG;
+    }
+    hipLaunchKernelGGL(k_argmax, dim3(1), dim3(kArgmaxThreads), 0, st, v, n, out);
     return check_launch("argmax");
 }
 
@@ -593,6 +596,10 @@ int l2q_attention_split(const float* q, const float* kcache, const float* vcache
     if (rc) return rc;
     return launch_attention_split(q, kcache, vcache, out, scratch, scratch + (size_t)n_heads * S * head_size, S,
                                   nullptr, pos, n_heads, n_kv_heads, head_size, max_t, (hipStream_t)stream);
+}
+
+int l2q_argmax(const float* v, int n, int* out, void* stream) {
+    return launch_argmax(v, n, out, (hipStream_t)stream);
 }
 
 int l2q_expf(const float* x, float* y, size_t n, void* stream) {

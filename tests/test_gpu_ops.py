@@ -283,6 +283,28 @@ def test_expf_identical_to_host_on_every_input(gpu_lib, torch_cuda):
         assert same.all(), f"chunk {c}: {int((~same).sum())} mismatches, first x={x[~same][0]!r}"
 
 
+@pytest.mark.parametrize("n", [1, 3, 4, 5, 1000, 32000, 32003, 40000])
+def test_argmax_first_index(gpu_lib, torch_cuda, n):
+    """Device argmax = the first index of the maximum (runq.c:578-585):
+    random values, ties planted before and after the maximum's first
+    occurrence, an all-equal vector, and a maximum in the scalar tail."""
+    t = torch_cuda
+    rng = np.random.default_rng(n)
+    out = t.zeros(1, dtype=t.int32, device="cuda")
+    cases = [rng.standard_normal(n).astype(np.float32), np.full(n, -2.5, np.float32)]
+    v = rng.standard_normal(n).astype(np.float32)
+    v[rng.integers(0, n, size=min(n, 3))] = 9.0     # several copies of the maximum
+    cases.append(v)
+    v = rng.standard_normal(n).astype(np.float32)
+    v[-1] = 7.0                                    # in the tail when n % 4
+    cases.append(v)
+    for v in cases:
+        d_v = dev(t, v)
+        abi.call("l2q_argmax", d_v.data_ptr(), n, out.data_ptr(), stream(t))
+        t.cuda.synchronize()
+        assert int(out.item()) == int(np.argmax(v)), (n, v[:8])
+
+
 def test_unbias(gpu_lib, torch_cuda):
     t = torch_cuda
     src = np.arange(1000, dtype=np.int64).astype(np.uint8)
