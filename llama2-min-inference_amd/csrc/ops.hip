@@ -369,25 +369,44 @@ int launch_pf_gemm(int bits, int group, const void* w, const float* ws, int rows
         set_error("prefill gemm: bad rows=%d cols=%d T=%d group=%d bits=%d", rows, cols, T, group, bits);
         return L2Q_ERR_ARG;
     }
-    // token tiles per wave: as many as keep >= 2048 waves in the grid (weight
-    // reuse in registers vs parallelism)
-    const long long nrt = (rows + kPfTile - 1) / kPfTile, ntt = (T + kPfTile - 1) / kPfTile;
-    int NT = 1;
-    if (nrt * ((ntt + 3) / 4) >= 2048) NT = 4;
-    else if (nrt * ((ntt + 1) / 2) >= 2048) NT = 2;
-    const long long waves = nrt * ((ntt + NT - 1) / NT);
-    const dim3 grid((unsigned)((waves + kPfWaves - 1) / kPfWaves)), block(kPfWaves * L2Q_WAVE);
+    if (reinterpret_cast<uintptr_t>(w) % 16 || reinterpret_cast<uintptr_t>(xqp) % 16) {
+        set_error("prefill gemm: weights and activations must be 16-byte aligned");
+        return L2Q_ERR_ARG;
+    }
+    // rows per workgroup (16, 32 or 64): the fewest rounds of workgroups
+    // over the CUs, times the rows each one folds; the larger tile on ties
+    // (each workgroup reads all the activations)
+    const long long rtiles = (rows + 15) / 16;
+    int rtw = 4;
+    long long best = -1;
+    for (int r : {4, 2, 1}) {
+        const long long wgs = (rtiles + r - 1) / r * ((T + kPf2Tokens - 1) / kPf2Tokens);
+        const long long cost = (wgs + 255) / 256 * r;
+        if (best < 0 || cost < best) { best = cost; rtw = r; }
+    }
+    const dim3 grid((unsigned)((rows + 16 * rtw - 1) / (16 * rtw)), (unsigned)((T + kPf2Tokens - 1) / kPf2Tokens));
     const uint8_t* wb = static_cast<const uint8_t*>(w);
-#define L2Q_PF_GEMM(B_, G_, N_) \
-    hipLaunchKernelGGL((k_pf_gemm<B_, G_, N_>), grid, block, 0, st, wb, ws, rows, cols, xqp, xs, sq, xt, T, out, ldo)
-#define L2Q_PF_GEMM_NT(B_, G_) \
-    do { if (NT == 4) L2Q_PF_GEMM(B_, G_, 4); else if (NT == 2) L2Q_PF_GEMM(B_, G_, 2); else L2Q_PF_GEMM(B_, G_, 1); } while (0)
-    if (bits == 4 && group == 64) L2Q_PF_GEMM_NT(4, 64);
-    if (bits == 4 && group == 32) L2Q_PF_GEMM_NT(4, 32);
-    if (bits == 8 && group == 64) L2Q_PF_GEMM_NT(8, 64);
-    if (bits == 8 && group == 32) L2Q_PF_GEMM_NT(8, 32);
-#undef L2Q_PF_GEMM_NT
-#undef L2Q_PF_GEMM
+    int rc = L2Q_OK;
+    auto go = [&](auto kern, size_t lds) {
+        const void* fn = reinterpret_cast<const void*>(kern);
+        if (lds > 65536) {
+            hipError_t e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+            if (e != hipSuccess) { rc = hip_fail(e, "prefill gemm: raising the LDS limit"); return; }
+        }
+        hipLaunchKernelGGL(kern, grid, dim3(kPf2Threads), lds, st, wb, ws, rows, cols, xqp, xs, sq, xt, T, out, ldo);
+    };
+#define L2Q_PF2(B_, G_)                                                                    \
+    do {                                                                                  \
+        if (rtw == 4) go(k_pf_gemm2<B_, G_, 4>, pf2_lds_bytes<B_, G_, 4>());              \
+        else if (rtw == 2) go(k_pf_gemm2<B_, G_, 2>, pf2_lds_bytes<B_, G_, 2>());         \
+        else go(k_pf_gemm2<B_, G_, 1>, pf2_lds_bytes<B_, G_, 1>());                       \
+    } while (0)
+    if (bits == 4 && group == 64) L2Q_PF2(4, 64);
+    if (bits == 4 && group == 32) L2Q_PF2(4, 32);
+    if (bits == 8 && group == 64) L2Q_PF2(8, 64);
+    if (bits == 8 && group == 32) L2Q_PF2(8, 32);
+#undef L2Q_PF2
+    if (rc) return rc;
     return check_launch("prefill_gemm");
 }
 
