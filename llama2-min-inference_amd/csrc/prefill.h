@@ -100,7 +100,9 @@ __global__ __launch_bounds__(kPf2Threads) void k_pf_gemm2(
     constexpr int BPT = kPf2Cols * kPf2Tokens / 16 / kPf2Threads;     // 16-byte activation loads per thread
     constexpr int SN = KS * kPf2Tokens;                               // per-token scalars per step
     constexpr int SPT = (SN + kPf2Threads - 1) / kPf2Threads;
-    static_assert(BPT >= 1 && KS * RT <= kPf2Threads, "step geometry");
+    constexpr int WN = KS * RT;                                       // weight scales per step
+    constexpr int WPT = (WN + kPf2Threads - 1) / kPf2Threads;
+    static_assert(BPT >= 1, "step geometry");
     extern __shared__ __attribute__((aligned(16))) uint8_t pf2_lds[];
     const int tid = threadIdx.x, lane = tid & (L2Q_WAVE - 1), wv = tid / L2Q_WAVE;
     const int r0 = blockIdx.x * RT, t0 = blockIdx.y * kPf2Tokens;
@@ -120,7 +122,7 @@ __global__ __launch_bounds__(kPf2Threads) void k_pf_gemm2(
         uint4 ra[APT], rb[BPT];
         float rxs[SPT], rxt[SPT];
         int rsq[SPT];
-        float rws;
+        float rws[WPT];
     };
     auto fetch = [&](int s, Regs& R) {
 #pragma unroll
@@ -143,9 +145,10 @@ __global__ __launch_bounds__(kPf2Threads) void k_pf_gemm2(
             R.rxt[k] = xt[gi];
             R.rsq[k] = sq[gi];
         }
-        {
-            const int e = min(tid, KS * RT - 1), r = e / KS, g = s * KS + e % KS;
-            R.rws = ws[(size_t)min(r0 + r, rows - 1) * nb + min(g, nb - 1)];
+#pragma unroll
+        for (int k = 0; k < WPT; k++) {
+            const int e = min(tid + kPf2Threads * k, WN - 1), r = e / KS, g = s * KS + e % KS;
+            R.rws[k] = ws[(size_t)min(r0 + r, rows - 1) * nb + min(g, nb - 1)];
         }
     };
     // registers -> LDS buffer: [A rows][AP] [B tokens][BPitch] [xs][xt][c: KS x 128] [ws: KS x RT]
@@ -174,7 +177,11 @@ __global__ __launch_bounds__(kPf2Threads) void k_pf_gemm2(
                 reinterpret_cast<int*>(S)[(2 * KS + g) * kPf2Tokens + t] = R.rsq[k] * (BITS == 4 ? 2048 : 128);
             }
         }
-        if (tid < KS * RT) S[3 * KS * kPf2Tokens + (tid % KS) * RT + tid / KS] = R.rws;
+#pragma unroll
+        for (int k = 0; k < WPT; k++) {
+            const int e = tid + kPf2Threads * k;
+            if (e < WN) S[3 * KS * kPf2Tokens + (e % KS) * RT + e / KS] = R.rws[k];
+        }
     };
 
     constexpr int TPW = kPf2Tpw, NW = 8 / TPW;

@@ -127,6 +127,24 @@ def test_int4_g64_7b_layers_debug(gpu_lib):
     eng.close()
 
 
+@pytest.mark.parametrize("bits", [8, 4])
+def test_hs64_g32_gqa_logits(gpu_lib, bits):
+    """Heads of 64 with groups of 32 and grouped-query attention (4 heads over
+    2 kv heads): logits bit-identical to the oracle at every position."""
+    cfg = host.make_config(256, 512, 2, 4, 2, 512, 64)
+    kw = {"q4_divisor": 7.0} if bits == 4 else {}
+    ck = host.synth_checkpoint(cfg, bits, 32, seed=5 + bits, **kw)
+    eng = Engine(ck, max_steps=24)
+    orc = O.Oracle(ck.cfg.as_list(), ck.weights, bits, 32, max_t=24)
+    token = 3
+    for pos in range(24):
+        lg, lo = eng.forward(token, pos), orc.forward(token, pos)
+        np.testing.assert_array_equal(lg, lo, err_msg=f"pos {pos}")
+        token = int(np.argmax(lo))
+    eng.close()
+    orc.close()
+
+
 @pytest.mark.parametrize("prompt,steps", [("Once upon a time", 48), ("a", 20)])
 def test_runner_output_equals_reference_runq(gpu_lib, c1_q8, tmp_path, prompt, steps):
     """The drop-in runner against the reference's own runq executable
