@@ -6,9 +6,11 @@
 // d_u8 = d + 128*sum(xq_b) and xt[b] = xs[b]*128*sum(xq_b).
 //
 // Mapping (wave64, no MFMA: at batch 1 this is a pure weight stream):
-//   - rows are cut into units of PR consecutive rows; every wave of the
-//     grid owns a contiguous, equal (+-1 unit) range of units, so the whole
-//     grid finishes together and each wave streams one contiguous region;
+//   - rows are cut into units of PR consecutive rows, dealt round-robin:
+//     wave w of W takes units w, w + W, w + 2W, ..., so every wave has the
+//     same number (+-1) and the grid sweeps the matrix front to back, all
+//     waves reading one window of ~W units at a time (better DRAM locality
+//     than a contiguous range per wave: measured 2-3% faster on every shape);
 //   - a row is read in sweeps of 1 KiB: in sweep s lane j loads the 16
 //     bytes at s*1024 + 16*j, so every load instruction of a wave covers
 //     one contiguous KiB (the best-coalesced form of the stream); the
@@ -536,8 +538,9 @@ __device__ __forceinline__ void wave_lds_sync() {
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
 
-// Persistent over units of PR rows: wave w of the grid owns units
-// [U*w/W, U*(w+1)/W) (U units, W waves).  The wave's first unit is loaded
+// Persistent over units of PR rows: local unit j of wave w is the grid's
+// unit w + j*W (U units, W waves, j < ceil((U - w)/W)); fold batches and
+// the loop count local units.  The wave's first unit is loaded
 // before the prologue (which runs once per workgroup while it streams in);
 // unit u+1 is loaded as soon as unit u has been consumed.  Terms of F rows
 // (F/PR units) are collected before one ordered fold on F lanes.  A wave
@@ -580,8 +583,9 @@ __global__ __launch_bounds__(gemv_waves(NS) * L2Q_WAVE) void k_gemv(GemvArgs a) 
     const int nunits = (a.rows + PR - 1) / PR;
     const int nwaves = gridDim.x * WAVES;
     const int gw = blockIdx.x * WAVES + wv;
-    const int u0 = (int)((long long)nunits * gw / nwaves);
-    const int u1 = (int)((long long)nunits * (gw + 1) / nwaves);
+    // units dealt round-robin: local unit j of this wave is gw + j*nwaves
+    const int u0 = 0;
+    const int u1 = gw < nunits ? (nunits - gw + nwaves - 1) / nwaves : 0;
 
     // 1. prologue inputs first, so that waiting for them never waits on the
     //    weight loads issued after them (vector loads complete in order)
@@ -652,7 +656,7 @@ __global__ __launch_bounds__(gemv_waves(NS) * L2Q_WAVE) void k_gemv(GemvArgs a) 
         const bool real = u < u1;
 #pragma unroll
         for (int k = 0; k < PR; k++) {
-            const int row = real ? min(u * PR + k, a.rows - 1) : 0;
+            const int row = real ? min((gw + u * nwaves) * PR + k, a.rows - 1) : 0;
             const uint8_t* p = wbase + (size_t)row * rowbytes;
 #pragma unroll
             for (int s = 0; s < NS; s++) {
@@ -719,7 +723,7 @@ __global__ __launch_bounds__(gemv_waves(NS) * L2Q_WAVE) void k_gemv(GemvArgs a) 
 
     // dots and per-group terms of row k of unit u into fold-batch row br
     auto consume_row = [&](int k, int u) {
-        const int row = u * PR + k;
+        const int row = (gw + u * nwaves) * PR + k;
         const int br = ((u - u0) % UB) * PR + k;
 #pragma unroll
         for (int s = 0; s < NS; s++) {
@@ -748,14 +752,14 @@ __global__ __launch_bounds__(gemv_waves(NS) * L2Q_WAVE) void k_gemv(GemvArgs a) 
         }
     };
 
-    // ordered fold of a batch of nrows rows (first row row0) on lanes
-    // 0..nrows-1, then the epilogue
-    auto fold_batch = [&](int row0, int nrows) {
+    // ordered fold of a batch of nrows rows (local units from j0 on) on
+    // lanes 0..nrows-1, then the epilogue
+    auto fold_batch = [&](int j0, int nrows) {
         wave_lds_sync();
         float sum = 0.0f;
         if (lane < nrows) sum = fold_row(tb + lane * nbp, sb + lane * nbp, nb);
         const bool mine = lane < nrows;
-        const int row = row0 + lane;
+        const int row = (gw + (j0 + lane / PR) * nwaves) * PR + lane % PR;
         if (EPI == kStore) {
             if (mine && row < a.rows) a.out[row] = sum;
         } else if (EPI == kRopeKV) {
@@ -806,12 +810,12 @@ __global__ __launch_bounds__(gemv_waves(NS) * L2Q_WAVE) void k_gemv(GemvArgs a) 
         __builtin_amdgcn_sched_barrier(0);
         load_unit(u + 1);
         __builtin_amdgcn_sched_barrier(0);
-        if ((u - u0 + 1) % UB == 0) fold_batch((u + 1 - UB) * PR, F);
+        if ((u - u0 + 1) % UB == 0) fold_batch(u + 1 - UB, F);
     }
 #pragma unroll
     for (int k = 0; k < PR; k++) consume_row(k, u1 - 1);
     const int last = (u1 - u0 - 1) % UB + 1;   // units in the last batch
-    fold_batch((u1 - last) * PR, last * PR);
+    fold_batch(u1 - last, last * PR);
 }
 
 }  // namespace l2q
