@@ -89,11 +89,11 @@ __host__ __device__ constexpr int gemv_unit_rows(int NS, int EPI) { return EPI =
 
 __host__ __device__ constexpr int gemv_sweeps(int bits, int cols) { return (cols * bits / 8 + kSweepBytes - 1) / kSweepBytes; }
 
-// One workgroup per CU, as many waves as the register budget allows (12 =
-// 3 per SIMD for rows of up to 3 sweeps, else 8): the workgroup-wide
-// prologue is then shared by every wave of the CU instead of being
-// recomputed by several workgroups.
-__host__ __device__ constexpr int gemv_waves(int NS) { return NS <= 3 ? 12 : 8; }
+// One workgroup of 8 waves (2 per SIMD) per CU: the workgroup-wide prologue
+// is then shared by every wave of the CU instead of being recomputed by
+// several workgroups.  (12 waves for short rows measured ~1% slower in the
+// decode step: a 4096-row matrix then fills only 171 of the 256 CUs.)
+__host__ __device__ constexpr int gemv_waves(int) { return 8; }
 
 // Rows folded at once per wave (F lanes run F ordered FMA chains side by
 // side): the fold's instructions are issued for the whole wave whatever the
