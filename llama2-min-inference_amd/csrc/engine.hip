@@ -136,11 +136,9 @@ int enqueue_step(l2q_engine* e, hipStream_t st, float* dbg_x, float* dbg_tmp, bo
         if (dbg_x && l == 0) HIPCHK(hipMemcpyAsync(dbg_x, e->xb, d * sizeof(float), hipMemcpyDeviceToHost, st), "copy x");
         if (kv8) {
             const size_t co = (size_t)l * kv * e->max_t, so = (size_t)l * c.n_kv_heads * e->max_t;
-            rc = launch_kv8_append(e->kvf, e->kvf + kv, e->k8 + co, e->v8 + co, e->ks + so, e->vs + so, nullptr,
-                                   e->meta, 0, c.n_kv_heads, e->hs, e->max_t, st);
-            if (!rc)
-                rc = launch_attention_kv8(e->q, e->k8 + co, e->v8 + co, e->ks + so, e->vs + so, e->att, e->scores,
-                                          e->meta, 0, c.n_heads, c.n_kv_heads, e->hs, e->max_t, st);
+            // append the staged k, v rows and attend, in one kernel
+            rc = launch_attention_kv8(e->q, e->k8 + co, e->v8 + co, e->ks + so, e->vs + so, e->att, e->scores,
+                                      e->meta, 0, c.n_heads, c.n_kv_heads, e->hs, e->max_t, st, e->kvf, e->kvf + kv);
         } else {
             rc = launch_attention_exact(e->q, kc, vc, e->att, e->scores, e->S, e->meta, 0, c.n_heads,
                                         c.n_kv_heads, e->hs, e->max_t, st, 1, 0, fused ? 1 : 0, 1);

@@ -733,13 +733,12 @@ __global__ __launch_bounds__(kAfThreads) void k_attn_fused(
 // (v5-cuda-fused/run.cu:204-249).  One wave; element pairs (2p, 2p+1) on
 // lane p mod 64.
 constexpr int kKv8Pairs = kAttnMaxHs / 2 / L2Q_WAVE;   // pairs per lane (hs <= 256)
-__global__ __launch_bounds__(L2Q_WAVE) void k_kv8_append(
-    const float* __restrict__ k, const float* __restrict__ v, int8_t* __restrict__ k8, int8_t* __restrict__ v8,
-    float* __restrict__ ks, float* __restrict__ vs, const float* __restrict__ rope, const int* __restrict__ meta,
-    int pos_arg, int hs, int max_t) {
-    const int g = blockIdx.x, isv = blockIdx.y, lane = threadIdx.x;
-    const int pos = meta_pos(meta, pos_arg);
-    const float* src = (isv ? v : k) + (size_t)g * hs;
+// One wave quantizes one row: src[0..hs) (rotated first when a RoPE table
+// is given) -> int8 row `dst` (global, may be null) and `ldst` (LDS, may be
+// null), scale to *scale / *lscale (lane 0).
+__device__ __forceinline__ void kv8_quant_row(const float* __restrict__ src, const float* __restrict__ rope, int pos,
+                                              int hs, int lane, int8_t* dst, float* scale, int8_t* ldst,
+                                              float* lscale) {
     float2 val[kKv8Pairs];
     float amax = 0.0f;
 #pragma unroll
@@ -748,7 +747,7 @@ __global__ __launch_bounds__(L2Q_WAVE) void k_kv8_append(
         val[i] = make_float2(0.0f, 0.0f);
         if (2 * p < hs) {
             float2 x = reinterpret_cast<const float2*>(src)[p];
-            if (!isv && rope) {   // the fp32 path's rotation (RoPE table of the position)
+            if (rope) {   // the fp32 path's rotation (RoPE table of the position)
                 const float c = rope[(size_t)pos * hs + 2 * p], s = rope[(size_t)pos * hs + 2 * p + 1];
                 x = make_float2(__builtin_fmaf(x.x, c, -(x.y * s)), __builtin_fmaf(x.x, s, x.y * c));
             }
@@ -759,103 +758,172 @@ __global__ __launch_bounds__(L2Q_WAVE) void k_kv8_append(
     amax = group_max<L2Q_WAVE>(amax);
     float sc = amax / 127.0f;
     if (sc == 0.0f) sc = 1e-8f;
-    int8_t* dst = (isv ? v8 : k8) + ((size_t)g * max_t + pos) * hs;
 #pragma unroll
     for (int i = 0; i < kKv8Pairs; i++) {
         const int p = lane + L2Q_WAVE * i;
         if (2 * p < hs) {
             const int q0 = q8_value(val[i].x, sc), q1 = q8_value(val[i].y, sc);
-            *reinterpret_cast<uint16_t*>(dst + 2 * p) = (uint16_t)((q0 & 0xff) | ((q1 & 0xff) << 8));
+            const uint16_t w = (uint16_t)((q0 & 0xff) | ((q1 & 0xff) << 8));
+            if (dst) *reinterpret_cast<uint16_t*>(dst + 2 * p) = w;
+            if (ldst) *reinterpret_cast<uint16_t*>(ldst + 2 * p) = w;
         }
     }
-    if (lane == 0) (isv ? vs : ks)[(size_t)g * max_t + pos] = sc;
+    if (lane == 0) {
+        if (scale) *scale = sc;
+        if (lscale) *lscale = sc;
+    }
 }
 
-// Scores over the int8 cache (v5-cuda-fused/run.cu:362-371): score_t =
-// (q . k8_t) / sqrt(hs) * ks_t.  Four lanes per position, each summing the
-// 4-element chunks c = 4*sub + 16*i with FMAs, then a two-step butterfly;
-// 64 positions per workgroup item.  Needs hs % 16 == 0.
-constexpr int kA8Pos = 64;
-constexpr int kA8GridMax = 2048;
+__global__ __launch_bounds__(L2Q_WAVE) void k_kv8_append(
+    const float* __restrict__ k, const float* __restrict__ v, int8_t* __restrict__ k8, int8_t* __restrict__ v8,
+    float* __restrict__ ks, float* __restrict__ vs, const float* __restrict__ rope, const int* __restrict__ meta,
+    int pos_arg, int hs, int max_t) {
+    const int g = blockIdx.x, isv = blockIdx.y, lane = threadIdx.x;
+    const int pos = meta_pos(meta, pos_arg);
+    const size_t row = (size_t)g * max_t + pos;
+    kv8_quant_row((isv ? v : k) + (size_t)g * hs, isv ? nullptr : rope, pos, hs, lane, (isv ? v8 : k8) + row * hs,
+                  (isv ? vs : ks) + row, nullptr, nullptr);
+}
+
+// Attention over the int8 cache (v5-cuda-fused/run.cu:350-410), one kernel
+// per step, a workgroup of kA8Threads threads per head:
+//   append   when kst / vst (the rotated k row and the v row of the step,
+//            [n_kv][hs] staging) are given: waves 0 and 1 quantize the
+//            head's kv row (kv8_quant_row, as k_kv8_append) into LDS; the
+//            group's first head also writes it to the cache (the others
+//            compute the same bits for their own use, so no workgroup waits
+//            for another);
+//   scores   (run.cu:362-371) score_t = (q . k8_t) / sqrt(hs) * ks_t, all
+//            threads, kA8Threads/4 positions per round with the next
+//            round's K in flight, four lanes per position, each summing the
+//            4-element chunks c = 4*sub + 16*i with FMAs, then a two-step
+//            butterfly; into LDS (position pos from the LDS row when
+//            appending);
+//   softmax  (run.cu:373-398) max as a block reduction; the sum: thread j
+//            sums positions j, j + 1024, ...; then the wave butterfly, then a
+//            pairwise tree over the 16 waves ((w0 + w1) + (w2 + w3)) + ...;
+//            e_t * vs_t kept in LDS;
+//   p*V      thread (slice, g) accumulates elements 4g..4g+3 over positions
+//            t = slice (mod slices), 1024/(hs/4) slices; the slices are
+//            added in LDS in slice order and divided by the sum.
+// Every reduction has a fixed order (restated by the oracle's
+// orc_attention_kv8_ordered), so results are reproducible bit for bit.
+// Needs hs % 16 == 0.
+constexpr int kA8Threads = 1024;
+constexpr int kA8Waves = kA8Threads / L2Q_WAVE;
+constexpr int kA8Chunks = kAttnMaxHs / 16;               // K dwords per lane and position (hs <= 256)
+// Byte b of w as a signed value.
 __device__ __forceinline__ float sbyte(int w, int b) { return (float)((w << (24 - 8 * b)) >> 24); }
-__global__ __launch_bounds__(kAttnThreads) void k_attn8_scores(
-    const float* __restrict__ q, const int8_t* __restrict__ k8, const float* __restrict__ ks,
-    float* __restrict__ scores, const int* __restrict__ meta, int pos_arg, int kv_mul, int n_heads, int hs,
-    int max_t) {
-    const int tid = threadIdx.x, sub = tid & 3;
+__host__ __device__ constexpr size_t attn8_fused_lds_bytes(int max_t) {
+    return ((size_t)(max_t + 3) / 4 * 4 + 4 * kA8Threads + 3 * kA8Waves + 2 * kAttnMaxHs / 4) * sizeof(float);
+}
+__global__ __launch_bounds__(kA8Threads) void k_attn8_fused(
+    const float* __restrict__ q, const float* __restrict__ kst, const float* __restrict__ vst,
+    int8_t* __restrict__ k8, int8_t* __restrict__ v8, float* __restrict__ ks, float* __restrict__ vs,
+    float* __restrict__ out, const int* __restrict__ meta, int pos_arg, int kv_mul, int hs, int max_t) {
+    extern __shared__ __attribute__((aligned(16))) float smf[];
+    float* sc = smf;                                   // [max_t] scores, then e_t * vs_t
+    float* part = sc + (max_t + 3) / 4 * 4;            // [slices][hs] partial sums
+    float* red = part + 4 * kA8Threads;                // [16] wave maxima, [16] wave sums, [2] row scales
+    int8_t* krow = reinterpret_cast<int8_t*>(red + 3 * kA8Waves);   // [hs] appended k row, then [hs] v row
+    int8_t* vrow = krow + kAttnMaxHs;
+    const int h = blockIdx.x, hk = h / kv_mul;
+    const int tid = threadIdx.x, lane = tid & (L2Q_WAVE - 1), wv = tid / L2Q_WAVE, sub = tid & 3;
     const int pos = meta_pos(meta, pos_arg);
     const int n = pos + 1;
-    const int ntile = (n + kA8Pos - 1) / kA8Pos;
+    const bool append = kst != nullptr;
+    const size_t prow = (size_t)hk * max_t + pos;
+    if (append && wv < 2) {
+        const bool first = h % kv_mul == 0;
+        if (wv == 0)
+            kv8_quant_row(kst + (size_t)hk * hs, nullptr, pos, hs, lane, first ? k8 + prow * hs : nullptr,
+                          first ? ks + prow : nullptr, krow, red + 2 * kA8Waves);
+        else
+            kv8_quant_row(vst + (size_t)hk * hs, nullptr, pos, hs, lane, first ? v8 + prow * hs : nullptr,
+                          first ? vs + prow : nullptr, vrow, red + 2 * kA8Waves + 1);
+    }
+
+    // scores: the lane's q chunks in registers, the next round's K dwords
+    // loaded before the current round's FMAs
     const float rs = sqrtf((float)hs);
-    for (int item = blockIdx.x; item < n_heads * ntile; item += gridDim.x) {
-        const int h = item / ntile;
-        const int t = (item - h * ntile) * kA8Pos + tid / 4;
-        const int hk = h / kv_mul;
-        const int tc = min(t, n - 1);
-        const int8_t* kr = k8 + ((size_t)hk * max_t + tc) * hs;
-        const float* qh = q + (size_t)h * hs;
+    const int nch = hs / 16;
+    const float* qh = q + (size_t)h * hs;
+    float4 qr[kA8Chunks];
+#pragma unroll
+    for (int i = 0; i < kA8Chunks; i++)
+        qr[i] = i < nch ? *reinterpret_cast<const float4*>(qh + 4 * sub + 16 * i) : make_float4(0, 0, 0, 0);
+    const int8_t* kb = k8 + (size_t)hk * max_t * hs;
+    int kw[kA8Chunks];
+    auto load_round = [&](int t0, int (&w)[kA8Chunks]) {
+        const int tc = min(t0 + tid / 4, n - 1);
+#pragma unroll
+        for (int i = 0; i < kA8Chunks; i++)
+            if (i < nch) w[i] = *reinterpret_cast<const int*>(kb + (size_t)tc * hs + 4 * sub + 16 * i);
+    };
+    load_round(0, kw);
+    __syncthreads();   // the appended row in LDS
+    for (int t0 = 0; t0 < n; t0 += kA8Threads / 4) {
+        int kn[kA8Chunks];
+        load_round(min(t0 + kA8Threads / 4, n - 1), kn);
+        const int t = t0 + tid / 4;
+        const bool own = append && min(t, n - 1) == pos;
         float acc = 0.0f;
-        for (int c = 4 * sub; c < hs; c += 16) {
-            const int w = *reinterpret_cast<const int*>(kr + c);
-            const float4 qq = *reinterpret_cast<const float4*>(qh + c);
-            acc = __builtin_fmaf(qq.x, sbyte(w, 0), acc);
-            acc = __builtin_fmaf(qq.y, sbyte(w, 1), acc);
-            acc = __builtin_fmaf(qq.z, sbyte(w, 2), acc);
-            acc = __builtin_fmaf(qq.w, sbyte(w, 3), acc);
+#pragma unroll
+        for (int i = 0; i < kA8Chunks; i++) {
+            if (i < nch) {
+                const int w = own ? *reinterpret_cast<const int*>(krow + 4 * sub + 16 * i) : kw[i];
+                acc = __builtin_fmaf(qr[i].x, sbyte(w, 0), acc);
+                acc = __builtin_fmaf(qr[i].y, sbyte(w, 1), acc);
+                acc = __builtin_fmaf(qr[i].z, sbyte(w, 2), acc);
+                acc = __builtin_fmaf(qr[i].w, sbyte(w, 3), acc);
+            }
         }
         acc += __shfl_xor(acc, 1);
         acc += __shfl_xor(acc, 2);
-        if (sub == 0 && t < n) scores[(size_t)h * max_t + t] = acc / rs * ks[(size_t)hk * max_t + t];
+        if (sub == 0 && t < n) sc[t] = acc / rs * (own ? red[2 * kA8Waves] : ks[(size_t)hk * max_t + t]);
+#pragma unroll
+        for (int i = 0; i < kA8Chunks; i++) kw[i] = kn[i];
     }
-}
+    __syncthreads();
 
-// Softmax and p*V over the int8 cache (v5-cuda-fused/run.cu:373-398), one
-// workgroup per head: max and sum as block reductions, e_t * vs_t kept in
-// LDS, then thread (slice, g) accumulates elements 4g..4g+3 over positions
-// t = slice (mod slices); the slices are added in LDS in slice order and
-// divided by the sum.  Every reduction has a fixed order (restated by the
-// oracle's orc_attention_kv8_ordered), so results are reproducible bit for
-// bit.  Needs hs % 4 == 0.
-__host__ __device__ constexpr size_t attn8_v_lds_bytes(int max_t) {
-    return ((size_t)(max_t + 3) / 4 * 4 + 4 * kAttnThreads + 16) * sizeof(float);
-}
-__global__ __launch_bounds__(kAttnThreads) void k_attn8_softmax_v(
-    const float* __restrict__ scores, const int8_t* __restrict__ v8, const float* __restrict__ vs,
-    float* __restrict__ out, const int* __restrict__ meta, int pos_arg, int kv_mul, int hs, int max_t) {
-    extern __shared__ __attribute__((aligned(16))) float sm8[];
-    float* pe = sm8;                                   // [max_t] e_t * vs_t
-    float* part = pe + (max_t + 3) / 4 * 4;            // [slices][hs] partial sums
-    float* red = part + 4 * kAttnThreads;              // [8] block reductions
-    const int h = blockIdx.x, hk = h / kv_mul;
-    const int tid = threadIdx.x, lane = tid & (L2Q_WAVE - 1), wv = tid / L2Q_WAVE;
-    const int pos = meta_pos(meta, pos_arg);
-    const int n = pos + 1;
-    const float* sc = scores + (size_t)h * max_t;
+    // softmax
     float m = -INFINITY;
-    for (int t = tid; t < n; t += kAttnThreads) m = fmaxf(m, sc[t]);
+    for (int t = tid; t < n; t += kA8Threads) m = fmaxf(m, sc[t]);
     m = group_max<L2Q_WAVE>(m);
     if (lane == 0) red[wv] = m;
     __syncthreads();
-    m = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
-    float sum = 0.0f;
-    for (int t = tid; t < n; t += kAttnThreads) {
-        const float e = exp_runq(sc[t] - m);   // the host C library's expf, bit for bit
-        sum += e;
-        pe[t] = e * vs[(size_t)hk * max_t + t];
+    m = red[0];
+#pragma unroll
+    for (int w = 1; w < kA8Threads / L2Q_WAVE; w++) m = fmaxf(m, red[w]);
+    {
+        float sum = 0.0f;
+        for (int t = tid; t < n; t += kA8Threads) {
+            const float e = exp_runq(sc[t] - m);   // the host C library's expf, bit for bit
+            sum += e;
+            sc[t] = e * (append && t == pos ? red[2 * kA8Waves + 1] : vs[(size_t)hk * max_t + t]);
+        }
+        for (int o = 32; o > 0; o >>= 1) sum += __shfl_xor(sum, o);
+        if (lane == 0) red[kA8Waves + wv] = sum;
     }
-    for (int o = 32; o > 0; o >>= 1) sum += __shfl_xor(sum, o);
-    if (lane == 0) red[4 + wv] = sum;
     __syncthreads();
-    sum = (red[4] + red[5]) + (red[6] + red[7]);
-    const int groups = hs / 4, slices = kAttnThreads / groups;
+    float tree[kA8Waves];
+#pragma unroll
+    for (int w = 0; w < kA8Waves; w++) tree[w] = red[kA8Waves + w];
+#pragma unroll
+    for (int width = kA8Waves / 2; width >= 1; width /= 2)
+#pragma unroll
+        for (int w = 0; w < width; w++) tree[w] = tree[2 * w] + tree[2 * w + 1];
+    const float sum = tree[0];
+    const int groups = hs / 4, slices = kA8Threads / groups;
     const int gi = tid % groups, slice = tid / groups;
-    float4 acc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
     if (slice < slices) {
+        float4 acc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
         const int8_t* vb = v8 + (size_t)hk * max_t * hs + 4 * gi;
 #pragma unroll 8
         for (int t = slice; t < n; t += slices) {
-            const int w = *reinterpret_cast<const int*>(vb + (size_t)t * hs);
-            const float p = pe[t];
+            const int w = append && t == pos ? *reinterpret_cast<const int*>(vrow + 4 * gi)
+                                             : *reinterpret_cast<const int*>(vb + (size_t)t * hs);
+            const float p = sc[t];
             acc.x = __builtin_fmaf(p, sbyte(w, 0), acc.x);
             acc.y = __builtin_fmaf(p, sbyte(w, 1), acc.y);
             acc.z = __builtin_fmaf(p, sbyte(w, 2), acc.z);
@@ -864,10 +932,10 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn8_softmax_v(
         *reinterpret_cast<float4*>(part + (size_t)slice * hs + 4 * gi) = acc;
     }
     __syncthreads();
-    for (int d = tid; d < hs; d += kAttnThreads) {
-        float s = 0.0f;
-        for (int sl = 0; sl < slices; sl++) s += part[(size_t)sl * hs + d];
-        out[(size_t)h * hs + d] = s / sum;
+    for (int d = tid; d < hs; d += kA8Threads) {
+        float s2 = 0.0f;
+        for (int sl = 0; sl < slices; sl++) s2 += part[(size_t)sl * hs + d];
+        out[(size_t)h * hs + d] = s2 / sum;
     }
 }
 

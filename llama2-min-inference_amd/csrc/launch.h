@@ -65,9 +65,12 @@ bool kv8_shape_ok(int n_heads, int n_kv_heads, int hs, int max_t);
 int launch_kv8_append(const float* k, const float* v, int8_t* k8, int8_t* v8, float* ks, float* vs,
                       const float* rope, const int* meta, int pos, int n_kv_heads, int hs, int max_t,
                       hipStream_t st);
-int launch_attention_kv8(const float* q, const int8_t* k8, const int8_t* v8, const float* ks, const float* vs,
-                         float* out, float* scores, const int* meta, int pos, int n_heads, int n_kv_heads, int hs,
-                         int max_t, hipStream_t st);
+// The one-kernel int8-cache attention (k_attn8_fused).  With kst / vst (the
+// step's rotated k and v rows, [n_kv][hs]) it first appends position pos to
+// the caches (the k_kv8_append operations); without them it only reads.
+int launch_attention_kv8(const float* q, int8_t* k8, int8_t* v8, float* ks, float* vs, float* out, float* scores,
+                         const int* meta, int pos, int n_heads, int n_kv_heads, int hs, int max_t, hipStream_t st,
+                         const float* kst = nullptr, const float* vst = nullptr);
 
 // Score workgroups for n positions: ~128 positions each, at most 64.
 inline int score_splits(int n) {

@@ -325,24 +325,30 @@ int launch_kv8_append(const float* k, const float* v, int8_t* k8, int8_t* v8, fl
     return check_launch("kv8_append");
 }
 
-int launch_attention_kv8(const float* q, const int8_t* k8, const int8_t* v8, const float* ks, const float* vs,
-                         float* out, float* scores, const int* meta, int pos, int n_heads, int n_kv_heads, int hs,
-                         int max_t, hipStream_t st) {
-    if (!kv8_shape_ok(n_heads, n_kv_heads, hs, max_t) || (!meta && (pos < 0 || pos >= max_t))) {
+int launch_attention_kv8(const float* q, int8_t* k8, int8_t* v8, float* ks, float* vs, float* out, float* scores,
+                         const int* meta, int pos, int n_heads, int n_kv_heads, int hs, int max_t, hipStream_t st,
+                         const float* kst, const float* vst) {
+    if (!kv8_shape_ok(n_heads, n_kv_heads, hs, max_t) || (!meta && (pos < 0 || pos >= max_t)) ||
+        (!kst != !vst)) {
         set_error("attention kv8: bad shape heads=%d kv_heads=%d hs=%d pos=%d max_t=%d", n_heads, n_kv_heads, hs,
                   pos, max_t);
         return L2Q_ERR_ARG;
     }
+    (void)scores;
     const int kv_mul = n_heads / n_kv_heads;
-    // a captured graph covers every position the cache can hold
-    const int items = n_heads * (((meta ? max_t : pos + 1) + kA8Pos - 1) / kA8Pos);
-    hipLaunchKernelGGL(k_attn8_scores, dim3(items < kA8GridMax ? items : kA8GridMax), dim3(kAttnThreads), 0, st, q,
-                       k8, ks, scores, meta, pos, kv_mul, n_heads, hs, max_t);
-    int rc = check_launch("attention_kv8_scores");
-    if (rc) return rc;
-    hipLaunchKernelGGL(k_attn8_softmax_v, dim3(n_heads), dim3(kAttnThreads), attn8_v_lds_bytes(max_t), st, scores,
-                       v8, vs, out, meta, pos, kv_mul, hs, max_t);
-    return check_launch("attention_kv8_softmax_v");
+    const size_t lds = attn8_fused_lds_bytes(max_t);
+    if (lds > 65536) {   // above the default dynamic-LDS limit: raise it once
+        static int raised = 0;
+        if (raised < (int)lds) {
+            hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&k_attn8_fused),
+                                               hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+            if (e != hipSuccess) return hip_fail(e, "attention kv8: raising the LDS limit");
+            raised = (int)lds;
+        }
+    }
+    hipLaunchKernelGGL(k_attn8_fused, dim3(n_heads), dim3(kA8Threads), lds, st, q, kst, vst, k8, v8, ks, vs, out,
+                       meta, pos, kv_mul, hs, max_t);
+    return check_launch("attention_kv8");
 }
 
 // ---------------------------------------------------------------------------
@@ -595,11 +601,10 @@ int l2q_attention_kv8(const float* q, const int8_t* kcache8, const int8_t* vcach
                   head_size, pos, max_t);
         return L2Q_ERR_ARG;
     }
-    float* scratch = nullptr;
-    int rc = attn_scratch((size_t)n_heads * max_t, &scratch);
-    if (rc) return rc;
-    return launch_attention_kv8(q, kcache8, vcache8, kscale, vscale, out, scratch, nullptr, pos, n_heads, n_kv_heads,
-                                head_size, max_t, (hipStream_t)stream);
+    // no staging rows: the caches are only read
+    return launch_attention_kv8(q, const_cast<int8_t*>(kcache8), const_cast<int8_t*>(vcache8),
+                                const_cast<float*>(kscale), const_cast<float*>(vscale), out, nullptr, nullptr, pos,
+                                n_heads, n_kv_heads, head_size, max_t, (hipStream_t)stream);
 }
 
 int l2q_attention_split(const float* q, const float* kcache, const float* vcache, float* out, int pos, int n_heads,

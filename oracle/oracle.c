@@ -334,15 +334,15 @@ void orc_attention_kv8(const float* q, const int8_t* kc, const int8_t* vc, const
 }
 
 /* The same attention in the float order of this build's GPU kernels
- * (k_attn8_scores / k_attn8_softmax_v), so that the int8-KV decode can be
+ * (k_attn8_fused), so that the int8-KV decode can be
  * compared bit for bit; pinned to orc_attention_kv8 (double) by the tests.
  *   score_t: four partial FMA chains, chain j over the 4-element chunks
  *            c = 4j + 16i in order, combined as (a0+a1)+(a2+a3); then
  *            (dot / sqrtf(hs)) * ks_t
- *   sum:     256 partial sums (thread j: t = j, j+256, ...), each wave's 64
- *            combined by the xor butterfly 32,16,...,1, the four waves as
- *            (w0+w1)+(w2+w3); e_t = expf(score_t - max)
- *   out[d]:  S = 256/(hs/4) slices, slice s: fma(e_t*vs_t, v8_t[d], acc)
+ *   sum:     1024 partial sums (thread j: t = j, j+1024, ...), each wave's 64
+ *            combined by the xor butterfly 32,16,...,1, the 16 waves by a
+ *            pairwise tree ((w0+w1)+(w2+w3))+...; e_t = expf(score_t - max)
+ *   out[d]:  S = 1024/(hs/4) slices, slice s: fma(e_t*vs_t, v8_t[d], acc)
  *            over t = s, s+S, ...; out = (((0+p_0)+p_1)+...+p_{S-1}) / sum */
 static float butterfly64(float* v) {
     for (int o = 32; o > 0; o >>= 1) {
@@ -376,18 +376,20 @@ void orc_attention_kv8_ordered(const float* q, const int8_t* kc, const int8_t* v
             sc[t] = dot / rs * ks[(size_t)t * s_t_stride + (size_t)g * s_head_stride];
             m = fmaxf(m, sc[t]);
         }
-        float part[256], wsum[4];
-        for (int j = 0; j < 256; j++) {
+        float part[1024], wsum[16];
+        for (int j = 0; j < 1024; j++) {
             part[j] = 0.0f;
-            for (int t = j; t < n; t += 256) {
+            for (int t = j; t < n; t += 1024) {
                 const float e = expf(sc[t] - m);
                 part[j] = part[j] + e;
                 pe[t] = e * vs[(size_t)t * s_t_stride + (size_t)g * s_head_stride];
             }
         }
-        for (int w = 0; w < 4; w++) wsum[w] = butterfly64(part + 64 * w);
-        const float sum = (wsum[0] + wsum[1]) + (wsum[2] + wsum[3]);
-        const int groups = hs / 4, slices = 256 / groups;
+        for (int w = 0; w < 16; w++) wsum[w] = butterfly64(part + 64 * w);
+        for (int width = 8; width >= 1; width /= 2)
+            for (int w = 0; w < width; w++) wsum[w] = wsum[2 * w] + wsum[2 * w + 1];
+        const float sum = wsum[0];
+        const int groups = hs / 4, slices = 1024 / groups;
         for (int d = 0; d < hs; d++) {
             float s = 0.0f;
             for (int sl = 0; sl < slices; sl++) {
