@@ -63,6 +63,26 @@ static int resident_blocks(const void* fn, int threads, size_t lds, int cap) {
     return blocks;
 }
 
+// Raise a kernel's dynamic-LDS limit to `lds` bytes on the current device
+// when it exceeds the default 64 KiB (gfx950 has 160 KiB per workgroup):
+// once per (kernel, device, size) and calling thread (the attribute is
+// idempotent, so threads need not share the record).
+static int raise_lds_limit(const void* fn, size_t lds, const char* what) {
+    if (lds <= 65536) return L2Q_OK;
+    struct Entry { const void* fn; int dev; size_t lds; };
+    static thread_local Entry done[64];
+    static thread_local int used = 0;
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return hip_fail(e, what);
+    for (int i = 0; i < used; i++)
+        if (done[i].fn == fn && done[i].dev == dev && done[i].lds >= lds) return L2Q_OK;
+    e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+    if (e != hipSuccess) return hip_fail(e, what);
+    if (used < 64) done[used++] = Entry{fn, dev, lds};
+    return L2Q_OK;
+}
+
 // One workgroup per CU (see gemv_waves).
 constexpr int kGemvBlocksPerCu = 1;
 constexpr size_t kGemvMaxLds = 160 * 1024;   // gfx950 LDS per workgroup
@@ -73,14 +93,7 @@ static int go_gemv(const GemvArgs& a, hipStream_t st) {
     const size_t lds = gemv_lds_bytes(PRO, a.cols, G, BITS, PR);
     constexpr int W = gemv_waves(NS);
     const void* fn = reinterpret_cast<const void*>(&k_gemv<BITS, G, NS, PRO, EPI, PR>);
-    if (lds > 65536) {   // above the default dynamic-LDS limit: raise it once per kernel
-        static int raised = 0;
-        if (raised < (int)lds) {
-            hipError_t e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
-            if (e != hipSuccess) return hip_fail(e, "gemv: raising the LDS limit");
-            raised = (int)lds;
-        }
-    }
+    if (int rc = raise_lds_limit(fn, lds, "gemv: raising the LDS limit")) return rc;
     const int maxb = resident_blocks(fn, W * L2Q_WAVE, lds, kGemvBlocksPerCu);
     const int nunits = (a.rows + PR - 1) / PR;
     int blocks = (nunits + W - 1) / W;
@@ -241,14 +254,7 @@ static int go_attn_fused_l(const float* q, const float* kcache, const float* vca
                            int pos, int kv_mul, int n_heads, int max_t, hipStream_t st) {
     const size_t lds = attn_fused_lds_bytes(max_t, HS);
     const void* fn = reinterpret_cast<const void*>(&k_attn_fused<HS, KIL>);
-    if (lds > 65536) {   // above the default dynamic-LDS limit: raise it once per kernel
-        static int raised = 0;
-        if (raised < (int)lds) {
-            hipError_t e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
-            if (e != hipSuccess) return hip_fail(e, "attention: raising the LDS limit");
-            raised = (int)lds;
-        }
-    }
+    if (int rc = raise_lds_limit(fn, lds, "attention: raising the LDS limit")) return rc;
     hipLaunchKernelGGL((k_attn_fused<HS, KIL>), dim3(n_heads * (HS / kVDims)), dim3(kAfThreads), lds, st, q, kcache,
                        vcache, out, meta, pos, kv_mul, n_heads, max_t);
     return check_launch("attention_fused");
@@ -337,15 +343,9 @@ int launch_attention_kv8(const float* q, int8_t* k8, int8_t* v8, float* ks, floa
     (void)scores;
     const int kv_mul = n_heads / n_kv_heads;
     const size_t lds = attn8_fused_lds_bytes(max_t);
-    if (lds > 65536) {   // above the default dynamic-LDS limit: raise it once
-        static int raised = 0;
-        if (raised < (int)lds) {
-            hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&k_attn8_fused),
-                                               hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
-            if (e != hipSuccess) return hip_fail(e, "attention kv8: raising the LDS limit");
-            raised = (int)lds;
-        }
-    }
+    if (int rc = raise_lds_limit(reinterpret_cast<const void*>(&k_attn8_fused), lds,
+                                 "attention kv8: raising the LDS limit"))
+        return rc;
     hipLaunchKernelGGL(k_attn8_fused, dim3(n_heads), dim3(kA8Threads), lds, st, q, kst, vst, k8, v8, ks, vs, out,
                        meta, pos, kv_mul, hs, max_t);
     return check_launch("attention_kv8");
@@ -394,11 +394,8 @@ int launch_pf_gemm(int bits, int group, const void* w, const float* ws, int rows
     const uint8_t* wb = static_cast<const uint8_t*>(w);
     int rc = L2Q_OK;
     auto go = [&](auto kern, size_t lds) {
-        const void* fn = reinterpret_cast<const void*>(kern);
-        if (lds > 65536) {
-            hipError_t e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
-            if (e != hipSuccess) { rc = hip_fail(e, "prefill gemm: raising the LDS limit"); return; }
-        }
+        if ((rc = raise_lds_limit(reinterpret_cast<const void*>(kern), lds, "prefill gemm: raising the LDS limit")))
+            return;
         hipLaunchKernelGGL(kern, grid, dim3(kPf2Threads), lds, st, wb, ws, rows, cols, xqp, xs, sq, xt, T, out, ldo);
     };
 #define L2Q_PF2(B_, G_)                                                                    \
