@@ -765,10 +765,17 @@ __global__ __launch_bounds__(gemv_waves(NS) * L2Q_WAVE) void k_gemv(GemvArgs a) 
         } else if (EPI == kRopeKV) {
             // rows come in (even, odd) pairs held by lanes (0,1), (2,3), ...
             const float other = dpp_f<kDppXor1>(sum);
+            // x / hs without an integer division: for 0 <= x < 2^24 and
+            // hs <= 256, umulhi(x, floor((2^32-1)/hs) + 1) is the exact
+            // quotient (the multiplier exceeds 2^32/hs by less than 1, so
+            // the error x*(m - 2^32/hs)/2^32 stays below 1/hs)
+            const unsigned hs_m = 0xFFFFFFFFu / (unsigned)a.hs + 1u;
+            auto hsdiv = [&](int x) { return (int)__umulhi((unsigned)x, hs_m); };
             // (cos, sin) of this lane's pair, gathered from the RoPE
             // registers by every lane (a permute reads any lane's value)
             const int e = row < a.dim ? row : row - a.dim;
-            const int hd = (e & ~1) % a.hs;
+            const int eg = hsdiv(e);                      // head of the row
+            const int hd = (e & ~1) - eg * a.hs;          // even element of the pair (hs is even)
             float c = 0.0f, s = 0.0f;
 #pragma unroll
             for (int k = 0; k < kRopeRegs; k++) {
@@ -783,10 +790,11 @@ __global__ __launch_bounds__(gemv_waves(NS) * L2Q_WAVE) void k_gemv(GemvArgs a) 
                 if (row < a.dim + a.kv_dim) {            // q or k: rotate
                     const float r = odd ? __builtin_fmaf(v0, s, v1 * c) : __builtin_fmaf(v0, c, -(v1 * s));
                     if (row < a.dim) a.out[row] = r;
-                    else a.kcache[k_index(a.k_il, e / a.hs, cpos, e % a.hs, a.hs, a.max_t)] = r;
+                    else a.kcache[k_index(a.k_il, eg, cpos, e - eg * a.hs, a.hs, a.max_t)] = r;
                 } else {                                  // v: appended as is
                     const int ev = row - a.dim - a.kv_dim;
-                    a.vcache[((size_t)(ev / a.hs) * a.max_t + cpos) * a.hs + (ev % a.hs)] = sum;
+                    const int gv = hsdiv(ev);
+                    a.vcache[((size_t)gv * a.max_t + cpos) * a.hs + (ev - gv * a.hs)] = sum;
                 }
             }
         } else {   // kSwiglu: (w1, w3) pairs on lanes (0,1), (2,3), ...

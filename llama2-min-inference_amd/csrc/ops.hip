@@ -154,7 +154,8 @@ int launch_gemv_fused(int bits, int group, int pro, int epi, const GemvArgs& a, 
         return L2Q_ERR_ARG;
     }
     if (epi == kRopeKV && (!a.meta || !a.rope || !a.kcache || !a.vcache || a.hs <= 0 || a.hs % 2 || a.dim % a.hs ||
-                           a.kv_dim % a.hs || a.rows != a.dim + 2 * a.kv_dim || !a.out || a.max_t <= 0)) {
+                           a.kv_dim % a.hs || a.rows != a.dim + 2 * a.kv_dim || !a.out || a.max_t <= 0 ||
+                           a.hs > kAttnMaxHs || a.rows >= 65536)) {
         set_error("gemv: bad RoPE/KV epilogue arguments");
         return L2Q_ERR_ARG;
     }
