@@ -568,7 +568,8 @@ __global__ __launch_bounds__(gemv_waves(NS) * L2Q_WAVE) void k_gemv(GemvArgs a) 
     const int nb = a.cols / G;
     const int nbp = gemv_nbp(nb);
     const int F = gemv_fold_rows(nb, WAVES);   // rows per fold batch
-    const int UB = F / PR;                     // units per fold batch
+    const int UB = F / PR;                     // units per fold batch (1, 2, 4 or 8)
+    const int ubm = UB - 1;                    // x % UB == x & ubm
     float* tb = lds + (size_t)wv * 2 * F * nbp;
     float* sb = tb + F * nbp;
     int8_t* act_q = reinterpret_cast<int8_t*>(lds + gemv_fold_floats(nb, WAVES));
@@ -724,7 +725,7 @@ __global__ __launch_bounds__(gemv_waves(NS) * L2Q_WAVE) void k_gemv(GemvArgs a) 
     // dots and per-group terms of row k of unit u into fold-batch row br
     auto consume_row = [&](int k, int u) {
         const int row = (gw + u * nwaves) * PR + k;
-        const int br = ((u - u0) % UB) * PR + k;
+        const int br = ((u - u0) & ubm) * PR + k;
 #pragma unroll
         for (int s = 0; s < NS; s++) {
             const int off = s * kSweepBytes + 16 * lane;
@@ -818,11 +819,11 @@ __global__ __launch_bounds__(gemv_waves(NS) * L2Q_WAVE) void k_gemv(GemvArgs a) 
         __builtin_amdgcn_sched_barrier(0);
         load_unit(u + 1);
         __builtin_amdgcn_sched_barrier(0);
-        if ((u - u0 + 1) % UB == 0) fold_batch(u + 1 - UB, F);
+        if (((u - u0 + 1) & ubm) == 0) fold_batch(u + 1 - UB, F);
     }
 #pragma unroll
     for (int k = 0; k < PR; k++) consume_row(k, u1 - 1);
-    const int last = (u1 - u0 - 1) % UB + 1;   // units in the last batch
+    const int last = ((u1 - u0 - 1) & ubm) + 1;   // units in the last batch
     fold_batch(u1 - last, last * PR);
 }
 
