@@ -600,7 +600,7 @@ constexpr int kAfRounds = kScorePer * kAttnThreads / kAfThreads;  // positions p
 constexpr int kAfDefaultMax = kScorePer * kAttnThreads;         // see attention_fused_max
 __host__ __device__ constexpr size_t attn_fused_lds_bytes(int max_t, int hs) {
     return ((size_t)(hs + 3) / 4 * 4 + (size_t)(max_t + 3) / 4 * 4 + kRingSlack + 2 * kVDims * kAfStride +
-            kRingSlack + 16) * sizeof(float);
+            kRingSlack + 16 + 64) * sizeof(float);
 }
 template <int HS, int KIL>
 __global__ __launch_bounds__(kAfThreads) void k_attn_fused(
@@ -614,6 +614,7 @@ __global__ __launch_bounds__(kAfThreads) void k_attn_fused(
     float* p = qs + (HS + 3) / 4 * 4;                        // [max_t] scores, e_t, then p_t
     float* vt = p + (max_t + 3) / 4 * 4 + kRingSlack;        // [2][kVDims][kAfStride]
     float* red = vt + 2 * kVDims * kAfStride + kRingSlack;   // [8] wave maxima, [8] sum
+    uint64_t* etab = reinterpret_cast<uint64_t*>(red + 16);  // [32] exp table
     const int h = blockIdx.x % n_heads, d0 = (blockIdx.x / n_heads) * kVDims;
     const int tid = threadIdx.x, lane = tid & (L2Q_WAVE - 1), wv = tid / L2Q_WAVE;
     const int n = meta_pos(meta, pos_arg) + 1;
@@ -622,10 +623,17 @@ __global__ __launch_bounds__(kAfThreads) void k_attn_fused(
     const int nchunks = (n + kAfChunk - 1) / kAfChunk;
 
     // loads in the order they are needed (they complete in order): q, the
-    // first round's K rows, the first V chunk
-    if (tid < F4) reinterpret_cast<float4*>(qs)[tid] = reinterpret_cast<const float4*>(q + (size_t)h * HS)[tid];
+    // first round's K rows, the first V chunk.  The q load and its LDS store
+    // are unconditional (clamped index; duplicates store equal values): a
+    // load or store under a thread condition can be sunk behind the later
+    // loads, and waiting for it then waits for them.  K and V rows are
+    // skipped by whole waves past the context (wave-uniform branches), the
+    // rest clamped to it: every load instruction of the per-CU load path
+    // then carries positions that are used.
+    const float4 qv = reinterpret_cast<const float4*>(q + (size_t)h * HS)[min(tid, F4 - 1)];
     float4 kr[F4];
     auto load_k = [&](int t) {   // column-interleaved: one coalesced KiB per column and wave
+        if (__builtin_amdgcn_readfirstlane(t) >= n) return;
         t = min(t, n - 1);
 #pragma unroll
         for (int f = 0; f < F4; f++) kr[f] = KIL ? kbase[(size_t)f * max_t + t] : kbase[(size_t)t * F4 + f];
@@ -637,9 +645,9 @@ __global__ __launch_bounds__(kAfThreads) void k_attn_fused(
         for (int k = 0; k < kAfVPer; k++) {
             const int e = tid + kAfThreads * k;                  // float4 index in the chunk
             const int r = e / (kVDims / 4), c4 = e % (kVDims / 4);
-            const int t = c * kAfChunk + r;
-            vr[k] = t < n ? *reinterpret_cast<const float4*>(vbase + (size_t)t * HS + 4 * c4)
-                          : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+            const int t = c * kAfChunk + r;              // positions >= n are never folded
+            if (__builtin_amdgcn_readfirstlane(t) >= n) continue;
+            vr[k] = *reinterpret_cast<const float4*>(vbase + (size_t)min(t, n - 1) * HS + 4 * c4);
         }
     };
     auto store_chunk = [&](int buf) {   // transposed: vt[buf][element][position]
@@ -655,7 +663,14 @@ __global__ __launch_bounds__(kAfThreads) void k_attn_fused(
         }
     };
     load_chunk(0);
-    __syncthreads();   // qs
+    // the exp table through the scalar cache (uniform loads: no vector
+    // memory traffic, no 512 lanes per workgroup on one table)
+    uint64_t tabv = 0;
+#pragma unroll
+    for (int i = 0; i < 32; i++) tabv = (lane & 31) == i ? kExp2Tab[i] : tabv;
+    reinterpret_cast<float4*>(qs)[min(tid, F4 - 1)] = qv;
+    if (wv == 0) etab[lane & 31] = tabv;
+    __syncthreads();   // qs, etab
 
     // scores: round r covers positions r*kAfThreads + tid
     float s[kAfRounds];
@@ -693,7 +708,7 @@ __global__ __launch_bounds__(kAfThreads) void k_attn_fused(
         const int t = kAfThreads * r + tid;
         e[r] = 0.0f;
         if (kAfThreads * r < n && t < n) {
-            e[r] = exp_runq(s[r] - m);
+            e[r] = exp_runq_t(s[r] - m, etab);
             p[t] = e[r];
         }
     }
