@@ -626,27 +626,29 @@ __global__ __launch_bounds__(kAfThreads) void k_attn_fused(
     // first round's K rows, the first V chunk.  The q load and its LDS store
     // are unconditional (clamped index; duplicates store equal values): a
     // load or store under a thread condition can be sunk behind the later
-    // loads, and waiting for it then waits for them.  K and V rows are
-    // skipped by whole waves past the context (wave-uniform branches), the
-    // rest clamped to it: every load instruction of the per-CU load path
-    // then carries positions that are used.
+    // loads, and waiting for it then waits for them.  In the first round
+    // and chunk (all of a short context), whole waves past the context skip
+    // their K and V loads (wave-uniform branches), so that the per-CU load
+    // path carries only positions that are used; the later ones load
+    // clamped positions unconditionally, so that the next chunk's loads
+    // stay in flight while the current one is folded.
     const float4 qv = reinterpret_cast<const float4*>(q + (size_t)h * HS)[min(tid, F4 - 1)];
     float4 kr[F4];
-    auto load_k = [&](int t) {   // column-interleaved: one coalesced KiB per column and wave
-        if (__builtin_amdgcn_readfirstlane(t) >= n) return;
+    auto load_k = [&](int t, bool skip) {   // column-interleaved: one coalesced KiB per column and wave
+        if (skip && __builtin_amdgcn_readfirstlane(t) >= n) return;
         t = min(t, n - 1);
 #pragma unroll
         for (int f = 0; f < F4; f++) kr[f] = KIL ? kbase[(size_t)f * max_t + t] : kbase[(size_t)t * F4 + f];
     };
-    load_k(tid);
+    load_k(tid, true);
     float4 vr[kAfVPer];
-    auto load_chunk = [&](int c) {
+    auto load_chunk = [&](int c, bool skip) {
 #pragma unroll
         for (int k = 0; k < kAfVPer; k++) {
             const int e = tid + kAfThreads * k;                  // float4 index in the chunk
             const int r = e / (kVDims / 4), c4 = e % (kVDims / 4);
             const int t = c * kAfChunk + r;              // positions >= n are never folded
-            if (__builtin_amdgcn_readfirstlane(t) >= n) continue;
+            if (skip && __builtin_amdgcn_readfirstlane(t) >= n) continue;
             vr[k] = *reinterpret_cast<const float4*>(vbase + (size_t)min(t, n - 1) * HS + 4 * c4);
         }
     };
@@ -662,7 +664,7 @@ __global__ __launch_bounds__(kAfThreads) void k_attn_fused(
             dst[(4 * c4 + 3) * kAfStride + r] = vr[k].w;
         }
     };
-    load_chunk(0);
+    load_chunk(0, true);
     // the exp table through the scalar cache (uniform loads: no vector
     // memory traffic, no 512 lanes per workgroup on one table)
     uint64_t tabv = 0;
@@ -681,7 +683,7 @@ __global__ __launch_bounds__(kAfThreads) void k_attn_fused(
         s[r] = -INFINITY;
         if (kAfThreads * r >= n) continue;   // uniform
         const int t = kAfThreads * r + tid;
-        if (r > 0) load_k(t);
+        if (r > 0) load_k(t, false);
         float score = 0.0f;
 #pragma unroll
         for (int f = 0; f < F4; f++) {
@@ -726,7 +728,7 @@ __global__ __launch_bounds__(kAfThreads) void k_attn_fused(
 
     float acc = 0.0f;
     for (int c = 0; c < nchunks; c++) {
-        if (c + 1 < nchunks) load_chunk(c + 1);
+        if (c + 1 < nchunks) load_chunk(c + 1, false);
         if (wv == 0 && lane < kVDims) {
             const int tb = c * kAfChunk;
             acc = serial_pv(p + tb, vt + (c & 1) * kVDims * kAfStride + lane * kAfStride, min(kAfChunk, n - tb), acc);
@@ -830,7 +832,7 @@ constexpr int kA8Chunks = kAttnMaxHs / 16;               // K dwords per lane an
 // Byte b of w as a signed value.
 __device__ __forceinline__ float sbyte(int w, int b) { return (float)((w << (24 - 8 * b)) >> 24); }
 __host__ __device__ constexpr size_t attn8_fused_lds_bytes(int max_t) {
-    return ((size_t)(max_t + 3) / 4 * 4 + 4 * kA8Threads + 3 * kA8Waves + 2 * kAttnMaxHs / 4) * sizeof(float);
+    return ((size_t)(max_t + 3) / 4 * 4 + 4 * kA8Threads + 3 * kA8Waves + 2 * kAttnMaxHs / 4 + 64) * sizeof(float);
 }
 __global__ __launch_bounds__(kA8Threads) void k_attn8_fused(
     const float* __restrict__ q, const float* __restrict__ kst, const float* __restrict__ vst,
@@ -842,6 +844,7 @@ __global__ __launch_bounds__(kA8Threads) void k_attn8_fused(
     float* red = part + 4 * kA8Threads;                // [16] wave maxima, [16] wave sums, [2] row scales
     int8_t* krow = reinterpret_cast<int8_t*>(red + 3 * kA8Waves);   // [hs] appended k row, then [hs] v row
     int8_t* vrow = krow + kAttnMaxHs;
+    uint64_t* etab = reinterpret_cast<uint64_t*>(vrow + kAttnMaxHs);   // [32] exp table
     const int h = blockIdx.x, hk = h / kv_mul;
     const int tid = threadIdx.x, lane = tid & (L2Q_WAVE - 1), wv = tid / L2Q_WAVE, sub = tid & 3;
     const int pos = meta_pos(meta, pos_arg);
@@ -876,7 +879,13 @@ __global__ __launch_bounds__(kA8Threads) void k_attn8_fused(
             if (i < nch) w[i] = *reinterpret_cast<const int*>(kb + (size_t)tc * hs + 4 * sub + 16 * i);
     };
     load_round(0, kw);
-    __syncthreads();   // the appended row in LDS
+    if (wv == 2) {   // the exp table through the scalar cache (uniform loads)
+        uint64_t tabv = 0;
+#pragma unroll
+        for (int i = 0; i < 32; i++) tabv = (lane & 31) == i ? kExp2Tab[i] : tabv;
+        etab[lane & 31] = tabv;
+    }
+    __syncthreads();   // the appended row and the exp table in LDS
     for (int t0 = 0; t0 < n; t0 += kA8Threads / 4) {
         int kn[kA8Chunks];
         load_round(min(t0 + kA8Threads / 4, n - 1), kn);
@@ -913,7 +922,7 @@ __global__ __launch_bounds__(kA8Threads) void k_attn8_fused(
     {
         float sum = 0.0f;
         for (int t = tid; t < n; t += kA8Threads) {
-            const float e = exp_runq(sc[t] - m);   // the host C library's expf, bit for bit
+            const float e = exp_runq_t(sc[t] - m, etab);   // the host C library's expf, bit for bit
             sum += e;
             sc[t] = e * (append && t == pos ? red[2 * kA8Waves + 1] : vs[(size_t)hk * max_t + t]);
         }
