@@ -69,6 +69,20 @@ __device__ __forceinline__ float dpp_f(float v) {
 // of two <= 64): every lane gets the result of its own group.  Both are
 // exact in any order; within a 16-lane row the butterfly is xor1, xor2,
 // half mirror, mirror (after the last two steps every lane has seen all 16).
+// group_max on unsigned values (the bit patterns of non-negative floats
+// order as the floats do): one integer max per step, with the lane move
+// folded into it.
+template <int W>
+__device__ __forceinline__ unsigned group_umax(unsigned v) {
+    if (W >= 2) v = max(v, (unsigned)dpp_i<kDppXor1>((int)v));
+    if (W >= 4) v = max(v, (unsigned)dpp_i<kDppXor2>((int)v));
+    if (W >= 8) v = max(v, (unsigned)dpp_i<kDppHalfMirror>((int)v));
+    if (W >= 16) v = max(v, (unsigned)dpp_i<kDppMirror>((int)v));
+    if (W >= 32) v = max(v, (unsigned)__shfl_xor((int)v, 16, L2Q_WAVE));
+    if (W >= 64) v = max(v, (unsigned)__shfl_xor((int)v, 32, L2Q_WAVE));
+    return v;
+}
+
 template <int W>
 __device__ __forceinline__ float group_max(float v) {
     if (W >= 2) v = fmaxf(v, dpp_f<kDppXor1>(v));
@@ -97,8 +111,16 @@ __device__ __forceinline__ int group_isum(int v) {
 // correctly rounded IEEE one (HIP default; never built with fast-math) and
 // rintf is round-half-even, as lrintf in the reference.
 
+// amax / 127 as the correctly rounded quotient of the reference, by one
+// product and one FMA correction: s0 = amax * RN(1/127), then
+// s = fma(fma(-s0, 127, amax), RN(1/127), s0), equal to the IEEE quotient for
+// every finite amax >= 0 (fp32 denormals kept, as these kernels run; the
+// identity is checked exhaustively by the CPU test suite).  Three
+// instructions instead of the division sequence.
 __device__ __forceinline__ float q8_scale(float amax) {
-    float s = amax / 127.0f;
+    constexpr float kInv127 = 1.0f / 127.0f;
+    const float s0 = amax * kInv127;
+    const float s = __builtin_fmaf(__builtin_fmaf(-s0, 127.0f, amax), kInv127, s0);
     return s == 0.0f ? 1e-8f : s;
 }
 
@@ -106,6 +128,18 @@ __device__ __forceinline__ int q8_value(float x, float s) {
     float r = rintf(x / s);
     r = fminf(fmaxf(r, -127.0f), 127.0f);
     return (int)r;
+}
+
+// q8_value_fast as the bits of rint(q) + 1.5*2^23: adding 1.5*2^23 rounds y
+// (|y| < 128) to an integer, to nearest even as rintf does, and leaves that
+// integer in the low bits, so the int8 value is the low byte of the result
+// (no conversion instruction); the off-path quotient is rounded the same way.
+__device__ __forceinline__ unsigned q8_byte_fast(float x, float s, float r) {
+    constexpr float kMagic = 0x1.8p23f;
+    const float y = x * r;
+    float t = y + kMagic;
+    if (__builtin_expect(!(fabsf(y - (t - kMagic)) < 0.5f - 0x1p-13f), 0)) t = x / s + kMagic;
+    return __float_as_uint(t);
 }
 
 // q8_value(x, s) without a division on the common path.  With r = rcp(s)

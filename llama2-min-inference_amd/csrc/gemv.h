@@ -458,19 +458,25 @@ __device__ __forceinline__ void prologue_compute(const GemvArgs& a, float4 (&xin
             o.z = nw[k].z * (inv * o.z); o.w = nw[k].w * (inv * o.w);
         }
         if (!in) o = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-        float m = fmaxf(fmaxf(fabsf(o.x), fabsf(o.y)), fmaxf(fabsf(o.z), fabsf(o.w)));
-        m = group_max<G / 4>(m);
-        const float s = q8_scale(m);
+        // the group maximum of |o| on the bit patterns (a NaN would win here
+        // where fmaxf drops it; the reference quantizer has no defined result
+        // for one either)
+        unsigned mb = max(max(__float_as_uint(o.x) & 0x7fffffffu, __float_as_uint(o.y) & 0x7fffffffu),
+                          max(__float_as_uint(o.z) & 0x7fffffffu, __float_as_uint(o.w) & 0x7fffffffu));
+        mb = group_umax<G / 4>(mb);
+        const float s = q8_scale(__uint_as_float(mb));
         const float r = q8_recip(s);
         if (in) {
-            const int q0 = q8_value_fast(o.x, s, r), q1 = q8_value_fast(o.y, s, r);
-            const int q2 = q8_value_fast(o.z, s, r), q3 = q8_value_fast(o.w, s, r);
+            // int8 values in the low bytes (q8_byte_fast), packed by byte permutes
+            const unsigned b0 = q8_byte_fast(o.x, s, r), b1 = q8_byte_fast(o.y, s, r);
+            const unsigned b2 = q8_byte_fast(o.z, s, r), b3 = q8_byte_fast(o.w, s, r);
+            constexpr unsigned kLoBytes = 0x0c0c0400u;   // byte 0 of lo, byte 0 of hi, zeros
             if (SPLIT) {   // INT4 pre-split layout: (q0, q2) to E, (q1, q3) to O
-                *reinterpret_cast<uint16_t*>(act_q + act_split_addr(4 * c)) = (uint16_t)((q0 & 0xff) | ((q2 & 0xff) << 8));
-                *reinterpret_cast<uint16_t*>(act_q + act_split_addr(4 * c + 1)) = (uint16_t)((q1 & 0xff) | ((q3 & 0xff) << 8));
+                *reinterpret_cast<uint16_t*>(act_q + act_split_addr(4 * c)) = (uint16_t)__builtin_amdgcn_perm(b2, b0, kLoBytes);
+                *reinterpret_cast<uint16_t*>(act_q + act_split_addr(4 * c + 1)) = (uint16_t)__builtin_amdgcn_perm(b3, b1, kLoBytes);
             } else {
-                const int packed = (q0 & 0xff) | ((q1 & 0xff) << 8) | ((q2 & 0xff) << 16) | ((q3 & 0xff) << 24);
-                reinterpret_cast<int*>(act_q)[c] = packed;
+                const unsigned lo = __builtin_amdgcn_perm(b1, b0, kLoBytes), hi = __builtin_amdgcn_perm(b3, b2, kLoBytes);
+                reinterpret_cast<unsigned*>(act_q)[c] = __builtin_amdgcn_perm(hi, lo, 0x05040100u);
             }
             if ((c % (G / 4)) == 0) act_s[c / (G / 4)] = s;
         }

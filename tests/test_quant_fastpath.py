@@ -41,3 +41,18 @@ def test_fast_quantizer_equals_division():
         assert slow[pick].mean() > 0.5          # the guard does fire near the boundaries
         assert slow[~pick].mean() < 2e-3        # and almost never elsewhere
     assert np.abs(exact).max() <= 127           # the clamp of the reference never binds
+
+
+def test_scale_fma_form_equals_division_exhaustively(tmp_path):
+    """device.h q8_scale computes amax / 127 as s0 = amax * RN(1/127) plus one
+    FMA correction; over every finite float amax >= 0 it must give the
+    correctly rounded quotient of the reference (runq.c:117-139).  Built with
+    gcc from tests/q8_scale_check.c (hardware or libm fmaf: both correctly
+    rounded; no flush of denormals, as on the GPU)."""
+    import os
+    import subprocess
+    src = os.path.join(os.path.dirname(__file__), "q8_scale_check.c")
+    exe = str(tmp_path / "q8_scale_check")
+    subprocess.run(["gcc", "-O2", "-ffp-contract=off", "-fopenmp", src, "-o", exe, "-lm"], check=True)
+    out = subprocess.run([exe], check=True, capture_output=True, text=True).stdout
+    assert int(out.strip()) == 0
