@@ -648,8 +648,10 @@ __global__ __launch_bounds__(gemv_waves(NS) * L2Q_WAVE) void k_gemv(GemvArgs a) 
 #if L2Q_INPUT_FIRST
     // a computing prologue: let its inputs arrive before this grid's weight
     // requests queue in front of them (measured: faster in the decode step;
-    // pre-quantized inputs are better left to arrive with the weights)
-    if (PRO != kPreq) __builtin_amdgcn_s_waitcnt(0x0F70);   // vmcnt(0)
+    // pre-quantized inputs are better left to arrive with the weights).  A
+    // grid of one unit per wave has nothing to overlap with its only weight
+    // load, which then goes out first (uniform branch).
+    if (PRO != kPreq && nunits > nwaves) __builtin_amdgcn_s_waitcnt(0x0F70);   // vmcnt(0)
 #endif
     __builtin_amdgcn_sched_barrier(0);
 
