@@ -133,12 +133,14 @@ __device__ __forceinline__ int q8_value(float x, float s) {
 // q8_value_fast as the bits of rint(q) + 1.5*2^23: adding 1.5*2^23 rounds y
 // (|y| < 128) to an integer, to nearest even as rintf does, and leaves that
 // integer in the low bits, so the int8 value is the low byte of the result
-// (no conversion instruction); the off-path quotient is rounded the same way.
+// (no conversion instruction); the off-path quotient is clamped to +-127 and
+// rounded the same way.
 __device__ __forceinline__ unsigned q8_byte_fast(float x, float s, float r) {
     constexpr float kMagic = 0x1.8p23f;
     const float y = x * r;
     float t = y + kMagic;
-    if (__builtin_expect(!(fabsf(y - (t - kMagic)) < 0.5f - 0x1p-13f), 0)) t = x / s + kMagic;
+    if (__builtin_expect(!(fabsf(y - (t - kMagic)) < 0.5f - 0x1p-13f), 0))
+        t = fminf(fmaxf(x / s, -127.0f), 127.0f) + kMagic;
     return __float_as_uint(t);
 }
 
@@ -146,16 +148,23 @@ __device__ __forceinline__ unsigned q8_byte_fast(float x, float s, float r) {
 // (v_rcp_f32, within 1 ulp) y = x*r is within 4 ulp(y) of x/s, so rint(y)
 // equals rint(fl(x/s)) unless y lies within that distance of a half-integer
 // (the only places where the two can round differently), i.e. unless
-// |y - rint(y)| >= 0.5 - margin; there, and for non-finite y (s denormal or
-// tiny), the correctly rounded division is taken.  No clamp is needed: s is
-// amax/127 rounded, so |x/s| < 127.5 for every x of the group, and |y| < 128
-// makes 4 ulp(y) <= 2^-15; the margin used, 2^-13, is four times that.
-__device__ __forceinline__ float q8_recip(float s) { return __builtin_amdgcn_rcpf(s); }
+// |y - rint(y)| >= 0.5 - margin; there, and for non-finite y, the correctly
+// rounded division is taken, clamped to +-127 as the reference clamps.  For a
+// normal s = amax/127 rounded, |x/s| < 127.5 for every x of the group, so the
+// clamp never binds on the fast path, and |y| < 128 makes 4 ulp(y) <= 2^-15
+// (the margin used, 2^-13, is four times that).  A denormal s (a group
+// maximum below 127 * 2^-126) keeps less precision, |x/s| can pass 127.5 and
+// the clamp binds: r = +inf sends every value of such a group to the
+// division.  (Clamping before rounding equals rounding then clamping: +-127
+// are integers and rounding is monotonic.)
+__device__ __forceinline__ float q8_recip(float s) {
+    return s >= 0x1p-126f ? __builtin_amdgcn_rcpf(s) : __builtin_inff();
+}
 
 __device__ __forceinline__ int q8_value_fast(float x, float s, float r) {
     const float y = x * r;
     float q = rintf(y);
-    if (__builtin_expect(!(fabsf(y - q) < 0.5f - 0x1p-13f), 0)) q = rintf(x / s);
+    if (__builtin_expect(!(fabsf(y - q) < 0.5f - 0x1p-13f), 0)) q = rintf(fminf(fmaxf(x / s, -127.0f), 127.0f));
     return (int)q;
 }
 

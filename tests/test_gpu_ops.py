@@ -121,6 +121,29 @@ def near_tie_inputs(n, group, seed):
 
 
 @pytest.mark.parametrize("group", [32, 64])
+def test_quantize_act_extreme_scales(gpu_lib, torch_cuda, group):
+    """Group maxima from denormal to near FLT_MAX: the scale amax/127 (an
+    FMA-corrected product on the GPU) and the quantized values must match the
+    reference's division bit for bit, also where the scale is denormal."""
+    rng = np.random.default_rng(11)
+    ng = 512
+    n = ng * group
+    exps = rng.uniform(-44, 38.5, ng)
+    amax = (10.0 ** exps).astype(np.float32)
+    amax[:4] = np.array([1e-45, 3e-44, 1e-40, 3.4e38], dtype=np.float32)
+    x = (rng.uniform(-1, 1, n).astype(np.float32) * np.repeat(amax, group)).astype(np.float32)
+    x[::group] = amax
+    xq_ref, xs_ref, _ = O.quantize_act(x, group)
+    d_x = dev(torch_cuda, x)
+    xq = torch_cuda.empty(n, dtype=torch_cuda.int8, device="cuda")
+    xs = torch_cuda.empty(ng, dtype=torch_cuda.float32, device="cuda")
+    abi.call("l2q_quantize_act", d_x.data_ptr(), n, group, xq.data_ptr(), xs.data_ptr(), stream(torch_cuda))
+    torch_cuda.cuda.synchronize()
+    np.testing.assert_array_equal(xs.cpu().numpy(), xs_ref)
+    np.testing.assert_array_equal(xq.cpu().numpy(), xq_ref)
+
+
+@pytest.mark.parametrize("group", [32, 64])
 def test_quantize_act_near_ties(gpu_lib, torch_cuda, group):
     n = 1 << 16
     x = near_tie_inputs(n, group, 3)

@@ -14,7 +14,7 @@ def fast_quantize(x, s, r):
     y = (x * r).astype(F)
     q = np.rint(y).astype(F)
     slow = ~(np.abs((y - q).astype(F)) < F(0.5) - F(2.0 ** -13))
-    return np.where(slow, np.rint((x / s).astype(F)), q), slow
+    return np.where(slow, np.rint(np.clip((x / s).astype(F), F(-127), F(127))), q), slow
 
 
 def test_fast_quantizer_equals_division():
@@ -56,3 +56,26 @@ def test_scale_fma_form_equals_division_exhaustively(tmp_path):
     subprocess.run(["gcc", "-O2", "-ffp-contract=off", "-fopenmp", src, "-o", exe, "-lm"], check=True)
     out = subprocess.run([exe], check=True, capture_output=True, text=True).stdout
     assert int(out.strip()) == 0
+
+
+def test_magic_add_rounding_equals_rint():
+    """device.h q8_byte_fast rounds y (|y| < 128) by t = y + 1.5*2^23 in
+    float32 and takes the int8 value from the low byte of t's bits.  That
+    must be rint(y) (ties to even) as int8, at every half-integer and a few
+    ulps around it, and on a dense sample of the range."""
+    M = F(1.5 * 2 ** 23)
+    k = np.arange(-128, 128, dtype=np.float64)
+    y = [(k + 0.5).astype(F)]
+    for _ in range(4):
+        y.append(np.nextafter(y[-1], F(np.inf)))
+    lo = [(k + 0.5).astype(F)]
+    for _ in range(4):
+        lo.append(np.nextafter(lo[-1], F(-np.inf)))
+    rng = np.random.default_rng(5)
+    y = np.concatenate(y + lo + [k.astype(F), rng.uniform(-128, 128, 1 << 22).astype(F)])
+    y = y[np.abs(y) < 128]
+    t = (y + M).astype(F)
+    byte = (t.view(np.uint32) & 0xFF).astype(np.uint8).view(np.int8)
+    q = np.rint(y).astype(np.int32)
+    np.testing.assert_array_equal((t - M).astype(F), np.rint(y).astype(F))
+    np.testing.assert_array_equal(byte.astype(np.int32), np.where(q > 127, q - 256, q))
