@@ -181,6 +181,34 @@ def test_rmsnorm_quant(gpu_lib, torch_cuda, group, n):
     np.testing.assert_array_equal(xs.cpu().numpy(), xs_ref)
 
 
+@pytest.mark.parametrize("scale", [1e-30, 1e-21, 1e-3, 1e3, 1e18, 1e20])
+def test_rmsnorm_quant_extreme_magnitudes(gpu_lib, torch_cuda, scale):
+    """Residual streams whose squares underflow into denormals or whose sum of
+    squares overflows to inf (inv = 0), with group maxima spread over several
+    decades: the fused residual add, RMSNorm and quantize must still equal
+    the reference bit for bit."""
+    n, group = 4096, 64
+    rng = np.random.default_rng(21)
+    spread = (10.0 ** rng.uniform(-6, 0, n // group)).astype(np.float32)
+    x = (host.gauss(n, 9, 1, 1.0) * np.float32(scale) * np.repeat(spread, group)).astype(np.float32)
+    r = (host.gauss(n, 9, 2, 0.5) * np.float32(scale)).astype(np.float32)
+    w = 1.0 + host.gauss(n, 9, 3, 0.1)
+    v = (x + r).astype(np.float32)
+    o_ref = O.rmsnorm(v, w)
+    xq_ref, xs_ref, _ = O.quantize_act(o_ref, group)
+    t = torch_cuda
+    d_x, d_r, d_w = dev(t, x), dev(t, r), dev(t, w)
+    xout = t.empty(n, dtype=t.float32, device="cuda")
+    xq = t.empty(n, dtype=t.int8, device="cuda")
+    xs = t.empty(n // group, dtype=t.float32, device="cuda")
+    abi.call("l2q_rmsnorm_quant", d_x.data_ptr(), d_r.data_ptr(), xout.data_ptr(), d_w.data_ptr(), n, group,
+             xq.data_ptr(), xs.data_ptr(), stream(t))
+    t.cuda.synchronize()
+    np.testing.assert_array_equal(xout.cpu().numpy(), v)
+    np.testing.assert_array_equal(xs.cpu().numpy(), xs_ref)
+    np.testing.assert_array_equal(xq.cpu().numpy(), xq_ref)
+
+
 @pytest.mark.parametrize("group", [32, 64])
 @pytest.mark.parametrize("n", [768, 11008])
 def test_swiglu_quant(gpu_lib, torch_cuda, group, n):
@@ -201,6 +229,32 @@ def test_swiglu_quant(gpu_lib, torch_cuda, group, n):
     np.testing.assert_array_equal(gout.cpu().numpy(), g_ref)
     np.testing.assert_array_equal(xq.cpu().numpy(), xq_ref)
     np.testing.assert_array_equal(xs.cpu().numpy(), xs_ref)
+
+
+@pytest.mark.parametrize("scale", [1e-30, 1e-3, 30.0, 1e4, 1e15])
+def test_swiglu_quant_extreme_magnitudes(gpu_lib, torch_cuda, scale):
+    """SwiGLU over gate values where expf underflows, saturates or overflows
+    (silu -> 0 or h), tiny and huge up-projections, group maxima over several
+    decades: bit for bit against the reference."""
+    n, group = 11008, 64
+    rng = np.random.default_rng(23)
+    spread = (10.0 ** rng.uniform(-5, 0, n // group)).astype(np.float32)
+    h = (host.gauss(n, 10, 1, 1.0) * np.float32(scale)).astype(np.float32)
+    h2 = (host.gauss(n, 10, 2, 1.0) * np.float32(scale) * np.repeat(spread, group)).astype(np.float32)
+    with np.errstate(over="ignore", invalid="ignore"):
+        g_ref = O.swiglu(h, h2)
+    xq_ref, xs_ref, _ = O.quantize_act(g_ref, group)
+    t = torch_cuda
+    d_h, d_h2 = dev(t, h), dev(t, h2)
+    gout = t.empty(n, dtype=t.float32, device="cuda")
+    xq = t.empty(n, dtype=t.int8, device="cuda")
+    xs = t.empty(n // group, dtype=t.float32, device="cuda")
+    abi.call("l2q_swiglu_quant", d_h.data_ptr(), d_h2.data_ptr(), n, group, xq.data_ptr(), xs.data_ptr(),
+             gout.data_ptr(), stream(t))
+    t.cuda.synchronize()
+    np.testing.assert_array_equal(gout.cpu().numpy(), g_ref)
+    np.testing.assert_array_equal(xs.cpu().numpy(), xs_ref)
+    np.testing.assert_array_equal(xq.cpu().numpy(), xq_ref)
 
 
 def attention_case(t, n_heads, n_kv, hs, max_t, pos, seed, entry="l2q_attention"):
