@@ -127,6 +127,37 @@ def test_int4_g64_7b_layers_debug(gpu_lib):
     eng.close()
 
 
+@pytest.mark.parametrize("shape", ["7b", "15m"])
+def test_denormal_activation_scales_layers_debug(gpu_lib, shape):
+    """A random-init model whose fp32 embedding table is scaled by 1e-42: the
+    residual stream starts denormal, the RMSNorm sum of squares underflows,
+    and the fused GEMV prologues quantize groups whose scale amax/127 is
+    denormal (the clamp to +-127 binds there) against weights of normal size,
+    so a wrong int8 activation changes every later value.  Every layer's
+    residual stream and the logits must equal the reference's."""
+    if shape == "7b":
+        cfg = host.config_7b(seq_len=64)
+        cfg.n_layers = 2
+        group = 64
+    else:
+        cfg = host.config_15m()
+        group = 32
+    ck = host.synth_checkpoint(cfg, 4, group, seed=8, q4_divisor=7.0)
+    off = ck.layout().emb
+    emb = ck.weights[off:off + cfg.vocab_size * cfg.dim * 4].view(np.float32)
+    emb *= np.float32(1e-42)
+    eng = Engine(ck, max_steps=8)
+    orc = O.Oracle(ck.cfg.as_list(), ck.weights, 4, group, max_t=8)
+    token = 23
+    for pos in range(4):
+        xl_g, lg_g = eng.forward_debug(token, pos)
+        xl_o, lg_o = orc.forward(token, pos, layers=True)
+        np.testing.assert_array_equal(xl_g, xl_o)
+        np.testing.assert_array_equal(lg_g, lg_o)
+        token = int(np.argmax(lg_o))
+    eng.close()
+
+
 @pytest.mark.parametrize("bits", [8, 4])
 def test_hs64_g32_gqa_logits(gpu_lib, bits):
     """Heads of 64 with groups of 32 and grouped-query attention (4 heads over
