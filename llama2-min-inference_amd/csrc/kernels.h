@@ -995,6 +995,10 @@ constexpr int kArgmaxThreads = 1024;
 __global__ __launch_bounds__(kArgmaxThreads) void k_argmax(const float* __restrict__ v, int n, int* __restrict__ out) {
     __shared__ float bv[kArgmaxThreads / L2Q_WAVE];
     __shared__ int bi[kArgmaxThreads / L2Q_WAVE];
+    // the reference starts from v[0] and takes v[i] > max: NaNs are never
+    // taken, and a NaN at index 0 makes the answer 0 (every comparison with
+    // it is false); v[0] is read with the first loads, not at the end
+    const float v0 = v[0];
     float best = -INFINITY;
     int idx = n;   // sentinel larger than every index
     const int n4 = n / 4;
@@ -1035,7 +1039,7 @@ __global__ __launch_bounds__(kArgmaxThreads) void k_argmax(const float* __restri
         int ix = bi[0];
         for (int k = 1; k < (int)(blockDim.x / L2Q_WAVE); k++)
             if (bv[k] > b || (bv[k] == b && bi[k] < ix)) { b = bv[k]; ix = bi[k]; }
-        out[0] = ix < n ? ix : 0;
+        out[0] = ix < n && !isnan(v0) ? ix : 0;
     }
 }
 

@@ -62,6 +62,12 @@ def olib():
     return _olib
 
 
+def argmax(v: np.ndarray) -> int:
+    """runq.c:578-585 greedy argmax: the scan from v[0] taking v[i] > max."""
+    v = np.ascontiguousarray(v, dtype=np.float32)
+    return int(olib().orc_argmax(_p(v), v.size))
+
+
 def quantize_act(x: np.ndarray, group: int):
     x = np.ascontiguousarray(x, dtype=np.float32)
     n = x.size
@@ -281,6 +287,11 @@ class RefRunq:
 
     def close(self):
         rlib().ref_close()
+
+
+def ref_argmax(v: np.ndarray) -> int:
+    v = np.ascontiguousarray(v, dtype=np.float32).copy()
+    return int(rlib().ref_sample_argmax(_p(v), v.size))
 
 
 def ref_quantize_act(x: np.ndarray):

@@ -375,11 +375,22 @@ def test_argmax_first_index(gpu_lib, torch_cuda, n):
     v = rng.standard_normal(n).astype(np.float32)
     v[-1] = 7.0                                    # in the tail when n % 4
     cases.append(v)
+    # NaN and -inf, where the reference's scan (start from v[0], take
+    # v[i] > max) differs from numpy's argmax: NaNs are skipped, a NaN at
+    # index 0 answers 0, an all -inf vector answers 0
+    v = rng.standard_normal(n).astype(np.float32)
+    v[rng.integers(0, n, size=min(n, 5))] = np.nan
+    cases.append(v)
+    v = rng.standard_normal(n).astype(np.float32)
+    v[0] = np.nan
+    cases.append(v)
+    cases.append(np.full(n, -np.inf, np.float32))
+    cases.append(np.full(n, np.nan, np.float32))
     for v in cases:
         d_v = dev(t, v)
         abi.call("l2q_argmax", d_v.data_ptr(), n, out.data_ptr(), stream(t))
         t.cuda.synchronize()
-        assert int(out.item()) == int(np.argmax(v)), (n, v[:8])
+        assert int(out.item()) == O.argmax(v), (n, v[:8])
 
 
 def test_unbias(gpu_lib, torch_cuda):

@@ -29,6 +29,24 @@ def test_quantize_act_bit_exact():
             np.testing.assert_array_equal(g, r)
 
 
+def test_argmax_equals_reference_scan():
+    """orc_argmax against runq.c's sample_argmax, including the cases where
+    the scan from v[0] differs from numpy's argmax (NaNs skipped, a NaN at
+    index 0, all -inf, ties)."""
+    rng = np.random.default_rng(4)
+    cases = []
+    for n in (1, 5, 32000):
+        v = rng.standard_normal(n).astype(np.float32)
+        cases.append(v)
+        w = v.copy(); w[rng.integers(0, n, size=min(n, 4))] = np.float32(9.0); cases.append(w)
+        w = v.copy(); w[rng.integers(0, n, size=min(n, 4))] = np.nan; cases.append(w)
+        w = v.copy(); w[0] = np.nan; cases.append(w)
+        cases.append(np.full(n, -np.inf, np.float32))
+        cases.append(np.full(n, np.nan, np.float32))
+    for v in cases:
+        assert O.argmax(v) == O.ref_argmax(v), v[:6]
+
+
 @pytest.mark.parametrize("rows,cols", [(64, 288), (96, 768), (17, 4096)])
 def test_matmul_q8_bit_exact(rows, cols):
     w = host.gauss(rows * cols, rows, 2, 0.02).reshape(rows, cols)
