@@ -342,6 +342,33 @@ def test_attention_forms_and_k_layouts(gpu_lib, torch_cuda, n_heads, n_kv, hs, m
             np.testing.assert_array_equal(out.cpu().numpy(), ref, err_msg=f"layout {layout} form {form}")
 
 
+@pytest.mark.parametrize("scale", [1e-30, 1e-6, 30.0, 1e6, 1e15])
+@pytest.mark.parametrize("ctx", [65, 700])
+def test_attention_forms_extreme_magnitudes(gpu_lib, torch_cuda, scale, ctx):
+    """Scores from ~0 (a uniform softmax, values that underflow in the
+    products) to ~1e30 (a softmax that collapses onto one position, exp
+    underflowing to 0 for the rest), in every form and K layout: the
+    oracle's bits."""
+    t = torch_cuda
+    n_heads = n_kv = 8
+    hs, max_t = 128, 1024
+    pos = ctx - 1
+    kc = (host.gauss(n_kv * max_t * hs, ctx, 1, 1.0) * np.float32(scale)).astype(np.float32).reshape(n_kv, max_t, hs)
+    vc = host.gauss(n_kv * max_t * hs, ctx, 2, 1.0).reshape(n_kv, max_t, hs)
+    q = (host.gauss(n_heads * hs, ctx, 3, 1.0) * np.float32(scale)).astype(np.float32)
+    ref = O.attention(q, kc, vc, pos, n_heads, n_kv, hs)
+    kil = np.ascontiguousarray(kc.reshape(n_kv, max_t, hs // 4, 4).transpose(0, 2, 1, 3))
+    d_q, d_v = dev(t, q), dev(t, vc)
+    out = t.empty(n_heads * hs, dtype=t.float32, device="cuda")
+    for layout, kd in ((0, dev(t, kc)), (abi.L2Q_ATTN_K_INTERLEAVED, dev(t, kil))):
+        for form in (abi.L2Q_ATTN_ONE_KERNEL, abi.L2Q_ATTN_TWO_KERNELS):
+            out.fill_(np.nan)
+            abi.call("l2q_attention_ex", d_q.data_ptr(), kd.data_ptr(), d_v.data_ptr(), out.data_ptr(), pos, n_heads,
+                     n_kv, hs, max_t, layout | form, stream(t))
+            t.cuda.synchronize()
+            np.testing.assert_array_equal(out.cpu().numpy(), ref, err_msg=f"layout {layout} form {form}")
+
+
 def test_expf_identical_to_host_on_every_input(gpu_lib, torch_cuda):
     """The device exp used by softmax and SwiGLU equals the host C library's
     expf on all 2^32 float bit patterns (NaNs compared as NaN)."""
