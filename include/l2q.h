@@ -279,7 +279,9 @@ int l2q_attention_kv8(const float* q, const int8_t* kcache8, const int8_t* vcach
 
 /* Greedy argmax on the device: out[0] = the first index of the maximum of
  * v[0..n), v 16-byte aligned (sample_argmax, runq.c:578-585; the engine's
- * l2q_engine_forward_argmax runs it inside its step). */
+ * l2q_engine_forward_argmax runs it inside its step).  As the reference's
+ * scan from v[0]: NaNs are never taken, a NaN at index 0 gives 0, and so
+ * does a vector of -inf. */
 int l2q_argmax(const float* v, int n, int* out, void* stream);
 
 /* expf exactly as the host C library computes it (the exp used by the
