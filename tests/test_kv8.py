@@ -135,6 +135,41 @@ def test_gpu_kv8_append_bit_exact(gpu_lib, torch_cuda, n_kv, hs):
 
 
 @pytest.mark.gpu
+@pytest.mark.parametrize("scale", [1e-44, 1e-40, 1e-37, 1e30])
+def test_gpu_kv8_append_extreme_magnitudes(gpu_lib, torch_cuda, scale):
+    """k and v rows from denormal (scales amax/127 of a few bits, where the
+    clamp to +-127 binds) to 1e30, RoPE applied to k: bit for bit."""
+    t = torch_cuda
+    n_kv, hs, max_t = 4, 128, 16
+    rope = np.empty(max_t * hs, dtype=np.float32)
+    abi.lib().l2q_rope_table(rope.ctypes.data, max_t, hs)
+    d_rope = dev(t, rope)
+    k8 = t.zeros(n_kv * max_t * hs, dtype=t.int8, device="cuda")
+    v8 = t.zeros_like(k8)
+    ks = t.zeros(n_kv * max_t, dtype=t.float32, device="cuda")
+    vs = t.zeros_like(ks)
+    for pos in (0, 5):
+        k = (host.gauss(n_kv * hs, pos, 6, 1.0) * np.float32(scale)).astype(np.float32)
+        v = (host.gauss(n_kv * hs, pos, 7, 1.0) * np.float32(scale)).astype(np.float32)
+        d_k, d_v = dev(t, k), dev(t, v)
+        abi.call("l2q_kv8_append", d_k.data_ptr(), d_v.data_ptr(), k8.data_ptr(), v8.data_ptr(), ks.data_ptr(),
+                 vs.data_ptr(), d_rope.data_ptr(), pos, n_kv, hs, max_t, stream(t))
+        t.cuda.synchronize()
+        _, kr = O.rope(np.zeros(n_kv * hs, np.float32), k, pos, hs)
+        g8 = k8.cpu().numpy().reshape(n_kv, max_t, hs)
+        h8 = v8.cpu().numpy().reshape(n_kv, max_t, hs)
+        gks = ks.cpu().numpy().reshape(n_kv, max_t)
+        gvs = vs.cpu().numpy().reshape(n_kv, max_t)
+        for g in range(n_kv):
+            eq, es = O.kv_quant(kr[g * hs:(g + 1) * hs])
+            np.testing.assert_array_equal(g8[g, pos], eq)
+            assert gks[g, pos] == es
+            eq, es = O.kv_quant(v[g * hs:(g + 1) * hs])
+            np.testing.assert_array_equal(h8[g, pos], eq)
+            assert gvs[g, pos] == es
+
+
+@pytest.mark.gpu
 @pytest.mark.parametrize("n_heads,n_kv,hs,max_t,ctx", [(32, 32, 128, 4096, 1), (32, 32, 128, 4096, 64),
                                                       (32, 32, 128, 4096, 256), (32, 32, 128, 4096, 1024),
                                                       (32, 32, 128, 4096, 4096), (6, 6, 48, 256, 200),
