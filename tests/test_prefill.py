@@ -115,3 +115,22 @@ def test_engine_prefill_rejects_bad_positions(gpu_lib, c1_q8):
     bad = np.array([5, 40000], dtype=np.int32)
     assert abi.lib().l2q_engine_prefill(eng._h, bad.ctypes.data, 2, 0, None) == abi.L2Q_ERR_ARG
     eng.close()
+
+
+@pytest.mark.parametrize("shape", ["15m", "7b"])
+def test_engine_prefill_denormal_embedding(gpu_lib, shape):
+    """The embedding table scaled by 1e-42: the batched prefill's RMSNorm,
+    SwiGLU and quantize kernels meet denormal residual streams and group
+    scales where the reference's clamp to +-127 binds; the last prompt
+    position's logits and the decode after it equal the reference's."""
+    if shape == "7b":
+        cfg = host.make_config(4096, 11008, 2, 32, 32, 32000, 4096)
+        ck = host.synth_checkpoint(cfg, 4, 64, seed=29, q4_divisor=7.0)
+    else:
+        cfg = host.config_15m()
+        ck = host.synth_checkpoint(cfg, 4, 32, seed=31, q4_divisor=8.0)
+    off = ck.layout().emb
+    emb = ck.weights[off:off + cfg.vocab_size * cfg.dim * 4].view(np.float32)
+    emb *= np.float32(1e-42)
+    prompt = [int(v) for v in host.uniform_ints(24, 8, 100, 3, 32000)]
+    prefill_then_greedy(ck, prompt, 4, 64)
