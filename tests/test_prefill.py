@@ -134,3 +134,15 @@ def test_engine_prefill_denormal_embedding(gpu_lib, shape):
     emb *= np.float32(1e-42)
     prompt = [int(v) for v in host.uniform_ints(24, 8, 100, 3, 32000)]
     prefill_then_greedy(ck, prompt, 4, 64)
+
+
+@pytest.mark.parametrize("bits", [8, 4])
+def test_engine_prefill_gqa_hs64(gpu_lib, bits):
+    """Batched prefill of a grouped-query model (4 heads over 2 kv heads,
+    heads of 64, groups of 32), in two calls: logits and the decode after it
+    equal the reference's."""
+    cfg = host.make_config(256, 512, 2, 4, 2, 512, 64)
+    kw = {"q4_divisor": 7.0} if bits == 4 else {}
+    ck = host.synth_checkpoint(cfg, bits, 32, seed=15 + bits, **kw)
+    prompt = [int(v) for v in host.uniform_ints(30, 9, 100, 3, 512)]
+    prefill_then_greedy(ck, prompt, 6, 64, split=11)
