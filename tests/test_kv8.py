@@ -204,7 +204,7 @@ def test_gpu_attention_kv8_rejects_bad_shapes(gpu_lib, torch_cuda):
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize("shape", ["c1_q8_g32", "7b2_q4_g64"])
+@pytest.mark.parametrize("shape", ["c1_q8_g32", "7b2_q4_g64", "gqa_hs64_q4_g32"])
 def test_gpu_engine_kv8_follows_oracle(gpu_lib, torch_cuda, shape):
     """Engine with the int8 KV cache against the oracle's int8-KV forward
     (attention in the kernels' float order): logits bit for bit at every
@@ -213,6 +213,10 @@ def test_gpu_engine_kv8_follows_oracle(gpu_lib, torch_cuda, shape):
     if shape == "c1_q8_g32":
         ck = host.synth_checkpoint(host.config_15m(), 8, 32, seed=21)
         steps = 64
+    elif shape == "gqa_hs64_q4_g32":   # 4 heads over 2 kv heads: the group's first head appends
+        cfg = host.make_config(256, 512, 2, 4, 2, 512, 64)
+        ck = host.synth_checkpoint(cfg, 4, 32, seed=24, q4_divisor=7.0)
+        steps = 40
     else:
         cfg = host.make_config(4096, 11008, 2, 32, 32, 32000, 4096)
         ck = host.synth_checkpoint(cfg, 4, 64, seed=22, q4_divisor=7.0)
