@@ -158,6 +158,24 @@ def test_denormal_activation_scales_layers_debug(gpu_lib, shape):
     eng.close()
 
 
+def test_decode_two_kernel_attention_hs32_gqa(gpu_lib):
+    """Heads of 32 (a size the one-kernel attention does not take), 8 heads
+    over 4 kv heads: the engine's step graph runs the two-kernel exact
+    attention at every position; logits equal the reference's for 300
+    positions."""
+    cfg = host.make_config(256, 512, 2, 8, 4, 512, 300)
+    ck = host.synth_checkpoint(cfg, 8, 32, seed=41)
+    eng = Engine(ck, max_steps=300)
+    orc = O.Oracle(ck.cfg.as_list(), ck.weights, 8, 32, max_t=300)
+    token = 7
+    for pos in range(300):
+        lg, lo = eng.forward(token, pos), orc.forward(token, pos)
+        np.testing.assert_array_equal(lg, lo, err_msg=f"pos {pos}")
+        token = int(np.argmax(lo))
+    eng.close()
+    orc.close()
+
+
 @pytest.mark.parametrize("bits", [8, 4])
 def test_hs64_g32_gqa_logits(gpu_lib, bits):
     """Heads of 64 with groups of 32 and grouped-query attention (4 heads over
