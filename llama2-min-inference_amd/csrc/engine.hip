@@ -524,10 +524,14 @@ int l2q_engine_create_ex(const l2q_config* cfg, const void* weights, size_t weig
     const int hs = c.dim / c.n_heads;
     const int kv_dim = hs * c.n_kv_heads;
     if (!gemv_shape_ok(wbits, group, 1, c.dim) || !gemv_shape_ok(wbits, group, 1, c.hidden_dim) ||
-        !attention_shape_ok(c.n_heads, c.n_kv_heads, hs) || hs % 2 || c.dim > kNormThreads * kNormMaxPer ||
-        !attention_exact_ok(max_steps <= 0 || max_steps > c.seq_len ? c.seq_len : max_steps)) {
+        !attention_shape_ok(c.n_heads, c.n_kv_heads, hs) || hs % 2 || c.dim > kNormThreads * kNormMaxPer) {
         set_error("engine: unsupported shape (dim %d hidden %d heads %d group %d bits %d)", c.dim, c.hidden_dim,
                   c.n_heads, group, wbits);
+        return L2Q_ERR_ARG;
+    }
+    if (!attention_exact_ok(max_steps <= 0 || max_steps > c.seq_len ? c.seq_len : max_steps)) {
+        set_error("engine: too many cached positions (max_steps %d, seq_len %d; the exact attention holds at most %d)",
+                  max_steps, c.seq_len, attention_exact_max());
         return L2Q_ERR_ARG;
     }
     const int steps = max_steps <= 0 || max_steps > c.seq_len ? c.seq_len : max_steps;

@@ -54,6 +54,7 @@ int launch_attention_exact(const float* q, const float* kcache, const float* vca
                            int S, const int* meta, int pos, int n_heads, int n_kv_heads, int hs, int max_t,
                            hipStream_t st, int T = 1, int q_stride = 0, int fused = -1, int k_il = 0);
 bool attention_exact_ok(int max_t);
+int attention_exact_max();   // the longest cache attention_exact_ok accepts
 bool attention_fused_ok(int hs);
 // Longest context served by the one-kernel form: every context the exact
 // path takes (measured faster than the pair at 64..4096 positions with the

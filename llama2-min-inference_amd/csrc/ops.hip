@@ -278,6 +278,8 @@ int attention_fused_max() {
     return v;
 }
 
+int attention_exact_max() { return kScorePer * kAttnThreads; }
+
 bool attention_exact_ok(int max_t) {
     return max_t <= kScorePer * kAttnThreads && attn_v_lds_bytes(max_t) <= 65536;
 }

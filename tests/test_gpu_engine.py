@@ -158,6 +158,16 @@ def test_denormal_activation_scales_layers_debug(gpu_lib, shape):
     eng.close()
 
 
+def test_engine_rejects_more_positions_than_the_exact_attention_holds(gpu_lib):
+    from llama2q.abi import L2QError
+    cfg = host.config_15m()
+    cfg.seq_len = 5000
+    ck = host.synth_checkpoint(cfg, 8, 32, seed=2)
+    with pytest.raises(L2QError, match="too many cached positions"):
+        Engine(ck, max_steps=5000)
+    Engine(ck, max_steps=4096).close()
+
+
 def test_decode_two_kernel_attention_hs32_gqa(gpu_lib):
     """Heads of 32 (a size the one-kernel attention does not take), 8 heads
     over 4 kv heads: the engine's step graph runs the two-kernel exact
