@@ -91,7 +91,8 @@ typedef struct l2q_engine l2q_engine;
  *
  * `max_steps` sizes the KV cache (positions 0..max_steps-1), as the GPU
  * reference runners do (v5-cuda-fused/run.cu:1147-1150); it is clamped to
- * cfg->seq_len.  Replaces read_checkpoint/memory_map_weights/
+ * cfg->seq_len, and a cache of more than 4096 positions (the exact-order
+ * attention's limit; Llama-2's seq_len is 4096) is L2Q_ERR_ARG.  Replaces read_checkpoint/memory_map_weights/
  * malloc_run_state (runq.c:190-283) and load_weights/alloc_state/build_graph
  * (v5-cuda-fused/run.cu:534-582, 671-679). */
 int l2q_engine_create(const l2q_config* cfg, const void* weights,
