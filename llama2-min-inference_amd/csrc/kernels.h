@@ -698,6 +698,7 @@ __global__ __launch_bounds__(kAfThreads) void k_attn_fused(
             m = fmaxf(m, s[r]);
         }
     }
+    store_chunk(0);   // the first V chunk (arrived with K) written while the waves meet
     m = group_max<L2Q_WAVE>(m);
     if (lane == 0) red[wv] = m;
     __syncthreads();
@@ -714,7 +715,6 @@ __global__ __launch_bounds__(kAfThreads) void k_attn_fused(
             p[t] = e[r];
         }
     }
-    store_chunk(0);
     __syncthreads();
     if (tid == 0) red[8] = serial_sum(p, n);
     __syncthreads();
