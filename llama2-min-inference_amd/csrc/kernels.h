@@ -622,8 +622,10 @@ __global__ __launch_bounds__(kAfThreads) void k_attn_fused(
     const float* vbase = vcache + (size_t)(h / kv_mul) * max_t * HS + d0;
     const int nchunks = (n + kAfChunk - 1) / kAfChunk;
 
-    // loads in the order they are needed (they complete in order): q, the
-    // first round's K rows, the first V chunk.  The q load and its LDS store
+    // loads in the order they are needed (they complete in order): q and
+    // the first round's K rows here, the first V chunk after the scores
+    // (they share one HBM-bound stream, and V is not needed before the
+    // softmax sum, so K arrives sooner).  The q load and its LDS store
     // are unconditional (clamped index; duplicates store equal values): a
     // load or store under a thread condition can be sunk behind the later
     // loads, and waiting for it then waits for them.  In the first round
@@ -664,7 +666,6 @@ __global__ __launch_bounds__(kAfThreads) void k_attn_fused(
             dst[(4 * c4 + 3) * kAfStride + r] = vr[k].w;
         }
     };
-    load_chunk(0, true);
     // the exp table through the scalar cache (uniform loads: no vector
     // memory traffic, no 512 lanes per workgroup on one table)
     uint64_t tabv = 0;
@@ -698,7 +699,7 @@ __global__ __launch_bounds__(kAfThreads) void k_attn_fused(
             m = fmaxf(m, s[r]);
         }
     }
-    store_chunk(0);   // the first V chunk (arrived with K) written while the waves meet
+    load_chunk(0, true);   // V after K: the scores need only K
     m = group_max<L2Q_WAVE>(m);
     if (lane == 0) red[wv] = m;
     __syncthreads();
@@ -724,6 +725,7 @@ __global__ __launch_bounds__(kAfThreads) void k_attn_fused(
         const int t = kAfThreads * r + tid;
         if (kAfThreads * r < n && t < n) p[t] = e[r] / sum;
     }
+    store_chunk(0);
     __syncthreads();
 
     float acc = 0.0f;
