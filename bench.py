@@ -12,14 +12,31 @@ hipGraph with the argmax on the device (the decode loop of runq.c:681-718).
 A "step" is one decode position; value = K / timed seconds (tok/s).
 
 Also reported on the same JSON line:
-  roofline      the dominant kernel (the INT4 GEMV at the largest per-layer
-                shape, 22016 x 4096 = w1|w3) timed live with HIP events over
-                rotating weight sets (>= 1 GiB, so the 256 MB MALL cannot
-                serve them): algorithmic bytes per launch / mean duration,
-                against the 8 TB/s HBM3E peak;
+  roofline      the decode's dominant kernel, the w1|w3 GEMV of the step
+                (22016 x 4096, RMSNorm + Q8 prologue, SwiGLU epilogue),
+                launched by the engine with the decode's own arguments over
+                the 32 layers' weights (1.6 GB, so the 256 MB MALL cannot
+                serve them) and timed live with HIP events on the engine's
+                stream: algorithmic bytes per launch / mean duration, against
+                the 8 TB/s HBM3E peak;
+  decode_gemv   the same for all five GEMV kinds of the step, and the
+                aggregate GEMV fraction of peak over one step;
+  runq_tok_s    the reference's own tok/s formula, (positions - 1) /
+                elapsed (runq.c:710-716), over the whole generation
+                (prefill + warmup + timed steps);
+  gemv_c2_int8, gemv_c3_int4
+                BASELINE configs 2 and 3: the four Llama-2-7B GEMV shapes,
+                pre-quantized activations, rotating >= 1 GiB weight sets;
   cpu_baseline  the reference's CPU runner (v1-int8-vnni/runq.c, AVX-512
                 VNNI, OpenMP), compiled from its own source, decoding the
-                7B shape at its native INT8 group 32 on this host's cores.
+                7B shape at its native INT8 group 32 on this host's cores;
+  cpu_reference the host CPU (model, AVX-512 VNNI), matmul_q8 GB/s on the
+                config-2 shapes (group 32: the reference's own code; group
+                64: the C port, as runq fixes QBLOCK = 32) and the config-1
+                model's end-to-end tok/s through the compiled reference.
+
+--decode-only runs the decode alone (no microbenchmarks, no CPU legs): the
+form the committed rocprofv3 kernel statistics are taken from.
 """
 import argparse
 import ctypes as C
@@ -172,6 +189,85 @@ def time_gemm(torch, abi, rows, cols, T, bits=4, group=64, reps=20):
     return e0.elapsed_time(e1) / reps
 
 
+C2_SHAPES = [(4096, 4096), (11008, 4096), (4096, 11008), (32000, 4096)]
+
+
+def cpu_info():
+    """Model name and the AVX-512 VNNI flag of this host (Linux)."""
+    model, flags = None, set()
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if model is None and line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                elif not flags and line.startswith("flags"):
+                    flags = set(line.split(":", 1)[1].split())
+    except OSError:
+        pass
+    return {"model": model, "avx512_vnni": "avx512_vnni" in flags, "avx512f": "avx512f" in flags,
+            "nproc": os.cpu_count(), "omp_threads": int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))}
+
+
+def cpu_matmul(reps=7):
+    """matmul_q8 (runq.c:142-159) on the config-2 shapes, median of `reps`
+    calls, in GB/s of the config-2 algorithmic bytes: group 32 through the
+    reference's own function (compiled runq.c), group 64 through the C port
+    (oracle.c orc_matmul_q8), since runq fixes its group at QBLOCK = 32."""
+    sys.path.insert(0, os.path.join(REPO, "oracle"))
+    import oracle_py as O
+    rng = np.random.default_rng(5)
+    out = {}
+    for rows, cols in C2_SHAPES:
+        w = rng.integers(0, 256, rows * cols, dtype=np.uint8)
+        x = rng.standard_normal(cols).astype(np.float32)
+        res = {}
+        for group, kind in ((32, "reference"), (64, "port")):
+            ws = rng.random(rows * (cols // group), dtype=np.float32) * np.float32(1e-3)
+            xq, xs, xt = O.quantize_act(x, group)
+            if kind == "reference":
+                if not O.ref_available():
+                    continue
+                fn = lambda: O.ref_matmul_q8(xq, xs, xt, w, ws, rows, cols)  # noqa: E731
+            else:
+                fn = lambda: O.matmul(8, xq, xs, xt, w, ws, rows, cols, group, want_dots=False)  # noqa: E731
+            fn()
+            fn()
+            ts = []
+            for _ in range(reps):
+                t = time.perf_counter()
+                fn()
+                ts.append(time.perf_counter() - t)
+            t = float(np.median(ts))
+            b = gemv_bytes(rows, cols, 8, group)
+            res[f"G{group}"] = {"kind": kind, "ms": round(t * 1e3, 3), "GB/s": round(b / t / 1e9, 1)}
+        out[f"{rows}x{cols}"] = res
+    return out
+
+
+def cpu_c1():
+    """BASELINE config 1 on the compiled reference runq.c: the stories15M-shaped
+    INT8 group-32 model, 16 prompt ids then 240 greedy steps, tok/s by the
+    reference's formula ((pos - 1) / elapsed from the end of step 1)."""
+    sys.path.insert(0, os.path.join(REPO, "oracle"))
+    import oracle_py as O
+    from llama2q import host
+    if not O.ref_available():
+        return None
+    ck = host.synth_checkpoint(host.config_15m(), 8, 32, seed=1234)
+    prompt = [int(v) for v in host.uniform_ints(16, 1234, 100, 3, 32000)]
+    ref = O.RefRunq(image=ck.data)
+    token = prompt[0]
+    t0 = 0.0
+    for pos in range(256):
+        lg = ref.forward(token, pos)
+        token = prompt[pos + 1] if pos < len(prompt) - 1 else O.ref_argmax(lg)
+        if pos == 0:
+            t0 = time.perf_counter()
+    el = time.perf_counter() - t0
+    ref.close()
+    return {"tok_s": round(255 / el, 1), "positions": 256, "kind": "reference"}
+
+
 def cpu_baseline(seconds_budget=20.0):
     """The reference runq.c (AVX-512 VNNI + OpenMP) on this host: 7B-shaped
     INT8 group-32 decode (its own format; the reference has no CPU INT4
@@ -215,6 +311,8 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
     ap.add_argument("--kv8-steps", type=int, default=64,
                     help="greedy steps timed again with the int8 KV cache engine (0: skip)")
+    ap.add_argument("--decode-only", action="store_true",
+                    help="the decode alone: no microbenchmarks, no int8-KV decode, no CPU legs")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="first run a 256 MiB device copy (x4): a kernel of known traffic for scaling "
                          "rocprofv3 FETCH_SIZE / WRITE_SIZE readings")
@@ -246,7 +344,7 @@ def main():
 
     # the same decode with the int8 KV cache (a secondary figure)
     kv8 = None
-    if args.kv8_steps > 0:
+    if args.kv8_steps > 0 and not args.decode_only:
         e8 = Engine(ck, max_steps=args.prompt + args.warmup + args.kv8_steps, kv8=True)
         e8.prefill(prompt[:-1], 0, logits=False)
         tok8, p8 = prompt[-1], args.prompt - 1
@@ -287,52 +385,93 @@ def main():
         pos += 1
     torch.cuda.synchronize()
     elapsed = time.perf_counter() - t0
+    gen_end = time.perf_counter()
+    # the reference's tok/s formula over the whole generation: positions run
+    # minus one over the time from the first forward (the prefill) on
+    n_pos = pos
+    runq_tok_s = (n_pos - 1) / (gen_end - tp)
     # the same positions replayed back to back without per-token host sync
     dev_ms = eng.time_steps([prompt[i % len(prompt)] for i in range(args.steps)], pos_start)
+
+    # the step's GEMV kernels, launched by the engine with the decode's own
+    # arguments, rotating over the layers' weights (HIP events)
+    d, h, L = cfg.dim, cfg.hidden_dim, cfg.n_layers
+    kv = d * cfg.n_kv_heads // cfg.n_heads
+    kinds = [("qkv", abi.L2Q_GEMV_QKV, d + 2 * kv, d, L), ("wo", abi.L2Q_GEMV_WO, d, d, L),
+             ("w13", abi.L2Q_GEMV_W13, 2 * h, d, L), ("w2", abi.L2Q_GEMV_W2, d, h, L),
+             ("wcls", abi.L2Q_GEMV_CLASSIFIER, cfg.vocab_size, d, 1)]
+    decode_gemv = None
+    if not args.decode_only:
+        decode_gemv = {}
+        tot_b = tot_us = 0.0
+        for name, kind, r, c, per_step in kinds:
+            n = 4 * L if per_step > 1 else 32
+            us = eng.time_gemv(kind, n) * 1e3 / n
+            b = gemv_bytes(r, c, 4, group)
+            decode_gemv[name] = {"rows": r, "cols": c, "us": round(us, 3), "bytes": b,
+                                 "GB/s": round(b / us / 1e3, 1), "frac": round(b / us / 1e3 / HBM_PEAK_GBS, 4),
+                                 "per_step": per_step, "launches": n}
+            tot_b += per_step * b
+            tot_us += per_step * us
+        decode_gemv["aggregate"] = {"bytes_per_step": int(tot_b), "us_per_step": round(tot_us, 1),
+                                    "GB/s": round(tot_b / tot_us / 1e3, 1),
+                                    "frac": round(tot_b / tot_us / 1e3 / HBM_PEAK_GBS, 4)}
     eng.close()
 
     ms_per_step = elapsed * 1e3 / args.steps
     tok_s = args.steps / elapsed
     avg_bytes = np.mean([step_bytes(cfg, group, p) for p in range(pos_start, pos_start + args.steps)])
 
-    # roofline of the dominant kernel + the other GEMV shapes of the step
-    shapes = {"w13": (2 * cfg.hidden_dim, cfg.dim), "qkv": (3 * cfg.dim, cfg.dim), "wo": (cfg.dim, cfg.dim),
-              "w2": (cfg.dim, cfg.hidden_dim), "wcls": (cfg.vocab_size, cfg.dim)}
-    gemv = {}
-    for k, (r, c) in shapes.items():
-        ms, n = time_gemv(torch, abi, r, c, 4, group)
-        b = gemv_bytes(r, c, 4, group)
-        gemv[k] = {"rows": r, "cols": c, "us": round(ms * 1e3, 3), "GB/s": round(b / ms / 1e6, 1),
-                   "frac": round(b / ms / 1e6 / HBM_PEAK_GBS, 4), "launches": n}
-    dom = gemv["w13"]
-    dom_bytes = gemv_bytes(*shapes["w13"], 4, group)
+    # BASELINE configs 2 and 3: the four 7B shapes, pre-quantized activations
+    gemv_c2 = gemv_c3 = attention = gemm_t = None
+    if not args.decode_only:
+        gemv_c2, gemv_c3 = {}, {}
+        for bits, dst in ((8, gemv_c2), (4, gemv_c3)):
+            for r, c in C2_SHAPES:
+                ms, n = time_gemv(torch, abi, r, c, bits, group)
+                b = gemv_bytes(r, c, bits, group)
+                dst[f"{r}x{c}"] = {"us": round(ms * 1e3, 3), "bytes": b, "GB/s": round(b / ms / 1e6, 1),
+                                   "frac": round(b / ms / 1e6 / HBM_PEAK_GBS, 4), "launches": n}
 
-    # one layer's attention at the BASELINE config-4 contexts: fp32 cache in
-    # the exact order and split over the context, int8 cache
-    attention = {}
-    for ctx in (256, 1024, 2048, 4096):
-        for name in ("exact", "split", "int8"):
-            ms, nbytes = time_attention(torch, abi, host, ctx, name)
-            attention[f"{name}_ctx{ctx}"] = {"us": round(ms * 1e3, 2), "bytes": nbytes,
-                                             "GB/s": round(nbytes / ms / 1e6, 1)}
+        # one layer's attention at the BASELINE config-4 contexts: fp32 cache in
+        # the exact order and split over the context, int8 cache
+        attention = {}
+        for ctx in (256, 1024, 2048, 4096):
+            for name in ("exact", "split", "int8"):
+                ms, nbytes = time_attention(torch, abi, host, ctx, name)
+                attention[f"{name}_ctx{ctx}"] = {"us": round(ms * 1e3, 2), "bytes": nbytes,
+                                                 "GB/s": round(nbytes / ms / 1e6, 1)}
 
-    # the batched prefill GEMM at T = 128 tokens (INT4 g64, 7B shapes);
-    # each launch includes the activation preparation kernel
-    gemm_t = {}
-    for k, (r, c) in shapes.items():
-        ms = time_gemm(torch, abi, r, c, 128)
-        gemm_t[k] = {"us": round(ms * 1e3, 2), "int8_TOPS": round(2 * r * c * 128 / ms / 1e9, 2),
-                     "weight_GB/s": round(gemv_bytes(r, c, 4, group) / ms / 1e6, 1)}
+        # the batched prefill GEMM at T = 128 tokens (INT4 g64, 7B shapes);
+        # each launch includes the activation preparation kernel
+        gemm_t = {}
+        for name, _, r, c, _ in kinds:
+            ms = time_gemm(torch, abi, r, c, 128)
+            gemm_t[name] = {"us": round(ms * 1e3, 2), "int8_TOPS": round(2 * r * c * 128 / ms / 1e9, 2),
+                            "weight_GB/s": round(gemv_bytes(r, c, 4, group) / ms / 1e6, 1)}
 
     traffic = None
-    tpath = os.path.join(REPO, "profiles", "gemv_q4_g64_w13_traffic.txt")
+    tpath = os.path.join(REPO, "profiles", "gemv_q4_g64_w13_decode_traffic.txt")
     if os.path.exists(tpath):
         with open(tpath) as f:
             for line in f:
                 if line.startswith("hbm_bytes_per_launch="):
                     traffic = int(line.split("=", 1)[1])
 
-    cpu = None if args.no_cpu_baseline else cpu_baseline(args.cpu_seconds)
+    cpu = cpu_ref = None
+    if not args.decode_only and not args.no_cpu_baseline:
+        cpu = cpu_baseline(args.cpu_seconds)
+        cpu_ref = {"host": cpu_info(), "matmul_q8": cpu_matmul(), "c1_decode": cpu_c1()}
+
+    dom = decode_gemv["w13"] if decode_gemv else None
+    roofline = None
+    if dom:
+        roofline = {"bound": "hbm", "achieved": dom["GB/s"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                    "frac": dom["frac"], "traffic": traffic,
+                    "kernel": "k_gemv<4,64,2,2,2,2>: the decode's w1|w3 GEMV, 22016 x 4096, RMSNorm + Q8 "
+                              "prologue, SwiGLU epilogue, launched by the engine with the step's arguments "
+                              "over the 32 layers' weights",
+                    "bytes_per_launch": dom["bytes"], "mean_us": dom["us"]}
 
     line = {
         "metric": METRIC,
@@ -351,16 +490,15 @@ def main():
                    "dim": cfg.dim, "layers": cfg.n_layers, "heads": cfg.n_heads, "hidden": cfg.hidden_dim,
                    "vocab": cfg.vocab_size, "group": group, "prompt_tokens": args.prompt,
                    "positions": [pos_start, pos_start + args.steps - 1], "parallelism": "single GPU"},
-        "roofline": {"bound": "hbm", "achieved": dom["GB/s"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": dom["frac"], "traffic": traffic,
-                     "kernel": "k_gemv<4,64,2,0,0,2> (INT4 g64 GEMV, pre-quantized input), "
-                               "22016 x 4096 (w1|w3 of one layer)",
-                     "bytes_per_launch": dom_bytes, "mean_us": dom["us"]},
+        "roofline": roofline,
         "cpu_baseline": cpu,
+        "runq_tok_s": round(runq_tok_s, 2),
+        "decode_gemv": decode_gemv,
         "step_bytes_avg": int(avg_bytes),
         "step_effective_GBs": round(avg_bytes / (ms_per_step * 1e-3) / 1e9, 1),
         "device_replay_ms_per_step": round(dev_ms / args.steps, 4),
-        "gemv": gemv,
+        "gemv_c2_int8": gemv_c2,
+        "gemv_c3_int4": gemv_c3,
         "attention_c4": attention,
         "prefill_gemm_t128": gemm_t,
         "prefill": {"tokens": args.prompt - 1, "ms": round(prefill_s * 1e3, 3),
@@ -368,6 +506,7 @@ def main():
                     "note": "batched prefill of the forced prompt positions (int8 MFMA GEMMs, host-timed, "
                             "includes the per-chunk token upload)"},
         "kv8_decode": kv8,
+        "cpu_reference": cpu_ref,
         "synth_seconds": round(t_synth, 1),
     }
     print(json.dumps(line))

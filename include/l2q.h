@@ -145,6 +145,21 @@ int l2q_engine_forward_debug(l2q_engine* e, int token, int pos,
 int l2q_engine_time_steps(l2q_engine* e, const int* tokens, int pos0,
                           int n_steps, double* elapsed_ms);
 
+/* Benchmark entry: launch the step's GEMV kernel of one matrix kind
+ * `n_launches` times back to back on the engine's stream, with the decode's
+ * own arguments (prologue, epilogue, weights of layer i % n_layers, so the
+ * launches rotate over every layer's weights), and report the elapsed device
+ * time in milliseconds (HIP events).  Inputs are the engine's current
+ * activations; outputs go to a scratch area, so the decode state is left
+ * unchanged.  The reference has no counterpart (its kernels are timed by the
+ * whole step, v5-cuda-fused/run.cu:10-11). */
+#define L2Q_GEMV_QKV        0   /* wq|wk|wv: RMSNorm prologue, RoPE + KV append epilogue */
+#define L2Q_GEMV_WO         1   /* wo: Q8 quantize prologue */
+#define L2Q_GEMV_W13        2   /* w1|w3: RMSNorm prologue, SwiGLU epilogue */
+#define L2Q_GEMV_W2         3   /* w2: Q8 quantize prologue */
+#define L2Q_GEMV_CLASSIFIER 4   /* wcls: final RMSNorm prologue */
+int l2q_engine_time_gemv(l2q_engine* e, int kind, int n_launches, double* elapsed_ms);
+
 /* Device bytes held by the engine (weights + KV cache + activations). */
 size_t l2q_engine_device_bytes(const l2q_engine* e);
 

@@ -68,6 +68,7 @@ struct l2q_engine {
     float *ks, *vs;          //   scales [L][n_kv][max_t]
     float* kvf;              //   the position's rotated k and v rows [2][kv_dim]
     int *meta, *am;
+    float *tout, *tx, *tkv;  // l2q_engine_time_gemv outputs (2h, d, 2kv floats): the state stays untouched
     int* h_meta = nullptr;   // pinned {token, pos} slots
     int h_meta_slots = 0;
     int* h_am = nullptr;     // pinned argmax result
@@ -100,41 +101,109 @@ struct Arena {
     }
 };
 
+// The GEMVs of the step: arguments, prologue and epilogue of matrix `kind`
+// of layer l (kClassifier: the final norm + classifier, l ignored).
+enum GemvKind { kQkv = 0, kWo = 1, kW13 = 2, kW2 = 3, kClassifier = 4 };
+
+struct StepGemv {
+    GemvArgs a{};
+    int pro = kQuant, epi = kStore;
+};
+
+StepGemv step_gemv(const l2q_engine* e, int kind, int l) {
+    const l2q_config& c = e->cfg;
+    const int d = c.dim, h = c.hidden_dim, kv = e->kv_dim, G = e->G;
+    const int qkv_rows = d + 2 * kv;
+    const size_t nbd = (size_t)d / G, nbh = (size_t)h / G;
+    StepGemv g;
+    GemvArgs& a = g.a;
+    switch (kind) {
+        case kQkv: {   // x = (l == 0 ? emb[token] : xa + ffn_out) -> xb; RMSNorm; q, k, v; RoPE + append
+            a.out = e->q;
+            a.w = e->qkv_w + (size_t)l * qkv_rows * e->rowb_d;
+            a.ws = e->qkv_s + (size_t)l * qkv_rows * nbd;
+            a.rows = qkv_rows;
+            a.cols = d;
+            a.x_in = e->xa;
+            a.emb = l == 0 ? e->emb : nullptr;
+            a.resid = l == 0 ? nullptr : e->ffn_out;
+            a.x_out = e->xb;
+            a.norm_w = e->rms_att + (size_t)l * d;
+            a.meta = e->meta;
+            a.dim = d; a.kv_dim = kv; a.hs = e->hs; a.max_t = e->max_t;
+            a.kcache = e->kcache + (size_t)l * kv * e->max_t;
+            a.vcache = e->vcache + (size_t)l * kv * e->max_t;
+            a.rope = e->rope;
+            a.k_il = 1;
+            if (e->flags & L2Q_ENGINE_KV_INT8) {   // k, v rows to the staging row, quantized by the attention
+                a.kcache = e->kvf; a.vcache = e->kvf + kv; a.max_t = 1; a.kv_stage = 1; a.k_il = 0;
+            }
+            g.pro = kNorm; g.epi = kRopeKV;
+            break;
+        }
+        case kWo:   // quantize the attention output in the prologue
+            a.out = e->wo_out;
+            a.w = e->wo_w + (size_t)l * d * e->rowb_d;
+            a.ws = e->wo_s + (size_t)l * d * nbd;
+            a.rows = d;
+            a.cols = d;
+            a.x_in = e->att;
+            break;
+        case kW13:   // x = xb + wo_out -> xa; RMSNorm; SwiGLU(w1 x, w3 x) -> hb
+            a.out = e->hb;
+            a.w = e->w13_w + (size_t)l * 2 * h * e->rowb_d;
+            a.ws = e->w13_s + (size_t)l * 2 * h * nbd;
+            a.rows = 2 * h;
+            a.cols = d;
+            a.x_in = e->xb;
+            a.resid = e->wo_out;
+            a.x_out = e->xa;
+            a.norm_w = e->rms_ffn + (size_t)l * d;
+            a.meta = e->meta;
+            g.pro = kNorm; g.epi = kSwiglu;
+            break;
+        case kW2:   // quantize hb in the prologue
+            a.out = e->ffn_out;
+            a.w = e->w2_w + (size_t)l * d * e->rowb_h;
+            a.ws = e->w2_s + (size_t)l * d * nbh;
+            a.rows = d;
+            a.cols = h;
+            a.x_in = e->hb;
+            break;
+        default:   // final RMSNorm of xa + ffn_out, classifier
+            a.out = e->logits;
+            a.w = e->wcls_w;
+            a.ws = e->wcls_s;
+            a.rows = c.vocab_size;
+            a.cols = d;
+            a.x_in = e->xa;
+            a.resid = e->ffn_out;
+            a.norm_w = e->rms_final;
+            a.meta = e->meta;
+            g.pro = kNorm;
+            break;
+    }
+    return g;
+}
+
+int launch_step_gemv(const l2q_engine* e, int kind, int l, hipStream_t st) {
+    const StepGemv g = step_gemv(e, kind, l);
+    return launch_gemv_fused(e->wbits, e->G, g.pro, g.epi, g.a, st);
+}
+
 // Enqueue one decode step on `st` (captured or eager).  If `dbg_x` is set
 // (eager diagnostic mode) the residual stream after the embedding and after
 // each layer is copied to it.
 int enqueue_step(l2q_engine* e, hipStream_t st, float* dbg_x, float* dbg_tmp, bool argmax, bool fused) {
     const l2q_config& c = e->cfg;
-    const int d = c.dim, h = c.hidden_dim, kv = e->kv_dim, G = e->G, bits = e->wbits;
-    const int qkv_rows = d + 2 * kv;
-    const size_t nbd = (size_t)d / G, nbh = (size_t)h / G;
+    const int d = c.dim, kv = e->kv_dim;
     int rc;
     for (int l = 0; l < c.n_layers; l++) {
         float* kc = e->kcache + (size_t)l * kv * e->max_t;
         float* vc = e->vcache + (size_t)l * kv * e->max_t;
-        // QKV: x = (l == 0 ? emb[token] : xa + ffn_out) -> xb; RMSNorm; q, k, v
-        GemvArgs qa{};
-        qa.out = e->q;
-        qa.w = e->qkv_w + (size_t)l * qkv_rows * e->rowb_d;
-        qa.ws = e->qkv_s + (size_t)l * qkv_rows * nbd;
-        qa.rows = qkv_rows;
-        qa.cols = d;
-        qa.x_in = e->xa;
-        qa.emb = l == 0 ? e->emb : nullptr;
-        qa.resid = l == 0 ? nullptr : e->ffn_out;
-        qa.x_out = e->xb;
-        qa.norm_w = e->rms_att + (size_t)l * d;
-        qa.meta = e->meta;
-        qa.dim = d; qa.kv_dim = kv; qa.hs = e->hs; qa.max_t = e->max_t;
-        qa.kcache = kc; qa.vcache = vc; qa.rope = e->rope;
-        const bool kv8 = e->flags & L2Q_ENGINE_KV_INT8;
-        qa.k_il = kv8 ? 0 : 1;
-        if (kv8) {   // k, v rows to the staging row, then quantized into the int8 cache
-            qa.kcache = e->kvf; qa.vcache = e->kvf + kv; qa.max_t = 1; qa.kv_stage = 1;
-        }
-        if ((rc = launch_gemv_fused(bits, G, kNorm, kRopeKV, qa, st))) return rc;
+        if ((rc = launch_step_gemv(e, kQkv, l, st))) return rc;
         if (dbg_x && l == 0) HIPCHK(hipMemcpyAsync(dbg_x, e->xb, d * sizeof(float), hipMemcpyDeviceToHost, st), "copy x");
-        if (kv8) {
+        if (e->flags & L2Q_ENGINE_KV_INT8) {
             const size_t co = (size_t)l * kv * e->max_t, so = (size_t)l * c.n_kv_heads * e->max_t;
             // append the staged k, v rows and attend, in one kernel
             rc = launch_attention_kv8(e->q, e->k8 + co, e->v8 + co, e->ks + so, e->vs + so, e->att, e->scores,
@@ -144,37 +213,9 @@ int enqueue_step(l2q_engine* e, hipStream_t st, float* dbg_x, float* dbg_tmp, bo
                                         c.n_kv_heads, e->hs, e->max_t, st, 1, 0, fused ? 1 : 0, 1);
         }
         if (rc) return rc;
-        // wo: quantize the attention output in the prologue
-        GemvArgs oa{};
-        oa.out = e->wo_out;
-        oa.w = e->wo_w + (size_t)l * d * e->rowb_d;
-        oa.ws = e->wo_s + (size_t)l * d * nbd;
-        oa.rows = d;
-        oa.cols = d;
-        oa.x_in = e->att;
-        if ((rc = launch_gemv_fused(bits, G, kQuant, kStore, oa, st))) return rc;
-        // W13: x = xb + wo_out -> xa; RMSNorm; SwiGLU(w1 x, w3 x) -> hb
-        GemvArgs ha{};
-        ha.out = e->hb;
-        ha.w = e->w13_w + (size_t)l * 2 * h * e->rowb_d;
-        ha.ws = e->w13_s + (size_t)l * 2 * h * nbd;
-        ha.rows = 2 * h;
-        ha.cols = d;
-        ha.x_in = e->xb;
-        ha.resid = e->wo_out;
-        ha.x_out = e->xa;
-        ha.norm_w = e->rms_ffn + (size_t)l * d;
-        ha.meta = e->meta;
-        if ((rc = launch_gemv_fused(bits, G, kNorm, kSwiglu, ha, st))) return rc;
-        // W2: quantize hb in the prologue
-        GemvArgs fa{};
-        fa.out = e->ffn_out;
-        fa.w = e->w2_w + (size_t)l * d * e->rowb_h;
-        fa.ws = e->w2_s + (size_t)l * d * nbh;
-        fa.rows = d;
-        fa.cols = h;
-        fa.x_in = e->hb;
-        if ((rc = launch_gemv_fused(bits, G, kQuant, kStore, fa, st))) return rc;
+        if ((rc = launch_step_gemv(e, kWo, l, st))) return rc;
+        if ((rc = launch_step_gemv(e, kW13, l, st))) return rc;
+        if ((rc = launch_step_gemv(e, kW2, l, st))) return rc;
         if (dbg_x) {
             float* dst = dbg_x + (size_t)(l + 1) * d;
             HIPCHK(hipMemcpyAsync(dst, e->xa, d * sizeof(float), hipMemcpyDeviceToHost, st), "copy x");
@@ -183,18 +224,7 @@ int enqueue_step(l2q_engine* e, hipStream_t st, float* dbg_x, float* dbg_tmp, bo
             for (int i = 0; i < d; i++) dst[i] = dst[i] + dbg_tmp[i];   // the add the next norm performs
         }
     }
-    // final RMSNorm of xa + ffn_out, classifier
-    GemvArgs ca{};
-    ca.out = e->logits;
-    ca.w = e->wcls_w;
-    ca.ws = e->wcls_s;
-    ca.rows = c.vocab_size;
-    ca.cols = d;
-    ca.x_in = e->xa;
-    ca.resid = e->ffn_out;
-    ca.norm_w = e->rms_final;
-    ca.meta = e->meta;
-    if ((rc = launch_gemv_fused(bits, G, kNorm, kStore, ca, st))) return rc;
+    if ((rc = launch_step_gemv(e, kClassifier, 0, st))) return rc;
     if (argmax) return launch_argmax(e->logits, c.vocab_size, e->am, st);
     return L2Q_OK;
 }
@@ -328,6 +358,7 @@ int build(l2q_engine* e, const void* weights, size_t weights_bytes) {
     const size_t o_rope = sa.take((size_t)e->max_t * e->hs * 4);
     const size_t o_sc = sa.take((size_t)c.n_heads * e->max_t * 4);
     const size_t o_meta = sa.take(2 * sizeof(int)), o_am = sa.take(sizeof(int));
+    const size_t o_tout = sa.take((size_t)2 * h * 4 + V * 4), o_tx = sa.take(d * 4), o_tkv = sa.take(2 * kv * 4);
     e->sbytes = align_up(sa.used, 256);
     HIPCHK(hipMalloc(&e->sarena, e->sbytes), "hipMalloc(state)");
     char* S_ = e->sarena;
@@ -339,6 +370,7 @@ int build(l2q_engine* e, const void* weights, size_t weights_bytes) {
     e->k8 = (int8_t*)(S_ + o_k8); e->v8 = (int8_t*)(S_ + o_v8);
     e->ks = (float*)(S_ + o_ks); e->vs = (float*)(S_ + o_vs); e->kvf = (float*)(S_ + o_kvf);
     e->meta = (int*)(S_ + o_meta); e->am = (int*)(S_ + o_am);
+    e->tout = (float*)(S_ + o_tout); e->tx = (float*)(S_ + o_tx); e->tkv = (float*)(S_ + o_tkv);
     // zero-fill the state (outside any graph) so unused cache rows are defined
     HIPCHK(hipMemsetAsync(e->sarena, 0, e->sbytes, e->stream), "hipMemset(state)");
 
@@ -619,6 +651,36 @@ int l2q_engine_time_steps(l2q_engine* e, const int* tokens, int pos0, int n_step
         int rc = launch_step(e, tokens[i], pos0 + i, step_graph(e, false, pos0 + i), i);
         if (rc) return rc;
     }
+    HIPCHK(hipEventRecord(e->ev1, e->stream), "hipEventRecord");
+    HIPCHK(hipEventSynchronize(e->ev1), "hipEventSynchronize");
+    float ms = 0.0f;
+    HIPCHK(hipEventElapsedTime(&ms, e->ev0, e->ev1), "hipEventElapsedTime");
+    *elapsed_ms = ms;
+    return L2Q_OK;
+}
+
+int l2q_engine_time_gemv(l2q_engine* e, int kind, int n_launches, double* elapsed_ms) {
+    if (!e || !elapsed_ms || n_launches <= 0 || kind < L2Q_GEMV_QKV || kind > L2Q_GEMV_CLASSIFIER) {
+        set_error("engine: bad GEMV timing arguments");
+        return L2Q_ERR_ARG;
+    }
+    const int L = e->cfg.n_layers;
+    auto launch = [&](int i) {
+        StepGemv g = step_gemv(e, kind, i % L);
+        // outputs to the timing area: the decode state is left as it was
+        g.a.out = e->tout;
+        if (g.a.x_out) g.a.x_out = e->tx;
+        if (g.epi == kRopeKV) {
+            g.a.kcache = e->tkv; g.a.vcache = e->tkv + e->kv_dim; g.a.max_t = 1; g.a.kv_stage = 1; g.a.k_il = 0;
+        }
+        return launch_gemv_fused(e->wbits, e->G, g.pro, g.epi, g.a, e->stream);
+    };
+    int rc;
+    for (int i = 0; i < L; i++)   // warm: every layer's launch once
+        if ((rc = launch(i))) return rc;
+    HIPCHK(hipEventRecord(e->ev0, e->stream), "hipEventRecord");
+    for (int i = 0; i < n_launches; i++)
+        if ((rc = launch(i))) return rc;
     HIPCHK(hipEventRecord(e->ev1, e->stream), "hipEventRecord");
     HIPCHK(hipEventSynchronize(e->ev1), "hipEventSynchronize");
     float ms = 0.0f;

@@ -54,19 +54,26 @@ static int step(decoder* d, int token, int pos, int want_next) {
     return sampler_sample(d->sampler, d->logits);
 }
 
-/* Generation loop of runq.c:681-718: prompt forcing, stop at BOS, tok/s
- * measured from the end of the first step. */
+/* Generation loop of runq.c:681-718: prompt forcing, stop at BOS.
+ *
+ * "achieved tok/s" keeps runq's formula, (pos - 1) / elapsed (runq.c:
+ * 710-716).  runq starts its clock when step 1 ends; when the forced prompt
+ * positions run as one batched prefill there is no separate step 1, so the
+ * clock starts before that prefill (the rate then also carries step 1's
+ * work: it can only read lower than runq's).  A second line gives the rate
+ * of the positions decoded after the prefill alone. */
 static void generate(decoder* d, l2q_tokenizer* tk, const char* prompt, int steps) {
     if (prompt == NULL) prompt = "";
     int* toks = (int*)malloc((strlen(prompt) + 3) * sizeof(int));
     int n = tok_encode(tk, prompt, 1, 0, toks);
     if (n < 1) die("something is wrong, expected at least 1 prompt token", NULL);
-    long start = 0;
-    int token = toks[0], pos = 0, next, pos_start = 0, done = 0;
+    long start = 0, decode_start = 0;
+    int token = toks[0], pos = 0, next, decode_pos0 = 0, done = 0;
     /* the forced prompt positions in one batched pass (the same KV cache and
      * text as forcing them one by one, runq.c:695-700), then the loop */
     const int npf = n - 1 < steps ? n - 1 : steps;
     if (npf > 1) {
+        start = time_in_ms();
         if (l2q_engine_prefill(d->engine, toks, npf, 0, NULL) != L2Q_OK) die("prefill failed", l2q_last_error());
         for (; pos < npf; pos++) {
             next = toks[pos + 1];
@@ -75,8 +82,8 @@ static void generate(decoder* d, l2q_tokenizer* tk, const char* prompt, int step
             token = next;
         }
         fflush(stdout);
-        start = time_in_ms();
-        pos_start = pos;
+        decode_start = time_in_ms();
+        decode_pos0 = pos;
     }
     while (!done && pos < steps) {
         int forced = pos < n - 1;
@@ -87,27 +94,31 @@ static void generate(decoder* d, l2q_tokenizer* tk, const char* prompt, int step
         tok_print_piece(tok_decode(tk, token, next));
         fflush(stdout);
         token = next;
-        if (start == 0) { start = time_in_ms(); pos_start = 1; }
+        if (start == 0) { start = time_in_ms(); decode_start = start; decode_pos0 = 1; }
     }
     printf("\n");
-    if (pos > pos_start && start != 0) {
-        long end = time_in_ms();
-        fprintf(stderr, "achieved tok/s: %f\n", (pos - pos_start) / (double)(end - start) * 1000);
-    }
+    long end = time_in_ms();
+    if (pos > 1 && start != 0)
+        fprintf(stderr, "achieved tok/s: %f\n", (pos - 1) / (double)(end - start) * 1000);
+    if (npf > 1 && pos > decode_pos0 && end > decode_start)
+        fprintf(stderr, "decode tok/s (after the %d-position prefill): %f\n", npf,
+                (pos - decode_pos0) / (double)(end - decode_start) * 1000);
     free(toks);
 }
 
-static int read_line(const char* guide, char* buf, size_t n) {
+/* read_stdin of runq.c:720-729: at end of input the buffer keeps what it
+ * held, so a chat whose input has run out repeats the last user turn. */
+static void read_line(const char* guide, char* buf, size_t n) {
     printf("%s", guide);
     fflush(stdout);
-    if (fgets(buf, (int)n, stdin) == NULL) return 0;
-    size_t len = strlen(buf);
-    if (len && buf[len - 1] == '\n') buf[len - 1] = 0;
-    return 1;
+    if (fgets(buf, (int)n, stdin) != NULL) {
+        size_t len = strlen(buf);
+        if (len && buf[len - 1] == '\n') buf[len - 1] = 0;
+    }
 }
 
-/* Llama-2 chat loop of runq.c:731-794 (ending on end of input as
- * v5-cuda-fused/run.cu:1020-1021 does). */
+/* Llama-2 chat loop of runq.c:731-794 (the same templates, turn switching
+ * on id 2 and printing; it runs for `steps` positions). */
 static void chat(decoder* d, l2q_tokenizer* tk, const char* cli_user, const char* cli_system,
                  int steps) {
     char system_prompt[512] = {0}, user_prompt[512] = {0}, rendered[1152];
@@ -120,7 +131,7 @@ static void chat(decoder* d, l2q_tokenizer* tk, const char* cli_user, const char
                 else snprintf(system_prompt, sizeof system_prompt, "%s", cli_system);
             }
             if (pos == 0 && cli_user != NULL) snprintf(user_prompt, sizeof user_prompt, "%s", cli_user);
-            else if (!read_line("User: ", user_prompt, sizeof user_prompt)) break;
+            else read_line("User: ", user_prompt, sizeof user_prompt);
             if (pos == 0 && system_prompt[0] != 0)
                 snprintf(rendered, sizeof rendered, "[INST] <<SYS>>\n%s\n<</SYS>>\n\n%s [/INST]",
                          system_prompt, user_prompt);

@@ -19,6 +19,7 @@ L2Q_ENGINE_KV_INT8 = 1
 L2Q_ATTN_K_INTERLEAVED = 1
 L2Q_ATTN_ONE_KERNEL = 2
 L2Q_ATTN_TWO_KERNELS = 4
+L2Q_GEMV_QKV, L2Q_GEMV_WO, L2Q_GEMV_W13, L2Q_GEMV_W2, L2Q_GEMV_CLASSIFIER = range(5)
 
 
 class L2QError(RuntimeError):
@@ -48,6 +49,7 @@ SIGNATURES = {
     "l2q_engine_forward_debug": (I, [P, I, I, P, P]),
     "l2q_engine_prefill": (I, [P, P, I, I, P]),
     "l2q_engine_time_steps": (I, [P, P, I, I, C.POINTER(C.c_double)]),
+    "l2q_engine_time_gemv": (I, [P, I, I, C.POINTER(C.c_double)]),
     "l2q_engine_device_bytes": (C.c_size_t, [P]),
     "l2q_engine_destroy": (None, [P]),
     "l2q_quantize_act": (I, [P, I, I, P, P, P]),

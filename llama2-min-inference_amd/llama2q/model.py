@@ -62,6 +62,14 @@ class Engine:
         abi.call("l2q_engine_time_steps", self._h, t.ctypes.data, pos0, len(t), C.byref(ms))
         return ms.value
 
+    def time_gemv(self, kind: int, n_launches: int) -> float:
+        """Device milliseconds for n_launches of the step's GEMV kernel of
+        `kind` (abi.L2Q_GEMV_*) with the decode's arguments, rotating over
+        the layers' weights; the decode state is left unchanged."""
+        ms = C.c_double()
+        abi.call("l2q_engine_time_gemv", self._h, kind, n_launches, C.byref(ms))
+        return ms.value
+
     def greedy(self, prompt, n_steps: int, device_argmax: bool = True):
         """Force `prompt`, then pick argmax until n_steps positions have run.
         Returns the id chosen after every position (no BOS stop)."""

@@ -204,13 +204,31 @@ def test_hs64_g32_gqa_logits(gpu_lib, bits):
     orc.close()
 
 
-@pytest.mark.parametrize("prompt,steps", [("Once upon a time", 48), ("a", 20)])
-def test_runner_output_equals_reference_runq(gpu_lib, c1_q8, tmp_path, prompt, steps):
+RUNNER_CASES = {
+    # greedy generation (device argmax), prompt forced by the batched prefill
+    "greedy_long": ["-n", "48", "-t", "0", "-i", "Once upon a time"],
+    "greedy_short": ["-n", "20", "-t", "0", "-i", "a"],
+    # sampled generation: temperature + top-p (sample_topp) and plain
+    # multinomial (-p 1: sample_mult), seeded; runq.c:652-667
+    "topp": ["-n", "40", "-t", "0.9", "-p", "0.9", "-s", "7", "-i", "Once upon a time"],
+    "mult": ["-n", "32", "-t", "1.0", "-p", "1.0", "-s", "42", "-i", "a b"],
+    # chat mode with the user and system prompts on the command line and no
+    # input on stdin (runq.c:731-794): the Llama-2 template, a full forward +
+    # sample at every position; greedy and sampled
+    "chat_greedy": ["-n", "64", "-t", "0", "-m", "chat", "-i", "hello there", "-y", "You are terse."],
+    "chat_sampled": ["-n", "48", "-t", "0.8", "-p", "0.9", "-s", "3", "-m", "chat", "-i", "hi",
+                     "-y", "Be brief."],
+}
+
+
+@pytest.mark.parametrize("case", sorted(RUNNER_CASES))
+def test_runner_output_equals_reference_runq(gpu_lib, c1_q8, tmp_path, case):
     """The drop-in runner against the reference's own runq executable
     (compiled from v1-int8-vnni/runq.c by oracle/Makefile) on the same
-    checkpoint, tokenizer and flags, greedy: identical generated text.  The
-    runner prefills the forced prompt positions in one batched pass; runq
-    forces them one by one."""
+    checkpoint, tokenizer and flags: identical stdout.  The runner prefills
+    the forced prompt positions of generate mode in one batched pass; runq
+    forces them one by one.  Sampling draws from the same xorshift64* stream
+    over bit-identical logits, so sampled text matches too."""
     import subprocess
     from conftest import PKG, REPO
     runq = os.path.join(REPO, "oracle", "_ref", "runq")
@@ -220,12 +238,14 @@ def test_runner_output_equals_reference_runq(gpu_lib, c1_q8, tmp_path, prompt, s
     c1_q8.save(model)
     pieces, scores = host.synth_tokenizer_pieces(32000)
     host.write_tokenizer(tok, pieces, scores)
-    args = [model, "-z", tok, "-n", str(steps), "-t", "0", "-i", prompt]
-    ref = subprocess.run([runq] + args, capture_output=True, text=True, timeout=300,
+    args = [model, "-z", tok] + RUNNER_CASES[case]
+    ref = subprocess.run([runq] + args, capture_output=True, text=True, timeout=300, stdin=subprocess.DEVNULL,
                          env={**os.environ, "OMP_NUM_THREADS": "4"})
     got = subprocess.run([os.path.join(PKG, "build", "llama2q_run")] + args, capture_output=True, text=True,
-                         timeout=300)
+                         timeout=300, stdin=subprocess.DEVNULL)
     assert ref.returncode == 0, ref.stderr
     assert got.returncode == 0, got.stderr
+    assert len(got.stdout) > 20
     assert got.stdout == ref.stdout
-    assert "achieved tok/s" in got.stderr
+    if "chat" not in case:
+        assert "achieved tok/s" in got.stderr
