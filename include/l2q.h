@@ -258,6 +258,20 @@ int l2q_attention_split(const float* q, const float* kcache, const float* vcache
                         float* out, int pos, int n_heads, int n_kv_heads,
                         int head_size, int max_t, void* stream);
 
+/* l2q_attention_split without any device allocation, for callers that
+ * cannot allocate (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc).  No counterpart in the reference.  Same
+ * arguments, kernels and results as l2q_attention_split; its partials live
+ * in a static per-GPU scratch array of 2^20 floats (4 MiB, held until the
+ * process ends), so n_heads * splits * (head_size + 2) must fit in it
+ * (splits = ceil((pos + 1) / 128), at most 512); larger calls return
+ * L2Q_ERR_ARG.  Every call on one GPU shares that array: calls that overlap
+ * on one GPU (other streams or threads) race and must be serialized by the
+ * caller. */
+int l2q_attention_split_noalloc(const float* q, const float* kcache, const float* vcache,
+                                float* out, int pos, int n_heads, int n_kv_heads,
+                                int head_size, int max_t, void* stream);
+
 /* Batched GEMV of T activation vectors (a GEMM): out[t][r] = the row-r
  * output of l2q_gemv_q8 / l2q_gemv_q4 for input t, bit for bit, for
  * t < T.  xq [T][cols] int8 and xs [T][cols/group] as l2q_quantize_act

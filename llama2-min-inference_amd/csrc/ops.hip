@@ -1,5 +1,7 @@
 // ops.hip - launchers and the op-level C ABI (see include/l2q.h).
 #include <hip/hip_runtime.h>
+
+#include <mutex>
 #include <math.h>
 #include <stdarg.h>
 #include <stdio.h>
@@ -481,6 +483,31 @@ static int attn_scratch(size_t floats, float** out) {
     return L2Q_OK;
 }
 
+// Device scratch of l2q_attention_split_noalloc: a file-scope array, one copy
+// per GPU, held until the process ends.  Host code never passes the array's
+// name to a kernel (on the host it is only a stand-in for the symbol): the
+// device address comes from hipGetSymbolAddress, once per device.
+constexpr size_t kNoAllocScratchFloats = (size_t)1 << 20;   // 4 MiB
+static __device__ __align__(256) float scratch[kNoAllocScratchFloats];
+static float* g_scratch_ptr[64];
+static std::mutex g_scratch_mu;
+
+static int noalloc_scratch(float** out) {
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return hip_fail(e, "hipGetDevice");
+    if (dev < 0 || dev >= 64) { set_error("attention: device %d out of range", dev); return L2Q_ERR_ARG; }
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (!g_scratch_ptr[dev]) {
+        void* p = nullptr;
+        e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess || !p) return hip_fail(e != hipSuccess ? e : hipErrorInvalidSymbol, "hipGetSymbolAddress(scratch)");
+        g_scratch_ptr[dev] = static_cast<float*>(p);
+    }
+    *out = g_scratch_ptr[dev];
+    return L2Q_OK;
+}
+
 }  // namespace l2q
 
 using namespace l2q;
@@ -620,6 +647,28 @@ int l2q_attention_split(const float* q, const float* kcache, const float* vcache
     if (rc) return rc;
     return launch_attention_split(q, kcache, vcache, out, scratch, scratch + (size_t)n_heads * S * head_size, S,
                                   nullptr, pos, n_heads, n_kv_heads, head_size, max_t, (hipStream_t)stream);
+}
+
+int l2q_attention_split_noalloc(const float* q, const float* kcache, const float* vcache, float* out, int pos,
+                                int n_heads, int n_kv_heads, int head_size, int max_t, void* stream) {
+    if (!attention_shape_ok(n_heads, n_kv_heads, head_size) || pos < 0 || pos >= max_t) {
+        set_error("attention: bad shape heads=%d kv_heads=%d hs=%d pos=%d max_t=%d", n_heads, n_kv_heads, head_size,
+                  pos, max_t);
+        return L2Q_ERR_ARG;
+    }
+    const int S = attention_splits(pos);
+    const size_t need = (size_t)n_heads * S * (head_size + 2);
+    if (need > kNoAllocScratchFloats) {
+        set_error("attention_split_noalloc: %d heads x %d splits x (%d + 2) partial floats exceed the %zu-float "
+                  "static scratch",
+                  n_heads, S, head_size, kNoAllocScratchFloats);
+        return L2Q_ERR_ARG;
+    }
+    float* buf = nullptr;
+    int rc = noalloc_scratch(&buf);
+    if (rc) return rc;
+    return launch_attention_split(q, kcache, vcache, out, buf, buf + (size_t)n_heads * S * head_size, S, nullptr, pos,
+                                  n_heads, n_kv_heads, head_size, max_t, (hipStream_t)stream);
 }
 
 int l2q_argmax(const float* v, int n, int* out, void* stream) {

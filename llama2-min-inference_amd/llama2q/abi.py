@@ -64,6 +64,7 @@ SIGNATURES = {
     "l2q_attention_ex": (I, [P, P, P, P, I, I, I, I, I, I, P]),
     "l2q_argmax": (I, [P, I, P, P]),
     "l2q_attention_split": (I, [P, P, P, P, I, I, I, I, I, P]),
+    "l2q_attention_split_noalloc": (I, [P, P, P, P, I, I, I, I, I, P]),
     "l2q_kv8_append": (I, [P, P, P, P, P, P, P, I, I, I, I, P]),
     "l2q_attention_kv8": (I, [P, P, P, P, P, P, I, I, I, I, I, P]),
     "l2q_expf": (I, [P, P, C.c_size_t, P]),
