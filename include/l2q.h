@@ -112,6 +112,14 @@ int l2q_engine_prefill(l2q_engine* e, const int* tokens, int n, int pos0,
 /* Engine options (l2q_engine_create_ex). */
 #define L2Q_ENGINE_KV_INT8 1   /* int8 KV cache (l2q_kv8_append / l2q_attention_kv8
                                   semantics), the reference's -DINT8_KV=1 build */
+#define L2Q_ENGINE_STEP_KERNEL 2   /* run each decode step as one persistent
+                                  kernel with grid barriers between its phases
+                                  where the shape allows it (see
+                                  l2q_engine_uses_step_kernel) instead of the
+                                  graph of one kernel per op (v5-cuda-fused/
+                                  run.cu:600-679's op sequence); same bits.
+                                  Opt-in: slower than the graph on MI355X
+                                  today.  No counterpart in the reference. */
 
 /* l2q_engine_create with option flags (0 gives l2q_engine_create). */
 int l2q_engine_create_ex(const l2q_config* cfg, const void* weights,
@@ -159,6 +167,13 @@ int l2q_engine_time_steps(l2q_engine* e, const int* tokens, int pos0,
 #define L2Q_GEMV_W2         3   /* w2: Q8 quantize prologue */
 #define L2Q_GEMV_CLASSIFIER 4   /* wcls: final RMSNorm prologue */
 int l2q_engine_time_gemv(l2q_engine* e, int kind, int n_launches, double* elapsed_ms);
+
+/* 1 when the engine runs each decode step as one persistent kernel
+ * (L2Q_ENGINE_STEP_KERNEL was given and the shape has it: INT4 group 64, the
+ * Llama-2-7B row shapes, head size 128, fp32 KV cache, one workgroup resident
+ * per CU), 0 when it runs the per-op kernel graph.  Both give the same bits.
+ * No counterpart in the reference. */
+int l2q_engine_uses_step_kernel(const l2q_engine* e);
 
 /* Device bytes held by the engine (weights + KV cache + activations). */
 size_t l2q_engine_device_bytes(const l2q_engine* e);

@@ -35,6 +35,7 @@
 #include <stdlib.h>
 #include <string.h>
 
+#include <algorithm>
 #include <cstring>
 #include <new>
 #include <vector>
@@ -69,9 +70,17 @@ struct l2q_engine {
     float* kvf;              //   the position's rotated k and v rows [2][kv_dim]
     int *meta, *am;
     float *tout, *tx, *tkv;  // l2q_engine_time_gemv outputs (2h, d, 2kv floats): the state stays untouched
+    // the one-kernel step (step.h): used when L2Q_ENGINE_STEP_KERNEL is set and the shape has it
+    bool step = false;
+    l2q::StepArgs sa{};
+    int step_grid = 0;
+    size_t step_lds_bytes = 0;
+    unsigned* sync = nullptr;   // grp | top | rel | err | epoch (StepSync)
+    size_t sync_bytes = 0;
+    float* dbg = nullptr;       // [L+1][d]: the residual stream of forward_debug
     int* h_meta = nullptr;   // pinned {token, pos} slots
     int h_meta_slots = 0;
-    int* h_am = nullptr;     // pinned argmax result
+    int* h_am = nullptr;     // pinned argmax result, then the step kernel's error word
     // batched prefill (allocated at the first l2q_engine_prefill): T tokens per chunk
     char* pfarena = nullptr;
     int pf_T = 0;
@@ -229,9 +238,86 @@ int enqueue_step(l2q_engine* e, hipStream_t st, float* dbg_x, float* dbg_tmp, bo
     return L2Q_OK;
 }
 
+// Whether the one-kernel step serves this engine (L2Q_ENGINE_STEP_KERNEL): INT4 weights in groups of
+// 64, dim-wide rows of 2 sweeps, w2 rows of 5-6 sweeps, heads of 128 with
+// the fp32 cache, a cache the fused attention holds, staged outputs within
+// kStepStage per wave, LDS within the CU's and one resident workgroup per CU.
+int step_setup(l2q_engine* e, int ncu) {
+    const l2q_config& c = e->cfg;
+    e->step = false;
+    if (!(e->flags & L2Q_ENGINE_STEP_KERNEL) || (e->flags & L2Q_ENGINE_KV_INT8) || ncu <= 0 || ncu % 8) return L2Q_OK;
+    if (e->wbits != 4 || e->G != 64 || !step_shape_ok(c.dim, c.hidden_dim, e->hs)) return L2Q_OK;
+    if (e->max_t > attention_fused_max()) return L2Q_OK;
+    // row pairs per workgroup within the fold areas; staged outputs per wave
+    const int rows_max = std::max(std::max(c.dim + 2 * e->kv_dim, 2 * c.hidden_dim), c.vocab_size);
+    const int pairs_wg = ((rows_max + 1) / 2 + ncu - 1) / ncu;
+    if (pairs_wg > kStepPairsCap || (c.dim / 2 + ncu - 1) / ncu > kStepPairsCapH) return L2Q_OK;
+    if (2 * ((pairs_wg + kStepCompute - 1) / kStepCompute) > kStepStage) return L2Q_OK;
+    const int items = c.n_heads * (e->hs / kStepAttnSlice);
+    if (kStepAttnSlice * ((items + ncu - 1) / ncu) > kStepStage) return L2Q_OK;
+    const size_t lds = step_lds_bytes();
+    int maxlds = 0;
+    if (hipDeviceGetAttribute(&maxlds, hipDeviceAttributeMaxSharedMemoryPerMultiprocessor, e->device) != hipSuccess ||
+        lds > (size_t)maxlds)
+        return L2Q_OK;
+    int per_cu = 0;
+    int rc = step_prepare(lds, &per_cu);
+    if (rc) return rc;
+    if (per_cu < 1) return L2Q_OK;
+    StepArgs& a = e->sa;
+    a.qkv_w = e->qkv_w; a.wo_w = e->wo_w; a.w13_w = e->w13_w; a.w2_w = e->w2_w; a.wcls_w = e->wcls_w;
+    a.qkv_s = e->qkv_s; a.wo_s = e->wo_s; a.w13_s = e->w13_s; a.w2_s = e->w2_s; a.wcls_s = e->wcls_s;
+    a.emb = e->emb; a.rms_att = e->rms_att; a.rms_ffn = e->rms_ffn; a.rms_final = e->rms_final; a.rope = e->rope;
+    a.xa = e->xa; a.xb = e->xb; a.q = e->q; a.att = e->att; a.wo_out = e->wo_out; a.hb = e->hb;
+    a.ffn_out = e->ffn_out; a.logits = e->logits; a.kcache = e->kcache; a.vcache = e->vcache;
+    a.meta = e->meta;
+    a.dbg_x = nullptr;
+    a.sync.grp = e->sync;
+    a.sync.top = e->sync + 8 * 16;
+    a.sync.rel = e->sync + 9 * 16;
+    a.sync.err = a.sync.rel + (size_t)ncu * 16;
+    a.sync.epoch = a.sync.err + 16;
+    a.d = c.dim; a.h = c.hidden_dim; a.L = c.n_layers; a.V = c.vocab_size;
+    a.n_heads = c.n_heads; a.n_kv = c.n_kv_heads; a.hs = e->hs; a.kv = e->kv_dim; a.max_t = e->max_t;
+    a.rowb_d = (int)e->rowb_d; a.rowb_h = (int)e->rowb_h;
+    a.nbar = step_phases(c.n_layers) - 1;
+    e->step_grid = ncu;
+    e->step_lds_bytes = lds;
+    e->step = true;
+    return L2Q_OK;
+}
+
+int launch_step_kernel(l2q_engine* e, hipStream_t st, float* dbg) {
+    StepArgs a = e->sa;
+    a.dbg_x = dbg;
+    return launch_step_kernel(a, e->step_grid, e->step_lds_bytes, st);
+}
+
+// A timed-out step leaves the barrier state inconsistent: report it and
+// reset the state (zeroed counters, epoch 0) for the next launch.
+int step_check(l2q_engine* e) {
+    if (!e->step || e->h_am[1] == 0) return L2Q_OK;
+    (void)hipMemsetAsync(e->sync, 0, e->sync_bytes, e->stream);
+    (void)hipStreamSynchronize(e->stream);
+    set_error("engine: a grid barrier of the decode step timed out (not every workgroup was resident)");
+    return L2Q_ERR_HIP;
+}
+
+int copy_step_err(l2q_engine* e) {
+    if (!e->step) return L2Q_OK;
+    HIPCHK(hipMemcpyAsync(e->h_am + 1, e->sa.sync.err, sizeof(int), hipMemcpyDeviceToHost, e->stream), "copy step error");
+    return L2Q_OK;
+}
+
 int capture(l2q_engine* e, bool argmax, bool fused, hipGraph_t* g, hipGraphExec_t* ex) {
     HIPCHK(hipStreamBeginCapture(e->stream, hipStreamCaptureModeThreadLocal), "hipStreamBeginCapture");
-    int rc = enqueue_step(e, e->stream, nullptr, nullptr, argmax, fused);
+    int rc;
+    if (e->step) {
+        rc = launch_step_kernel(e, e->stream, nullptr);
+        if (!rc && argmax) rc = launch_argmax(e->logits, e->cfg.vocab_size, e->am, e->stream);
+    } else {
+        rc = enqueue_step(e, e->stream, nullptr, nullptr, argmax, fused);
+    }
     hipGraph_t graph = nullptr;
     hipError_t ee = hipStreamEndCapture(e->stream, &graph);
     if (rc) {
@@ -359,6 +445,10 @@ int build(l2q_engine* e, const void* weights, size_t weights_bytes) {
     const size_t o_sc = sa.take((size_t)c.n_heads * e->max_t * 4);
     const size_t o_meta = sa.take(2 * sizeof(int)), o_am = sa.take(sizeof(int));
     const size_t o_tout = sa.take((size_t)2 * h * 4 + V * 4), o_tx = sa.take(d * 4), o_tkv = sa.take(2 * kv * 4);
+    int ncu = 0;
+    if (hipDeviceGetAttribute(&ncu, hipDeviceAttributeMultiprocessorCount, e->device) != hipSuccess || ncu < 8) ncu = 0;
+    e->sync_bytes = (size_t)(8 * 16 + 16 + (size_t)(ncu > 0 ? ncu : 8) * 16 + 16 + 16) * sizeof(unsigned);
+    const size_t o_sync = sa.take(e->sync_bytes), o_dbg = sa.take((L + 1) * d * 4);
     e->sbytes = align_up(sa.used, 256);
     HIPCHK(hipMalloc(&e->sarena, e->sbytes), "hipMalloc(state)");
     char* S_ = e->sarena;
@@ -371,6 +461,7 @@ int build(l2q_engine* e, const void* weights, size_t weights_bytes) {
     e->ks = (float*)(S_ + o_ks); e->vs = (float*)(S_ + o_vs); e->kvf = (float*)(S_ + o_kvf);
     e->meta = (int*)(S_ + o_meta); e->am = (int*)(S_ + o_am);
     e->tout = (float*)(S_ + o_tout); e->tx = (float*)(S_ + o_tx); e->tkv = (float*)(S_ + o_tkv);
+    e->sync = (unsigned*)(S_ + o_sync); e->dbg = (float*)(S_ + o_dbg);
     // zero-fill the state (outside any graph) so unused cache rows are defined
     HIPCHK(hipMemsetAsync(e->sarena, 0, e->sbytes, e->stream), "hipMemset(state)");
 
@@ -381,12 +472,13 @@ int build(l2q_engine* e, const void* weights, size_t weights_bytes) {
 
     e->h_meta_slots = 1;
     HIPCHK(hipHostMalloc((void**)&e->h_meta, 2 * sizeof(int) * e->h_meta_slots, hipHostMallocDefault), "hipHostMalloc");
-    HIPCHK(hipHostMalloc((void**)&e->h_am, sizeof(int), hipHostMallocDefault), "hipHostMalloc");
+    HIPCHK(hipHostMalloc((void**)&e->h_am, 2 * sizeof(int), hipHostMallocDefault), "hipHostMalloc");
+    if ((rc = step_setup(e, ncu))) return rc;
     HIPCHK(hipEventCreate(&e->ev0), "hipEventCreate");
     HIPCHK(hipEventCreate(&e->ev1), "hipEventCreate");
     // short contexts: one-kernel attention where the head size has it
-    const bool fused = attention_fused_ok(e->hs) && !(e->flags & L2Q_ENGINE_KV_INT8);
-    const bool need_long = !fused || e->max_t > attention_fused_max();
+    const bool fused = e->step || (attention_fused_ok(e->hs) && !(e->flags & L2Q_ENGINE_KV_INT8));
+    const bool need_long = !e->step && (!fused || e->max_t > attention_fused_max());
     for (int a = 0; a < 2; a++) {
         if (fused && (rc = capture(e, a, true, &e->graph[a][0], &e->exec[a][0]))) return rc;
         if (need_long && (rc = capture(e, a, false, &e->graph[a][1], &e->exec[a][1]))) return rc;
@@ -567,7 +659,7 @@ int l2q_engine_create_ex(const l2q_config* cfg, const void* weights, size_t weig
         return L2Q_ERR_ARG;
     }
     const int steps = max_steps <= 0 || max_steps > c.seq_len ? c.seq_len : max_steps;
-    if ((flags & ~L2Q_ENGINE_KV_INT8) ||
+    if ((flags & ~(L2Q_ENGINE_KV_INT8 | L2Q_ENGINE_STEP_KERNEL)) ||
         ((flags & L2Q_ENGINE_KV_INT8) && !kv8_shape_ok(c.n_heads, c.n_kv_heads, hs, steps))) {
         set_error("engine: unsupported flags %d for this shape (int8 KV needs head_size %% 16 == 0, <= 8192 steps)",
                   flags);
@@ -602,8 +694,9 @@ int l2q_engine_forward(l2q_engine* e, int token, int pos, float* logits) {
     if (logits)
         HIPCHK(hipMemcpyAsync(logits, e->logits, (size_t)e->cfg.vocab_size * 4, hipMemcpyDeviceToHost, e->stream),
                "copy logits");
+    if ((rc = copy_step_err(e))) return rc;
     HIPCHK(hipStreamSynchronize(e->stream), "hipStreamSynchronize");
-    return L2Q_OK;
+    return step_check(e);
 }
 
 int l2q_engine_forward_argmax(l2q_engine* e, int token, int pos, int* next) {
@@ -612,7 +705,9 @@ int l2q_engine_forward_argmax(l2q_engine* e, int token, int pos, int* next) {
     if (!next) { set_error("engine: null output"); return L2Q_ERR_ARG; }
     if ((rc = launch_step(e, token, pos, step_graph(e, true, pos), 0))) return rc;
     HIPCHK(hipMemcpyAsync(e->h_am, e->am, sizeof(int), hipMemcpyDeviceToHost, e->stream), "copy argmax");
+    if ((rc = copy_step_err(e))) return rc;
     HIPCHK(hipStreamSynchronize(e->stream), "hipStreamSynchronize");
+    if ((rc = step_check(e))) return rc;
     *next = *e->h_am;
     return L2Q_OK;
 }
@@ -624,14 +719,22 @@ int l2q_engine_forward_debug(l2q_engine* e, int token, int pos, float* x_layers,
     e->h_meta[0] = token;
     e->h_meta[1] = pos;
     HIPCHK(hipMemcpyAsync(e->meta, e->h_meta, 2 * sizeof(int), hipMemcpyHostToDevice, e->stream), "upload meta");
-    std::vector<float> tmp(e->cfg.dim);
-    if ((rc = enqueue_step(e, e->stream, x_layers, tmp.data(), false, step_graph(e, false, pos) == e->exec[0][0])))
-        return rc;
+    if (e->step) {
+        if ((rc = launch_step_kernel(e, e->stream, e->dbg))) return rc;
+        HIPCHK(hipMemcpyAsync(x_layers, e->dbg, (size_t)(e->cfg.n_layers + 1) * e->cfg.dim * sizeof(float),
+                              hipMemcpyDeviceToHost, e->stream),
+               "copy x");
+        if ((rc = copy_step_err(e))) return rc;
+    } else {
+        std::vector<float> tmp(e->cfg.dim);
+        if ((rc = enqueue_step(e, e->stream, x_layers, tmp.data(), false, step_graph(e, false, pos) == e->exec[0][0])))
+            return rc;
+    }
     if (logits)
         HIPCHK(hipMemcpyAsync(logits, e->logits, (size_t)e->cfg.vocab_size * 4, hipMemcpyDeviceToHost, e->stream),
                "copy logits");
     HIPCHK(hipStreamSynchronize(e->stream), "hipStreamSynchronize");
-    return L2Q_OK;
+    return step_check(e);
 }
 
 int l2q_engine_time_steps(l2q_engine* e, const int* tokens, int pos0, int n_steps, double* elapsed_ms) {
@@ -652,11 +755,14 @@ int l2q_engine_time_steps(l2q_engine* e, const int* tokens, int pos0, int n_step
         if (rc) return rc;
     }
     HIPCHK(hipEventRecord(e->ev1, e->stream), "hipEventRecord");
+    int rc = copy_step_err(e);
+    if (rc) return rc;
     HIPCHK(hipEventSynchronize(e->ev1), "hipEventSynchronize");
+    HIPCHK(hipStreamSynchronize(e->stream), "hipStreamSynchronize");
     float ms = 0.0f;
     HIPCHK(hipEventElapsedTime(&ms, e->ev0, e->ev1), "hipEventElapsedTime");
     *elapsed_ms = ms;
-    return L2Q_OK;
+    return step_check(e);
 }
 
 int l2q_engine_time_gemv(l2q_engine* e, int kind, int n_launches, double* elapsed_ms) {
@@ -688,6 +794,8 @@ int l2q_engine_time_gemv(l2q_engine* e, int kind, int n_launches, double* elapse
     *elapsed_ms = ms;
     return L2Q_OK;
 }
+
+int l2q_engine_uses_step_kernel(const l2q_engine* e) { return e && e->step ? 1 : 0; }
 
 size_t l2q_engine_device_bytes(const l2q_engine* e) { return e ? e->wbytes + e->sbytes : 0; }
 

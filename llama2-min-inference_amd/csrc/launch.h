@@ -8,6 +8,7 @@
 
 #include "gemv.h"
 #include "l2q.h"
+#include "step_args.h"
 
 namespace l2q {
 
@@ -89,6 +90,14 @@ int launch_pf_embed(const float* emb, const int* tokens, float* x, int dim, int 
 int launch_pf_swiglu_quant(const float* h13, int n, int T, int group, int8_t* xq, float* xs, hipStream_t st);
 
 int launch_argmax(const float* v, int n, int* out, hipStream_t st);
+
+// The one-kernel decode step (step.h): whether it is built for this shape;
+// bytes of its LDS layout; raising its LDS limit to `lds` and reporting how
+// many of its workgroups fit on one CU; one launch of `grid` workgroups.
+bool step_shape_ok(int d, int h, int hs);
+size_t step_lds_bytes();
+int step_prepare(size_t lds, int* per_cu);
+int launch_step_kernel(const StepArgs& a, int grid, size_t lds, hipStream_t st);
 int launch_unbias(const uint8_t* src, int8_t* dst, size_t n, hipStream_t st);
 
 // Shape checks shared by the op ABI and the engine.

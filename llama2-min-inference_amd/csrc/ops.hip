@@ -11,6 +11,7 @@
 #include "kernels.h"
 #include "prefill.h"
 #include "launch.h"
+#include "step.h"
 
 namespace l2q {
 
@@ -481,6 +482,33 @@ static int attn_scratch(size_t floats, float** out) {
     }
     *out = s.buf;
     return L2Q_OK;
+}
+
+// The instantiated one-kernel step: the Llama-2-7B shape.
+constexpr int kStepD = 4096, kStepH = 11008, kStepHs = 128;
+
+bool step_shape_ok(int d, int h, int hs) { return d == kStepD && h == kStepH && hs == kStepHs; }
+
+size_t step_lds_bytes() { return (size_t)StepShape<kStepD, kStepH, kStepHs>::kTotal * sizeof(float); }
+
+int step_prepare(size_t lds, int* per_cu) {
+    const void* fn = reinterpret_cast<const void*>(&k_step<kStepD, kStepH, kStepHs>);
+    hipError_t e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+    if (e != hipSuccess) return hip_fail(e, "hipFuncSetAttribute(step)");
+    e = hipOccupancyMaxActiveBlocksPerMultiprocessor(per_cu, fn, kStepThreads, lds);
+    if (e != hipSuccess) return hip_fail(e, "occupancy(step)");
+    return L2Q_OK;
+}
+
+#ifdef L2Q_STEP_TRACE
+extern "C" int l2q_step_trace_read(void* dst, size_t bytes) {
+    return hipMemcpyFromSymbol(dst, HIP_SYMBOL(g_step_trace), bytes) == hipSuccess ? 0 : -2;
+}
+#endif
+
+int launch_step_kernel(const StepArgs& a, int grid, size_t lds, hipStream_t st) {
+    hipLaunchKernelGGL((k_step<kStepD, kStepH, kStepHs>), dim3(grid), dim3(kStepThreads), lds, st, a);
+    return check_launch("step");
 }
 
 // Device scratch of l2q_attention_split_noalloc: a file-scope array, one copy

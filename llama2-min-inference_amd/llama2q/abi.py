@@ -16,6 +16,7 @@ L2Q_ERR_FORMAT = -3
 L2Q_ERR_NOMEM = -4
 L2Q_ERR_STATE = -5
 L2Q_ENGINE_KV_INT8 = 1
+L2Q_ENGINE_STEP_KERNEL = 2
 L2Q_ATTN_K_INTERLEAVED = 1
 L2Q_ATTN_ONE_KERNEL = 2
 L2Q_ATTN_TWO_KERNELS = 4
@@ -51,6 +52,7 @@ SIGNATURES = {
     "l2q_engine_time_steps": (I, [P, P, I, I, C.POINTER(C.c_double)]),
     "l2q_engine_time_gemv": (I, [P, I, I, C.POINTER(C.c_double)]),
     "l2q_engine_device_bytes": (C.c_size_t, [P]),
+    "l2q_engine_uses_step_kernel": (I, [P]),
     "l2q_engine_destroy": (None, [P]),
     "l2q_quantize_act": (I, [P, I, I, P, P, P]),
     "l2q_gemv_q8": (I, [P, P, P, P, P, I, I, I, P, P]),

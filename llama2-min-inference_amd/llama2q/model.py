@@ -12,16 +12,19 @@ from .host import Checkpoint
 
 
 class Engine:
-    def __init__(self, ckpt: Checkpoint, max_steps: int = 0, kv8: bool = False):
-        """kv8: int8 KV cache (L2Q_ENGINE_KV_INT8, the reference's INT8_KV build)."""
+    def __init__(self, ckpt: Checkpoint, max_steps: int = 0, kv8: bool = False, step_kernel: bool = False):
+        """kv8: int8 KV cache (L2Q_ENGINE_KV_INT8, the reference's INT8_KV build);
+        step_kernel: run each step as one persistent kernel where the shape
+        allows it (L2Q_ENGINE_STEP_KERNEL; same bits as the per-op graph)."""
         if ckpt.header.shared_weights:
             raise ValueError("shared weights not supported")   # runq.c:247-251
         self.cfg = ckpt.cfg
         self.vocab = self.cfg.vocab_size
         w = ckpt.weights
         h = C.c_void_p()
+        flags = (abi.L2Q_ENGINE_KV_INT8 if kv8 else 0) | (abi.L2Q_ENGINE_STEP_KERNEL if step_kernel else 0)
         abi.call("l2q_engine_create_ex", C.byref(self.cfg), w.ctypes.data, w.nbytes, ckpt.wbits, ckpt.group,
-                 max_steps, abi.L2Q_ENGINE_KV_INT8 if kv8 else 0, C.byref(h))
+                 max_steps, flags, C.byref(h))
         self._h = h
         self.max_steps = max_steps if 0 < max_steps <= self.cfg.seq_len else self.cfg.seq_len
         self._logits = np.empty(self.vocab, dtype=np.float32)
@@ -86,6 +89,11 @@ class Engine:
             ids.append(int(nxt))
             token = nxt
         return ids
+
+    @property
+    def step_kernel(self) -> bool:
+        """Whether each step runs as the one persistent kernel."""
+        return bool(abi.lib().l2q_engine_uses_step_kernel(self._h))
 
     @property
     def device_bytes(self) -> int:

@@ -15,7 +15,10 @@ restatement of runq.c:320-421 with the tools/quantize_int4.py dequant):
     residual stream after the embedding and after each of the 32 layers,
     and the logits, must be bit-identical (sha256 of the fp32 bytes).
 The checkpoint generator is pinned by the sha256 of the image's first and
-last 64 MiB.
+last 64 MiB.  Both step forms run the case: the default graph of one kernel
+per op, and the opt-in single persistent kernel (L2Q_ENGINE_STEP_KERNEL),
+whose eager diagnostic form writes the per-layer residual stream from inside
+the kernel.
 """
 import hashlib
 import json
@@ -49,11 +52,13 @@ def c5():
     return ck, gold
 
 
-def test_c5_full_depth_greedy_256_and_layers(gpu_lib, c5):
+@pytest.mark.parametrize("step_kernel", [False, True], ids=["graph", "step_kernel"])
+def test_c5_full_depth_greedy_256_and_layers(gpu_lib, c5, step_kernel):
     ck, gold = c5
     prompt = gold["prompt"]
     n_pos = gold["n_positions"]
-    eng = Engine(ck, max_steps=n_pos)
+    eng = Engine(ck, max_steps=n_pos, step_kernel=step_kernel)
+    assert eng.step_kernel == step_kernel, "the MI355X (256 CUs) runs this shape as one kernel when asked"
     eng.prefill(prompt[:-1], 0, logits=False)
     token, ids = prompt[-1], []
     for pos in range(len(prompt) - 1, n_pos):
