@@ -208,39 +208,59 @@ def cpu_info():
             "nproc": os.cpu_count(), "omp_threads": int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))}
 
 
-def cpu_matmul(reps=7):
-    """matmul_q8 (runq.c:142-159) on the config-2 shapes, median of `reps`
-    calls, in GB/s of the config-2 algorithmic bytes: group 32 through the
-    reference's own function (compiled runq.c), group 64 through the C port
-    (oracle.c orc_matmul_q8), since runq fixes its group at QBLOCK = 32."""
+def cpu_matmul(reps=3, rotate_bytes=1 << 30):
+    """matmul_q8 (runq.c:142-159) on the config-2 shapes in GB/s of the
+    config-2 algorithmic bytes: group 32 through the reference's own function
+    (compiled runq.c), group 64 through the C port (oracle.c orc_matmul_q8),
+    since runq fixes its group at QBLOCK = 32.  Each timed pass calls the
+    function once on each of n distinct weight copies, n * (weight + scale
+    bytes) >= rotate_bytes (1 GiB, well above the host's last-level cache),
+    so every call streams its weights from DRAM; the figure is the median over
+    `reps` passes of the mean call time."""
     sys.path.insert(0, os.path.join(REPO, "oracle"))
     import oracle_py as O
     rng = np.random.default_rng(5)
+    # one arena of weight bytes, filled by tiling 64 MiB of random bytes
+    arena = np.empty(rotate_bytes + (140 << 20), dtype=np.uint8)
+    tile = rng.integers(0, 256, 64 << 20, dtype=np.uint8)
+    for o in range(0, arena.size, tile.size):
+        n = min(tile.size, arena.size - o)
+        arena[o:o + n] = tile[:n]
+    del tile
     out = {}
     for rows, cols in C2_SHAPES:
-        w = rng.integers(0, 256, rows * cols, dtype=np.uint8)
         x = rng.standard_normal(cols).astype(np.float32)
         res = {}
         for group, kind in ((32, "reference"), (64, "port")):
-            ws = rng.random(rows * (cols // group), dtype=np.float32) * np.float32(1e-3)
+            if kind == "reference" and not O.ref_available():
+                continue
+            wb = rows * cols
+            nsc = rows * (cols // group)
+            ncopy = -(-rotate_bytes // (wb + 4 * nsc))
+            wcopies = [arena[(k * wb) % (arena.size - wb):][:wb] for k in range(ncopy)]
+            scopies = [(rng.random(nsc, dtype=np.float32) * np.float32(1e-3)) for _ in range(ncopy)]
             xq, xs, xt = O.quantize_act(x, group)
             if kind == "reference":
-                if not O.ref_available():
-                    continue
-                fn = lambda: O.ref_matmul_q8(xq, xs, xt, w, ws, rows, cols)  # noqa: E731
+                def fn(k):
+                    return O.ref_matmul_q8(xq, xs, xt, wcopies[k], scopies[k], rows, cols)
             else:
-                fn = lambda: O.matmul(8, xq, xs, xt, w, ws, rows, cols, group, want_dots=False)  # noqa: E731
-            fn()
-            fn()
+                def fn(k):
+                    return O.matmul(8, xq, xs, xt, wcopies[k], scopies[k], rows, cols, group, want_dots=False)
+            for k in range(ncopy):   # untimed pass: page-in
+                fn(k)
             ts = []
             for _ in range(reps):
                 t = time.perf_counter()
-                fn()
-                ts.append(time.perf_counter() - t)
+                for k in range(ncopy):
+                    fn(k)
+                ts.append((time.perf_counter() - t) / ncopy)
             t = float(np.median(ts))
             b = gemv_bytes(rows, cols, 8, group)
-            res[f"G{group}"] = {"kind": kind, "ms": round(t * 1e3, 3), "GB/s": round(b / t / 1e9, 1)}
+            res[f"G{group}"] = {"kind": kind, "ms": round(t * 1e3, 3), "GB/s": round(b / t / 1e9, 1),
+                                "weight_copies": ncopy}
+            del wcopies, scopies
         out[f"{rows}x{cols}"] = res
+    del arena
     return out
 
 
@@ -312,7 +332,8 @@ def main():
     ap.add_argument("--kv8-steps", type=int, default=64,
                     help="greedy steps timed again with the int8 KV cache engine (0: skip)")
     ap.add_argument("--decode-only", action="store_true",
-                    help="the decode alone: no microbenchmarks, no int8-KV decode, no CPU legs")
+                    help="the decode and its own GEMV kernels alone: no microbenchmarks of other "
+                         "kernel forms, no int8-KV decode, no CPU legs")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="first run a 256 MiB device copy (x4): a kernel of known traffic for scaling "
                          "rocprofv3 FETCH_SIZE / WRITE_SIZE readings")
@@ -400,22 +421,23 @@ def main():
     kinds = [("qkv", abi.L2Q_GEMV_QKV, d + 2 * kv, d, L), ("wo", abi.L2Q_GEMV_WO, d, d, L),
              ("w13", abi.L2Q_GEMV_W13, 2 * h, d, L), ("w2", abi.L2Q_GEMV_W2, d, h, L),
              ("wcls", abi.L2Q_GEMV_CLASSIFIER, cfg.vocab_size, d, 1)]
-    decode_gemv = None
-    if not args.decode_only:
-        decode_gemv = {}
-        tot_b = tot_us = 0.0
-        for name, kind, r, c, per_step in kinds:
-            n = 4 * L if per_step > 1 else 32
-            us = eng.time_gemv(kind, n) * 1e3 / n
-            b = gemv_bytes(r, c, 4, group)
-            decode_gemv[name] = {"rows": r, "cols": c, "us": round(us, 3), "bytes": b,
-                                 "GB/s": round(b / us / 1e3, 1), "frac": round(b / us / 1e3 / HBM_PEAK_GBS, 4),
-                                 "per_step": per_step, "launches": n}
-            tot_b += per_step * b
-            tot_us += per_step * us
-        decode_gemv["aggregate"] = {"bytes_per_step": int(tot_b), "us_per_step": round(tot_us, 1),
-                                    "GB/s": round(tot_b / tot_us / 1e3, 1),
-                                    "frac": round(tot_b / tot_us / 1e3 / HBM_PEAK_GBS, 4)}
+    # each kernel launched alone n times in a row by the engine with the
+    # decode's arguments, rotating over the 32 layers' weights (>= 1 GiB for
+    # the layer kinds); HIP events around the run
+    decode_gemv = {}
+    tot_b = tot_us = 0.0
+    for name, kind, r, c, per_step in kinds:
+        n = 4 * L if per_step > 1 else 32
+        us = eng.time_gemv(kind, n) * 1e3 / n
+        b = gemv_bytes(r, c, 4, group)
+        decode_gemv[name] = {"rows": r, "cols": c, "us": round(us, 3), "bytes": b,
+                             "GB/s": round(b / us / 1e3, 1), "frac": round(b / us / 1e3 / HBM_PEAK_GBS, 4),
+                             "per_step": per_step, "launches": n}
+        tot_b += per_step * b
+        tot_us += per_step * us
+    decode_gemv["aggregate"] = {"bytes_per_step": int(tot_b), "us_per_step": round(tot_us, 1),
+                                "GB/s": round(tot_b / tot_us / 1e3, 1),
+                                "frac": round(tot_b / tot_us / 1e3 / HBM_PEAK_GBS, 4)}
     eng.close()
 
     ms_per_step = elapsed * 1e3 / args.steps
@@ -470,7 +492,7 @@ def main():
                     "frac": dom["frac"], "traffic": traffic,
                     "kernel": "k_gemv<4,64,2,2,2,2>: the decode's w1|w3 GEMV, 22016 x 4096, RMSNorm + Q8 "
                               "prologue, SwiGLU epilogue, launched by the engine with the step's arguments "
-                              "over the 32 layers' weights",
+                              "over the 32 layers' weights (1.6 GB), back to back",
                     "bytes_per_launch": dom["bytes"], "mean_us": dom["us"]}
 
     line = {

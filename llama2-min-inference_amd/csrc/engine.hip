@@ -737,25 +737,31 @@ int l2q_engine_forward_debug(l2q_engine* e, int token, int pos, float* x_layers,
     return step_check(e);
 }
 
-int l2q_engine_time_steps(l2q_engine* e, const int* tokens, int pos0, int n_steps, double* elapsed_ms) {
-    if (!e || !tokens || !elapsed_ms || n_steps <= 0) { set_error("engine: bad timing arguments"); return L2Q_ERR_ARG; }
-    for (int i = 0; i < n_steps; i++) {
-        int rc = check_step(e, tokens[i], pos0 + i);
-        if (rc) return rc;
-    }
+// Pinned (token, pos) slots for n steps enqueued before any completes.
+int ensure_meta_slots(l2q_engine* e, int n_steps) {
     if (e->h_meta_slots < n_steps) {
         HIPCHK(hipHostFree(e->h_meta), "hipHostFree");
         e->h_meta = nullptr;
         HIPCHK(hipHostMalloc((void**)&e->h_meta, 2 * sizeof(int) * n_steps, hipHostMallocDefault), "hipHostMalloc");
         e->h_meta_slots = n_steps;
     }
-    HIPCHK(hipEventRecord(e->ev0, e->stream), "hipEventRecord");
+    return L2Q_OK;
+}
+
+int l2q_engine_time_steps(l2q_engine* e, const int* tokens, int pos0, int n_steps, double* elapsed_ms) {
+    if (!e || !tokens || !elapsed_ms || n_steps <= 0) { set_error("engine: bad timing arguments"); return L2Q_ERR_ARG; }
     for (int i = 0; i < n_steps; i++) {
-        int rc = launch_step(e, tokens[i], pos0 + i, step_graph(e, false, pos0 + i), i);
+        int rc = check_step(e, tokens[i], pos0 + i);
         if (rc) return rc;
     }
+    int rc = ensure_meta_slots(e, n_steps);
+    if (rc) return rc;
+    HIPCHK(hipEventRecord(e->ev0, e->stream), "hipEventRecord");
+    for (int i = 0; i < n_steps; i++) {
+        if ((rc = launch_step(e, tokens[i], pos0 + i, step_graph(e, false, pos0 + i), i))) return rc;
+    }
     HIPCHK(hipEventRecord(e->ev1, e->stream), "hipEventRecord");
-    int rc = copy_step_err(e);
+    rc = copy_step_err(e);
     if (rc) return rc;
     HIPCHK(hipEventSynchronize(e->ev1), "hipEventSynchronize");
     HIPCHK(hipStreamSynchronize(e->stream), "hipStreamSynchronize");
