@@ -116,7 +116,9 @@ def time_attention(torch, abi, host, ctx, mode, reps=50, n_heads=32, hs=128, max
     (32 heads x 128, cache of 4096 positions): mode
     "exact" (fp32 cache, the reference's order), "split" (fp32 cache,
     split-context, the config's 1e-5 tolerance) or "int8" (int8 cache); and
-    its algorithmic bytes (K and V read, q read, output written)."""
+    its algorithmic bytes (K and V read, q read, output written).  Mode
+    "split1" is the engine's tolerance-mode form (L2Q_ATTN_SPLIT_CONTEXT:
+    one kernel, the engine's K layout)."""
     kv8 = mode == "int8"
     g = torch.Generator(device="cuda")
     g.manual_seed(ctx)
@@ -134,10 +136,12 @@ def time_attention(torch, abi, host, ctx, mode, reps=50, n_heads=32, hs=128, max
         k = torch.randn(n_heads * max_t * hs, device="cuda", generator=g)
         v = torch.randn(n_heads * max_t * hs, device="cuda", generator=g)
         args = (q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr())
-        fn, nbytes = "l2q_attention_ex" if mode == "exact" else "l2q_attention_split", 2 * ctx * n_heads * hs * 4
+        fn = "l2q_attention_split" if mode == "split" else "l2q_attention_ex"
+        nbytes = 2 * ctx * n_heads * hs * 4
     nbytes += 2 * n_heads * hs * 4
-    # exact: the engine's K layout and choice of kernels
-    extra = (abi.L2Q_ATTN_K_INTERLEAVED,) if mode == "exact" else ()
+    # exact, split1: the engine's K layout (and, exact, its choice of kernels)
+    extra = {"exact": (abi.L2Q_ATTN_K_INTERLEAVED,),
+             "split1": (abi.L2Q_ATTN_K_INTERLEAVED | abi.L2Q_ATTN_SPLIT_CONTEXT,)}.get(mode, ())
 
     def launch():
         abi.call(fn, *args, ctx - 1, n_heads, n_heads, hs, max_t, *extra, torch.cuda.current_stream().cuda_stream)
@@ -321,6 +325,31 @@ def cpu_baseline(seconds_budget=20.0):
                       f"checkpoint synthesis {t_synth:.1f}s not timed"}
 
 
+LONG_PROMPT = 3000   # prompt positions before the long-context decode figures
+
+
+def decode_rate(torch, Engine, ck, prompt, warmup, steps, **options):
+    """Greedy decode of an engine built with `options`: the prompt prefilled,
+    `warmup` untimed steps, then `steps` timed steps through the captured
+    graph with the device argmax (host loop)."""
+    e = Engine(ck, max_steps=len(prompt) + warmup + steps, **options)
+    e.prefill(prompt[:-1], 0, logits=False)
+    tok, p = prompt[-1], len(prompt) - 1
+    for _ in range(warmup):
+        tok = e.forward_argmax(tok, p)
+        p += 1
+    torch.cuda.synchronize()
+    t = time.perf_counter()
+    for _ in range(steps):
+        tok = e.forward_argmax(tok, p)
+        p += 1
+    torch.cuda.synchronize()
+    el = time.perf_counter() - t
+    e.close()
+    return {"tok_s": round(steps / el, 2), "ms_per_step": round(el * 1e3 / steps, 4), "steps": steps,
+            "positions": [p - steps, p - 1]}
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -363,25 +392,23 @@ def main():
     max_steps = args.prompt + args.warmup + args.steps
     prompt = [int(v) for v in host.uniform_ints(args.prompt, 2024, 100, 3, cfg.vocab_size)]
 
-    # the same decode with the int8 KV cache (a secondary figure)
-    kv8 = None
+    # secondary figures: the same greedy decode with the int8 KV cache and
+    # with the tolerance-mode attention, at the bench window and after a
+    # long prompt (a context of ~3000 positions)
+    kv8 = decode_modes = None
     if args.kv8_steps > 0 and not args.decode_only:
-        e8 = Engine(ck, max_steps=args.prompt + args.warmup + args.kv8_steps, kv8=True)
-        e8.prefill(prompt[:-1], 0, logits=False)
-        tok8, p8 = prompt[-1], args.prompt - 1
-        for _ in range(args.warmup):
-            tok8 = e8.forward_argmax(tok8, p8)
-            p8 += 1
-        torch.cuda.synchronize()
-        t8 = time.perf_counter()
-        for _ in range(args.kv8_steps):
-            tok8 = e8.forward_argmax(tok8, p8)
-            p8 += 1
-        torch.cuda.synchronize()
-        el8 = time.perf_counter() - t8
-        e8.close()
-        kv8 = {"tok_s": round(args.kv8_steps / el8, 2), "ms_per_step": round(el8 * 1e3 / args.kv8_steps, 4),
-               "steps": args.kv8_steps, "positions": [p8 - args.kv8_steps, p8 - 1]}
+        n2 = args.kv8_steps
+        kv8 = decode_rate(torch, Engine, ck, prompt, args.warmup, n2, kv8=True)
+        long_prompt = [int(v) for v in host.uniform_ints(LONG_PROMPT, 2025, 100, 3, cfg.vocab_size)]
+        decode_modes = {
+            "note": "tok/s of greedy decode through the captured graph (device argmax), per engine option; "
+                    "attn_split = L2Q_ENGINE_ATTN_SPLIT (split-context attention, equal to the exact order up "
+                    "to rounding), kv8 = L2Q_ENGINE_KV_INT8",
+            "attn_split": decode_rate(torch, Engine, ck, prompt, args.warmup, n2, attn_split=True),
+            "long_context": {name: decode_rate(torch, Engine, ck, long_prompt, args.warmup, n2, **kw)
+                             for name, kw in (("exact", {}), ("attn_split", {"attn_split": True}),
+                                              ("kv8", {"kv8": True}))},
+        }
 
     eng = Engine(ck, max_steps=max_steps)
     del ck
@@ -459,7 +486,7 @@ def main():
         # the exact order and split over the context, int8 cache
         attention = {}
         for ctx in (256, 1024, 2048, 4096):
-            for name in ("exact", "split", "int8"):
+            for name in ("exact", "split", "split1", "int8"):
                 ms, nbytes = time_attention(torch, abi, host, ctx, name)
                 attention[f"{name}_ctx{ctx}"] = {"us": round(ms * 1e3, 2), "bytes": nbytes,
                                                  "GB/s": round(nbytes / ms / 1e6, 1)}
@@ -528,6 +555,7 @@ def main():
                     "note": "batched prefill of the forced prompt positions (int8 MFMA GEMMs, host-timed, "
                             "includes the per-chunk token upload)"},
         "kv8_decode": kv8,
+        "decode_modes": decode_modes,
         "cpu_reference": cpu_ref,
         "synth_seconds": round(t_synth, 1),
     }

@@ -121,6 +121,17 @@ int l2q_engine_prefill(l2q_engine* e, const int* tokens, int n, int pos0,
                                   Opt-in: slower than the graph on MI355X
                                   today.  No counterpart in the reference. */
 
+#define L2Q_ENGINE_ATTN_SPLIT 4   /* tolerance mode: decode attention split over
+                                  the context in one kernel (per-split softmax
+                                  partials merged in split order), with the
+                                  fp32 cache; equal to the reference's
+                                  attention up to rounding (relative error
+                                  ~1e-6), not bit for bit.  The default is the
+                                  reference's exact order (runq.c:367-391).
+                                  head_size 48, 64 or 128; not with
+                                  L2Q_ENGINE_KV_INT8.  No counterpart in the
+                                  reference. */
+
 /* l2q_engine_create with option flags (0 gives l2q_engine_create). */
 int l2q_engine_create_ex(const l2q_config* cfg, const void* weights,
                          size_t weights_bytes, int wbits, int group,
@@ -257,10 +268,15 @@ int l2q_attention(const float* q, const float* kcache, const float* vcache,
  * L2Q_ATTN_ONE_KERNEL / L2Q_ATTN_TWO_KERNELS force the single-kernel form
  * (head sizes 48, 64, 128) or the scores + softmax/p*V pair; by default the
  * single kernel serves contexts up to a measured threshold.  Every form
- * gives the same bits. */
+ * gives the same bits.  L2Q_ATTN_SPLIT_CONTEXT instead runs the engine's
+ * tolerance-mode form (L2Q_ENGINE_ATTN_SPLIT: the context split over about
+ * two workgroups per CU in one kernel, head sizes 48, 64, 128), equal to
+ * the exact result up to rounding; its partials and per-head counters live
+ * in per-GPU library buffers, so calls that overlap on one GPU race. */
 #define L2Q_ATTN_K_INTERLEAVED 1
 #define L2Q_ATTN_ONE_KERNEL 2
 #define L2Q_ATTN_TWO_KERNELS 4
+#define L2Q_ATTN_SPLIT_CONTEXT 8
 int l2q_attention_ex(const float* q, const float* kcache, const float* vcache,
                      float* out, int pos, int n_heads, int n_kv_heads,
                      int head_size, int max_t, int flags, void* stream);

@@ -78,6 +78,11 @@ struct l2q_engine {
     unsigned* sync = nullptr;   // grp | top | rel | err | epoch (StepSync)
     size_t sync_bytes = 0;
     float* dbg = nullptr;       // [L+1][d]: the residual stream of forward_debug
+    // L2Q_ENGINE_ATTN_SPLIT: the one-kernel split-context attention's
+    // partials [n_heads][aS][hs + 2] and per-head counters (left zeroed)
+    float* apart = nullptr;
+    unsigned* acnt = nullptr;
+    int aS = 0;
     int* h_meta = nullptr;   // pinned {token, pos} slots
     int h_meta_slots = 0;
     int* h_am = nullptr;     // pinned argmax result, then the step kernel's error word
@@ -217,6 +222,9 @@ int enqueue_step(l2q_engine* e, hipStream_t st, float* dbg_x, float* dbg_tmp, bo
             // append the staged k, v rows and attend, in one kernel
             rc = launch_attention_kv8(e->q, e->k8 + co, e->v8 + co, e->ks + so, e->vs + so, e->att, e->scores,
                                       e->meta, 0, c.n_heads, c.n_kv_heads, e->hs, e->max_t, st, e->kvf, e->kvf + kv);
+        } else if (e->flags & L2Q_ENGINE_ATTN_SPLIT) {
+            rc = launch_attention_flash(e->q, kc, vc, e->att, e->apart, e->acnt, e->aS, e->meta, 0, c.n_heads,
+                                        c.n_kv_heads, e->hs, e->max_t, 1, st);
         } else {
             rc = launch_attention_exact(e->q, kc, vc, e->att, e->scores, e->S, e->meta, 0, c.n_heads,
                                         c.n_kv_heads, e->hs, e->max_t, st, 1, 0, fused ? 1 : 0, 1);
@@ -245,7 +253,9 @@ int enqueue_step(l2q_engine* e, hipStream_t st, float* dbg_x, float* dbg_tmp, bo
 int step_setup(l2q_engine* e, int ncu) {
     const l2q_config& c = e->cfg;
     e->step = false;
-    if (!(e->flags & L2Q_ENGINE_STEP_KERNEL) || (e->flags & L2Q_ENGINE_KV_INT8) || ncu <= 0 || ncu % 8) return L2Q_OK;
+    if (!(e->flags & L2Q_ENGINE_STEP_KERNEL) || (e->flags & (L2Q_ENGINE_KV_INT8 | L2Q_ENGINE_ATTN_SPLIT)) || ncu <= 0 ||
+        ncu % 8)
+        return L2Q_OK;
     if (e->wbits != 4 || e->G != 64 || !step_shape_ok(c.dim, c.hidden_dim, e->hs)) return L2Q_OK;
     if (e->max_t > attention_fused_max()) return L2Q_OK;
     // row pairs per workgroup within the fold areas; staged outputs per wave
@@ -449,6 +459,10 @@ int build(l2q_engine* e, const void* weights, size_t weights_bytes) {
     if (hipDeviceGetAttribute(&ncu, hipDeviceAttributeMultiprocessorCount, e->device) != hipSuccess || ncu < 8) ncu = 0;
     e->sync_bytes = (size_t)(8 * 16 + 16 + (size_t)(ncu > 0 ? ncu : 8) * 16 + 16 + 16) * sizeof(unsigned);
     const size_t o_sync = sa.take(e->sync_bytes), o_dbg = sa.take((L + 1) * d * 4);
+    const bool asplit = e->flags & L2Q_ENGINE_ATTN_SPLIT;
+    e->aS = asplit ? attention_flash_splits(c.n_heads, e->max_t, ncu) : 0;
+    const size_t o_apart = sa.take(asplit ? attention_flash_part_floats(c.n_heads, e->aS, e->hs) * 4 : 0);
+    const size_t o_acnt = sa.take(asplit ? (size_t)c.n_heads * sizeof(unsigned) : 0);
     e->sbytes = align_up(sa.used, 256);
     HIPCHK(hipMalloc(&e->sarena, e->sbytes), "hipMalloc(state)");
     char* S_ = e->sarena;
@@ -462,6 +476,7 @@ int build(l2q_engine* e, const void* weights, size_t weights_bytes) {
     e->meta = (int*)(S_ + o_meta); e->am = (int*)(S_ + o_am);
     e->tout = (float*)(S_ + o_tout); e->tx = (float*)(S_ + o_tx); e->tkv = (float*)(S_ + o_tkv);
     e->sync = (unsigned*)(S_ + o_sync); e->dbg = (float*)(S_ + o_dbg);
+    e->apart = (float*)(S_ + o_apart); e->acnt = (unsigned*)(S_ + o_acnt);
     // zero-fill the state (outside any graph) so unused cache rows are defined
     HIPCHK(hipMemsetAsync(e->sarena, 0, e->sbytes, e->stream), "hipMemset(state)");
 
@@ -477,8 +492,9 @@ int build(l2q_engine* e, const void* weights, size_t weights_bytes) {
     HIPCHK(hipEventCreate(&e->ev0), "hipEventCreate");
     HIPCHK(hipEventCreate(&e->ev1), "hipEventCreate");
     // short contexts: one-kernel attention where the head size has it
-    const bool fused = e->step || (attention_fused_ok(e->hs) && !(e->flags & L2Q_ENGINE_KV_INT8));
-    const bool need_long = !e->step && (!fused || e->max_t > attention_fused_max());
+    // (the split-context attention serves every position in one graph)
+    const bool fused = e->step || asplit || (attention_fused_ok(e->hs) && !(e->flags & L2Q_ENGINE_KV_INT8));
+    const bool need_long = !e->step && !asplit && (!fused || e->max_t > attention_fused_max());
     for (int a = 0; a < 2; a++) {
         if (fused && (rc = capture(e, a, true, &e->graph[a][0], &e->exec[a][0]))) return rc;
         if (need_long && (rc = capture(e, a, false, &e->graph[a][1], &e->exec[a][1]))) return rc;
@@ -659,9 +675,11 @@ int l2q_engine_create_ex(const l2q_config* cfg, const void* weights, size_t weig
         return L2Q_ERR_ARG;
     }
     const int steps = max_steps <= 0 || max_steps > c.seq_len ? c.seq_len : max_steps;
-    if ((flags & ~(L2Q_ENGINE_KV_INT8 | L2Q_ENGINE_STEP_KERNEL)) ||
-        ((flags & L2Q_ENGINE_KV_INT8) && !kv8_shape_ok(c.n_heads, c.n_kv_heads, hs, steps))) {
-        set_error("engine: unsupported flags %d for this shape (int8 KV needs head_size %% 16 == 0, <= 8192 steps)",
+    if ((flags & ~(L2Q_ENGINE_KV_INT8 | L2Q_ENGINE_STEP_KERNEL | L2Q_ENGINE_ATTN_SPLIT)) ||
+        ((flags & L2Q_ENGINE_KV_INT8) && !kv8_shape_ok(c.n_heads, c.n_kv_heads, hs, steps)) ||
+        ((flags & L2Q_ENGINE_ATTN_SPLIT) && ((flags & L2Q_ENGINE_KV_INT8) || !attention_flash_ok(hs)))) {
+        set_error("engine: unsupported flags %d for this shape (int8 KV needs head_size %% 16 == 0, <= 8192 steps; "
+                  "the split-context attention needs the fp32 cache and head_size 48, 64 or 128)",
                   flags);
         return L2Q_ERR_ARG;
     }

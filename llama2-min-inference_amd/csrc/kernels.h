@@ -988,6 +988,213 @@ __global__ __launch_bounds__(256) void k_attn_combine(const float* __restrict__ 
 }
 
 // ---------------------------------------------------------------------------
+// Split-context single-query attention in ONE kernel (the engine's
+// tolerance mode; runq.c:367-391 + softmax :307-318 up to rounding).
+// Workgroup (head h, split s) of kFlThreads threads covers positions
+// [s*C, min((s+1)*C, n)), C = ceil(n/S) <= kFlMaxC, n = pos + 1:
+//   scores  blocks of 64 positions: wave w forms the dot over chunks
+//           [w*HS/16, (w+1)*HS/16) of q.k for position lane (two FMA chains),
+//           the four wave partials are added in LDS ((p0 + p1) + (p2 + p3))
+//           and scaled by 1/sqrtf(HS); K in either cache layout (k_index);
+//   softmax m = max s_t, e_t = expf(s_t - m), l = sum e_t (wave sums, then
+//           (l0 + l1) + (l2 + l3));
+//   p*V     thread (row slice r of 8, float4 column c) accumulates e_t v_t
+//           over t = r, r + 8, ...; the 8 slices are added in order;
+//   merge   the partial (m, l, o[HS]) goes to part[h][s] through agent-scope
+//           stores; once they are acknowledged the workgroup arrives on the
+//           head's counter (agent-scope atomic), and the one whose arrival
+//           is the S-th reads the head's S partials with agent-scope loads,
+//           merges them in split order, out = sum_s w_s o_s / sum_s w_s l_s
+//           with w_s = expf(m_s - M), and resets the counter for the next
+//           launch.  (Release / acquire fences would write back and
+//           invalidate the whole L2 once per workgroup: measured 2x slower.)
+// Every workgroup arrives exactly once (empty splits too), and no
+// workgroup waits on another, so the kernel always drains.
+constexpr int kFlThreads = 256;
+constexpr int kFlBlock = 64;     // positions per score block (one per lane)
+constexpr int kFlMaxC = 256;     // positions per workgroup
+constexpr int kFlSlices = kFlThreads / 32;
+constexpr int kFlMaxSplits = 64;
+template <int HS, int KIL>
+__global__ __launch_bounds__(kFlThreads) void k_attn_flash(
+    const float* __restrict__ q, const float* __restrict__ kcache, const float* __restrict__ vcache,
+    float* __restrict__ out, float* __restrict__ part, unsigned* __restrict__ cnt, const int* __restrict__ meta,
+    int pos_arg, int kv_mul, int max_t) {
+    static_assert(HS == 48 || HS == 64 || HS == 128, "head size");
+    constexpr int F4 = HS / 4;           // float4 chunks per row
+    constexpr int CW = F4 / 4;           // chunks per wave in the scores
+    constexpr int NV = kFlBlock / kFlSlices;   // V rows per thread per block
+    __shared__ float4 qs[F4];
+    __shared__ float sp[4][kFlBlock];
+    __shared__ float sc[kFlMaxC];
+    __shared__ float4 po[kFlSlices][32];
+    __shared__ float red[8];
+    __shared__ float wsm[2 * kFlMaxSplits];   // merge: w_s, then w_s * l_s
+    __shared__ float mrg[kFlMaxSplits * (HS + 2)];   // merge: the head's partials
+    __shared__ int is_last;
+    const int h = blockIdx.x, s = blockIdx.y, S = gridDim.y;
+    const int tid = threadIdx.x, lane = tid & (L2Q_WAVE - 1), wv = tid / L2Q_WAVE;
+    const int n = meta_pos(meta, pos_arg) + 1;
+    const int C = (n + S - 1) / S;
+    const int t0 = min(s * C, n), t1 = min(n, t0 + C);
+    const int m_n = t1 - t0;
+    const int kvh = h / kv_mul;
+    const float4* k4 = reinterpret_cast<const float4*>(kcache);
+    const float4* v4 = reinterpret_cast<const float4*>(vcache) + (size_t)kvh * max_t * F4;
+    auto kaddr = [&](int t, int c) {
+        return KIL ? k4 + ((size_t)(kvh * F4 + c) * max_t + t) : k4 + ((size_t)kvh * max_t + t) * F4 + c;
+    };
+    const int r = tid >> 5, c4 = tid & 31;   // p*V: row slice, float4 column (c4 < F4 active)
+    const int tl = max(t1 - 1, 0);           // clamped positions load a valid row, never used
+
+    // loads in the order they are needed: q, the first block's K, its V
+    if (tid < F4) qs[tid] = reinterpret_cast<const float4*>(q + (size_t)h * HS)[tid];
+    float4 kr[CW], vr[NV];
+    auto load_k = [&](int b) {
+        const int t = min(t0 + kFlBlock * b + lane, tl);
+#pragma unroll
+        for (int c = 0; c < CW; c++) kr[c] = *kaddr(t, wv * CW + c);
+    };
+    auto load_v = [&](int b) {
+#pragma unroll
+        for (int k = 0; k < NV; k++)
+            vr[k] = c4 < F4 ? v4[(size_t)min(t0 + kFlBlock * b + r + kFlSlices * k, tl) * F4 + c4]
+                            : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    };
+    const int nblk = (m_n + kFlBlock - 1) / kFlBlock;
+    if (nblk > 0) {
+        load_k(0);
+        load_v(0);
+    }
+    __syncthreads();   // qs
+    const float rs = sqrtf((float)HS);
+    for (int b = 0; b < nblk; b++) {
+        if (b > 0) load_k(b);
+        float a0 = 0.0f, a1 = 0.0f;
+#pragma unroll
+        for (int c = 0; c < CW; c++) {
+            const float4 qv = qs[wv * CW + c];
+            a0 = __builtin_fmaf(qv.x, kr[c].x, a0);
+            a1 = __builtin_fmaf(qv.y, kr[c].y, a1);
+            a0 = __builtin_fmaf(qv.z, kr[c].z, a0);
+            a1 = __builtin_fmaf(qv.w, kr[c].w, a1);
+        }
+        sp[wv][lane] = a0 + a1;
+        __syncthreads();
+        if (tid < kFlBlock) {
+            const int j = kFlBlock * b + tid;
+            if (j < m_n) sc[j] = ((sp[0][tid] + sp[1][tid]) + (sp[2][tid] + sp[3][tid])) / rs;
+        }
+        __syncthreads();
+    }
+    float m = -INFINITY;
+    for (int j = tid; j < m_n; j += kFlThreads) m = fmaxf(m, sc[j]);
+    m = wave_max(m);
+    if (lane == 0) red[wv] = m;
+    __syncthreads();
+    m = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+    float l = 0.0f;
+    for (int j = tid; j < m_n; j += kFlThreads) {
+        const float e = expf(sc[j] - m);
+        sc[j] = e;
+        l += e;
+    }
+    l = wave_sum(l);
+    if (lane == 0) red[4 + wv] = l;
+    __syncthreads();   // sc holds e_t; red[4..8) the wave sums
+    l = (red[4] + red[5]) + (red[6] + red[7]);
+    float4 o = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    for (int b = 0; b < nblk; b++) {
+        if (b > 0) load_v(b);
+#pragma unroll
+        for (int k = 0; k < NV; k++) {
+            const int j = kFlBlock * b + r + kFlSlices * k;
+            if (j < m_n) {
+                const float e = sc[j];
+                o.x = __builtin_fmaf(e, vr[k].x, o.x);
+                o.y = __builtin_fmaf(e, vr[k].y, o.y);
+                o.z = __builtin_fmaf(e, vr[k].z, o.z);
+                o.w = __builtin_fmaf(e, vr[k].w, o.w);
+            }
+        }
+    }
+    po[r][c4] = o;
+    __syncthreads();
+    // the partial, written by wave 0 with agent-scope stores (written
+    // through to the device-coherent level, no L2 writeback of the whole
+    // cache as a release fence would do); once they are acknowledged, the
+    // arrival on the head's counter
+    float* pp = part + ((size_t)h * S + s) * (HS + 2);
+    auto put = [](float* a, float v) { __hip_atomic_store(a, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); };
+    auto get = [](const float* a) {
+        return __hip_atomic_load(const_cast<float*>(a), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    };
+    if (tid < F4) {
+        float4 acc = po[0][tid];
+#pragma unroll
+        for (int k = 1; k < kFlSlices; k++) {
+            const float4 x = po[k][tid];
+            acc.x += x.x; acc.y += x.y; acc.z += x.z; acc.w += x.w;
+        }
+        put(pp + 4 * tid, acc.x);
+        put(pp + 4 * tid + 1, acc.y);
+        put(pp + 4 * tid + 2, acc.z);
+        put(pp + 4 * tid + 3, acc.w);
+    }
+    if (tid == 0) {
+        put(pp + HS, m_n > 0 ? m : -INFINITY);
+        put(pp + HS + 1, m_n > 0 ? l : 0.0f);
+    }
+    if (wv == 0) {
+        __atomic_signal_fence(__ATOMIC_SEQ_CST);
+        __builtin_amdgcn_s_waitcnt(0x0F70);   // vmcnt(0): this wave's partial stores are acknowledged
+        __atomic_signal_fence(__ATOMIC_SEQ_CST);
+        if (tid == 0)
+            is_last = __hip_atomic_fetch_add(cnt + h, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+                      (unsigned)(S - 1);
+    }
+    __syncthreads();
+    if (!is_last) return;
+    // merge the head's S partials in split order: staged into LDS by
+    // batches of independent agent-scope loads (the other workgroups'
+    // partials, read past every non-coherent cache level)
+    const float* ph = part + (size_t)h * S * (HS + 2);
+    const int total = S * (HS + 2);
+    for (int e0 = 0; e0 < total; e0 += 8 * kFlThreads) {
+        float v[8];
+#pragma unroll
+        for (int k = 0; k < 8; k++) {
+            const int e = e0 + k * kFlThreads + tid;
+            v[k] = e < total ? get(ph + e) : 0.0f;
+        }
+#pragma unroll
+        for (int k = 0; k < 8; k++) {
+            const int e = e0 + k * kFlThreads + tid;
+            if (e < total) mrg[e] = v[k];
+        }
+    }
+    __syncthreads();
+    float M = -INFINITY;
+    for (int k = 0; k < S; k++) M = fmaxf(M, mrg[k * (HS + 2) + HS]);
+    if (tid < S) {
+        const float ms = mrg[tid * (HS + 2) + HS];
+        const float w = ms == -INFINITY ? 0.0f : expf(ms - M);
+        wsm[tid] = w;
+        wsm[kFlMaxSplits + tid] = w * mrg[tid * (HS + 2) + HS + 1];
+    }
+    __syncthreads();
+    if (tid < HS) {
+        float L = 0.0f, acc = 0.0f;
+        for (int k = 0; k < S; k++) {
+            L += wsm[kFlMaxSplits + k];
+            acc = __builtin_fmaf(wsm[k], mrg[k * (HS + 2) + tid], acc);
+        }
+        out[(size_t)h * HS + tid] = acc / L;
+    }
+    if (tid == 0) __hip_atomic_store(cnt + h, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// ---------------------------------------------------------------------------
 // Greedy argmax (runq.c:578-585: first index of the maximum).  One
 // workgroup; each thread takes float4 chunks t, t + 1024, ... (v 16-byte
 // aligned), the loads of eight chunks in flight at once, and scans its

@@ -43,6 +43,17 @@ int launch_attention_split(const float* q, const float* kcache, const float* vca
                            float* part_ml, int S, const int* meta, int pos, int n_heads, int n_kv_heads, int hs,
                            int max_t, hipStream_t st);
 
+// Split-context attention in one kernel (the engine's tolerance mode):
+// S splits per head (attention_flash_splits), partials of
+// attention_flash_part_floats floats and n_heads zeroed counters that the
+// kernel leaves zeroed; K in the layout k_il (see k_index).
+bool attention_flash_ok(int hs);
+int attention_flash_splits(int n_heads, int max_t, int ncu);
+size_t attention_flash_part_floats(int n_heads, int S, int hs);
+int launch_attention_flash(const float* q, const float* kcache, const float* vcache, float* out, float* part,
+                           unsigned* cnt, int S, const int* meta, int pos, int n_heads, int n_kv_heads, int hs,
+                           int max_t, int k_il, hipStream_t st);
+
 // Attention in the reference's exact order: `scores` is n_heads*max_t
 // floats of scratch, S the number of score workgroups per head.
 // T > 1: queries at positions pos..pos+T-1 (causal), q rows `q_stride` floats

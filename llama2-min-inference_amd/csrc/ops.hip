@@ -287,6 +287,49 @@ bool attention_exact_ok(int max_t) {
     return max_t <= kScorePer * kAttnThreads && attn_v_lds_bytes(max_t) <= 65536;
 }
 
+bool attention_flash_ok(int hs) { return hs == 48 || hs == 64 || hs == 128; }
+
+int attention_flash_splits(int n_heads, int max_t, int ncu) {
+    int S = (2 * (ncu > 0 ? ncu : 256) + n_heads - 1) / n_heads;   // about two workgroups per CU
+    const int need = (max_t + kFlMaxC - 1) / kFlMaxC;
+    if (S < need) S = need;
+    return S < 1 ? 1 : (S > kFlMaxSplits ? kFlMaxSplits : S);
+}
+
+size_t attention_flash_part_floats(int n_heads, int S, int hs) { return (size_t)n_heads * S * (hs + 2); }
+
+template <int HS>
+static int go_attn_flash(const float* q, const float* kcache, const float* vcache, float* out, float* part,
+                         unsigned* cnt, int S, const int* meta, int pos, int n_heads, int kv_mul, int max_t, int k_il,
+                         hipStream_t st) {
+    if (k_il)
+        hipLaunchKernelGGL((k_attn_flash<HS, 1>), dim3(n_heads, S), dim3(kFlThreads), 0, st, q, kcache, vcache, out,
+                           part, cnt, meta, pos, kv_mul, max_t);
+    else
+        hipLaunchKernelGGL((k_attn_flash<HS, 0>), dim3(n_heads, S), dim3(kFlThreads), 0, st, q, kcache, vcache, out,
+                           part, cnt, meta, pos, kv_mul, max_t);
+    return check_launch("attention_flash");
+}
+
+int launch_attention_flash(const float* q, const float* kcache, const float* vcache, float* out, float* part,
+                           unsigned* cnt, int S, const int* meta, int pos, int n_heads, int n_kv_heads, int hs,
+                           int max_t, int k_il, hipStream_t st) {
+    // positions a launch may cover: any of the cache's under a captured graph
+    const int nmax = meta ? max_t : pos + 1;
+    if (!attention_shape_ok(n_heads, n_kv_heads, hs) || !attention_flash_ok(hs) || S <= 0 || S > kFlMaxSplits ||
+        max_t <= 0 || (!meta && (pos < 0 || pos >= max_t)) || (nmax + S - 1) / S > kFlMaxC || !part || !cnt) {
+        set_error("attention_flash: bad shape heads=%d kv_heads=%d hs=%d S=%d pos=%d max_t=%d", n_heads, n_kv_heads,
+                  hs, S, pos, max_t);
+        return L2Q_ERR_ARG;
+    }
+    const int kv_mul = n_heads / n_kv_heads;
+    switch (hs) {
+        case 48: return go_attn_flash<48>(q, kcache, vcache, out, part, cnt, S, meta, pos, n_heads, kv_mul, max_t, k_il, st);
+        case 64: return go_attn_flash<64>(q, kcache, vcache, out, part, cnt, S, meta, pos, n_heads, kv_mul, max_t, k_il, st);
+        default: return go_attn_flash<128>(q, kcache, vcache, out, part, cnt, S, meta, pos, n_heads, kv_mul, max_t, k_il, st);
+    }
+}
+
 int launch_attention_exact(const float* q, const float* kcache, const float* vcache, float* out, float* scores,
                            int S, const int* meta, int pos, int n_heads, int n_kv_heads, int hs, int max_t,
                            hipStream_t st, int T, int q_stride, int fused, int k_il) {
@@ -598,19 +641,67 @@ int l2q_rope_kv_append(float* q, const float* k, const float* v, float* kcache, 
                                  n_kv_heads * head_size, head_size, max_t, (hipStream_t)stream);
 }
 
+// Per-device counters of the split-context attention (zeroed when
+// allocated; every launch leaves them zeroed).
+struct FlashCounters {
+    unsigned* buf = nullptr;
+    int n = 0;
+};
+static FlashCounters g_flash_cnt[64];
+static std::mutex g_flash_mu;
+
+static int flash_counters(int n, unsigned** out) {
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return hip_fail(e, "hipGetDevice");
+    if (dev < 0 || dev >= 64) { set_error("attention: device %d out of range", dev); return L2Q_ERR_ARG; }
+    std::lock_guard<std::mutex> lock(g_flash_mu);
+    FlashCounters& c = g_flash_cnt[dev];
+    if (c.n < n) {
+        if (c.buf) {
+            e = hipDeviceSynchronize();
+            if (e != hipSuccess) return hip_fail(e, "hipDeviceSynchronize");
+            (void)hipFree(c.buf);
+            c.buf = nullptr;
+            c.n = 0;
+        }
+        e = hipMalloc(&c.buf, (size_t)n * sizeof(unsigned));
+        if (e != hipSuccess) { c.buf = nullptr; return hip_fail(e, "hipMalloc(attention counters)"); }
+        e = hipMemset(c.buf, 0, (size_t)n * sizeof(unsigned));
+        if (e != hipSuccess) return hip_fail(e, "hipMemset(attention counters)");
+        c.n = n;
+    }
+    *out = c.buf;
+    return L2Q_OK;
+}
+
 int l2q_attention_ex(const float* q, const float* kcache, const float* vcache, float* out, int pos, int n_heads,
                      int n_kv_heads, int head_size, int max_t, int flags, void* stream) {
     const int one = flags & L2Q_ATTN_ONE_KERNEL, two = flags & L2Q_ATTN_TWO_KERNELS;
+    const int sc = flags & L2Q_ATTN_SPLIT_CONTEXT;
     if (!attention_shape_ok(n_heads, n_kv_heads, head_size) || pos < 0 || pos >= max_t ||
-        (flags & ~(L2Q_ATTN_K_INTERLEAVED | L2Q_ATTN_ONE_KERNEL | L2Q_ATTN_TWO_KERNELS)) || (one && two) ||
-        (one && !attention_fused_ok(head_size))) {
+        (flags & ~(L2Q_ATTN_K_INTERLEAVED | L2Q_ATTN_ONE_KERNEL | L2Q_ATTN_TWO_KERNELS | L2Q_ATTN_SPLIT_CONTEXT)) ||
+        (one && two) || (one && !attention_fused_ok(head_size)) || (sc && (one || two)) ||
+        (sc && !attention_flash_ok(head_size))) {
         set_error("attention: bad shape or flags heads=%d kv_heads=%d hs=%d pos=%d max_t=%d flags=%d", n_heads,
                   n_kv_heads, head_size, pos, max_t, flags);
         return L2Q_ERR_ARG;
     }
     float* scratch = nullptr;
-    int rc = attn_scratch((size_t)n_heads * max_t, &scratch);
-    if (rc) return rc;
+    int rc;
+    if (sc) {
+        int dev = 0, ncu = 0;
+        if (hipGetDevice(&dev) != hipSuccess ||
+            hipDeviceGetAttribute(&ncu, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
+            ncu = 0;
+        const int S = attention_flash_splits(n_heads, pos + 1, ncu);
+        unsigned* cnt = nullptr;
+        if ((rc = attn_scratch(attention_flash_part_floats(n_heads, S, head_size), &scratch))) return rc;
+        if ((rc = flash_counters(n_heads, &cnt))) return rc;
+        return launch_attention_flash(q, kcache, vcache, out, scratch, cnt, S, nullptr, pos, n_heads, n_kv_heads,
+                                      head_size, max_t, flags & L2Q_ATTN_K_INTERLEAVED ? 1 : 0, (hipStream_t)stream);
+    }
+    if ((rc = attn_scratch((size_t)n_heads * max_t, &scratch))) return rc;
     return launch_attention_exact(q, kcache, vcache, out, scratch, score_splits(pos + 1), nullptr, pos, n_heads,
                                   n_kv_heads, head_size, max_t, (hipStream_t)stream, 1, 0, one ? 1 : two ? 0 : -1,
                                   flags & L2Q_ATTN_K_INTERLEAVED ? 1 : 0);

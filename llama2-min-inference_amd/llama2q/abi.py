@@ -17,9 +17,11 @@ L2Q_ERR_NOMEM = -4
 L2Q_ERR_STATE = -5
 L2Q_ENGINE_KV_INT8 = 1
 L2Q_ENGINE_STEP_KERNEL = 2
+L2Q_ENGINE_ATTN_SPLIT = 4
 L2Q_ATTN_K_INTERLEAVED = 1
 L2Q_ATTN_ONE_KERNEL = 2
 L2Q_ATTN_TWO_KERNELS = 4
+L2Q_ATTN_SPLIT_CONTEXT = 8
 L2Q_GEMV_QKV, L2Q_GEMV_WO, L2Q_GEMV_W13, L2Q_GEMV_W2, L2Q_GEMV_CLASSIFIER = range(5)
 
 

@@ -12,17 +12,21 @@ from .host import Checkpoint
 
 
 class Engine:
-    def __init__(self, ckpt: Checkpoint, max_steps: int = 0, kv8: bool = False, step_kernel: bool = False):
+    def __init__(self, ckpt: Checkpoint, max_steps: int = 0, kv8: bool = False, step_kernel: bool = False,
+                 attn_split: bool = False):
         """kv8: int8 KV cache (L2Q_ENGINE_KV_INT8, the reference's INT8_KV build);
         step_kernel: run each step as one persistent kernel where the shape
-        allows it (L2Q_ENGINE_STEP_KERNEL; same bits as the per-op graph)."""
+        allows it (L2Q_ENGINE_STEP_KERNEL; same bits as the per-op graph);
+        attn_split: split-context decode attention, equal to the reference
+        up to rounding (L2Q_ENGINE_ATTN_SPLIT)."""
         if ckpt.header.shared_weights:
             raise ValueError("shared weights not supported")   # runq.c:247-251
         self.cfg = ckpt.cfg
         self.vocab = self.cfg.vocab_size
         w = ckpt.weights
         h = C.c_void_p()
-        flags = (abi.L2Q_ENGINE_KV_INT8 if kv8 else 0) | (abi.L2Q_ENGINE_STEP_KERNEL if step_kernel else 0)
+        flags = (abi.L2Q_ENGINE_KV_INT8 if kv8 else 0) | (abi.L2Q_ENGINE_STEP_KERNEL if step_kernel else 0) | \
+            (abi.L2Q_ENGINE_ATTN_SPLIT if attn_split else 0)
         abi.call("l2q_engine_create_ex", C.byref(self.cfg), w.ctypes.data, w.nbytes, ckpt.wbits, ckpt.group,
                  max_steps, flags, C.byref(h))
         self._h = h

@@ -342,6 +342,40 @@ def test_attention_forms_and_k_layouts(gpu_lib, torch_cuda, n_heads, n_kv, hs, m
             np.testing.assert_array_equal(out.cpu().numpy(), ref, err_msg=f"layout {layout} form {form}")
 
 
+@pytest.mark.parametrize("n_heads,n_kv,hs,max_t,ctx,scale", [
+    (32, 32, 128, 4096, 1, 1.0), (32, 32, 128, 4096, 64, 1.0), (32, 32, 128, 4096, 65, 1.0),
+    (32, 32, 128, 4096, 1024, 1.0), (32, 32, 128, 4096, 1025, 1.0), (32, 32, 128, 4096, 2049, 1.0),
+    (32, 32, 128, 4096, 4096, 1.0), (6, 6, 48, 256, 1, 1.0), (6, 6, 48, 256, 256, 1.0),
+    (8, 2, 64, 512, 300, 1.0), (32, 8, 128, 4096, 3000, 1.0),
+    (32, 32, 128, 4096, 700, 1e-30), (32, 32, 128, 4096, 700, 1e15), (32, 32, 128, 4096, 1500, 30.0),
+])
+def test_attention_split_context_tolerance(gpu_lib, torch_cuda, n_heads, n_kv, hs, max_t, ctx, scale):
+    """L2Q_ATTN_SPLIT_CONTEXT (the engine's tolerance-mode attention: the
+    context split over ~2 workgroups per CU, per-split softmax partials
+    merged in split order by the last workgroup of each head) in both K
+    layouts: within 1e-5 of the oracle's exact order (elementwise, floor at
+    the output's RMS), at contexts of one to several 64-position score blocks
+    per split, GQA, and score magnitudes from ~0 to ~1e30."""
+    t = torch_cuda
+    print(f"attention split-context heads={n_heads}/{n_kv} hs={hs} ctx={ctx} scale={scale}", flush=True)
+    pos = ctx - 1
+    sc = np.float32(scale)
+    kc = (host.gauss(n_kv * max_t * hs, ctx, 1, 1.0) * sc).astype(np.float32).reshape(n_kv, max_t, hs)
+    vc = host.gauss(n_kv * max_t * hs, ctx, 2, 1.0).reshape(n_kv, max_t, hs)
+    q = (host.gauss(n_heads * hs, ctx, 3, 1.0) * sc).astype(np.float32)
+    ref = O.attention(q, kc, vc, pos, n_heads, n_kv, hs)
+    kil = np.ascontiguousarray(kc.reshape(n_kv, max_t, hs // 4, 4).transpose(0, 2, 1, 3))
+    d_q, d_v = dev(t, q), dev(t, vc)
+    out = t.empty(n_heads * hs, dtype=t.float32, device="cuda")
+    for layout, kd in ((0, dev(t, kc)), (abi.L2Q_ATTN_K_INTERLEAVED, dev(t, kil))):
+        for rep in range(2):   # the second call finds the counters the first left zeroed
+            out.fill_(np.nan)
+            abi.call("l2q_attention_ex", d_q.data_ptr(), kd.data_ptr(), d_v.data_ptr(), out.data_ptr(), pos, n_heads,
+                     n_kv, hs, max_t, layout | abi.L2Q_ATTN_SPLIT_CONTEXT, stream(t))
+            t.cuda.synchronize()
+            assert_close(out.cpu().numpy(), ref, 1e-5, what=f"layout {layout} call {rep}")
+
+
 @pytest.mark.parametrize("scale", [1e-30, 1e-6, 30.0, 1e6, 1e15])
 @pytest.mark.parametrize("ctx", [65, 700])
 def test_attention_forms_extreme_magnitudes(gpu_lib, torch_cuda, scale, ctx):
@@ -445,4 +479,8 @@ def test_bad_shapes_raise(gpu_lib, torch_cuda):
     with pytest.raises(abi.L2QError):
         abi.call("l2q_attention_ex", p, p, p, p, 1, 4, 4, 128, 8, 6, None)     # both forms
     with pytest.raises(abi.L2QError):
-        abi.call("l2q_attention_ex", p, p, p, p, 1, 4, 4, 128, 8, 8, None)     # unknown flag
+        abi.call("l2q_attention_ex", p, p, p, p, 1, 4, 4, 128, 8, 16, None)    # unknown flag
+    with pytest.raises(abi.L2QError):
+        abi.call("l2q_attention_ex", p, p, p, p, 1, 4, 4, 128, 8, 10, None)    # split context + one kernel
+    with pytest.raises(abi.L2QError):
+        abi.call("l2q_attention_ex", p, p, p, p, 1, 4, 4, 96, 8, abi.L2Q_ATTN_SPLIT_CONTEXT, None)  # no 96 form
