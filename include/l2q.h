@@ -20,6 +20,14 @@
  * calls exit(); the runner maps a failure to the reference's fail-fast exit
  * (runq.c:258-275, v5-cuda-fused/run.cu:50-52).
  *
+ * Device scratch: l2q_attention, l2q_attention_ex, l2q_attention_split and
+ * l2q_gemm_q keep their intermediates (per-head scores, split partials,
+ * permuted activations) in one library-owned buffer per GPU, grown on
+ * demand (growing synchronizes the device).  They return before the GPU
+ * work ends, so calls from different host threads or on different streams
+ * of one GPU must not overlap: issue them from one thread on one stream.
+ * The engine owns its own buffers and is not affected.
+ *
  * Quantization conventions shared by every entry point:
  *   - a "group" is G consecutive elements of one row (G = 32 for reference
  *     files, 64 for the Llama-2-7B configurations);
