@@ -573,6 +573,188 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn_softmax_v(
 }
 
 // ---------------------------------------------------------------------------
+// Batched attention (T > 1 queries at positions pos..pos+T-1, causal), the
+// same operations in the same order as k_attn_scores + k_attn_softmax_v, so
+// every output is bit-identical to T single-query steps; three kernels that
+// share each K and V row over the queries instead of re-reading it per query.
+//
+// k_attn_scores_b: workgroup (head, 64-key tile, 32-query block): the K tile
+//   and the block's q rows are staged in LDS once; thread (key t, query group
+//   g) forms the dots of key t with queries 8g..8g+7 (eight independent
+//   chains), each in serial_dot's order (products rounded and added in index
+//   order over hs & ~7 elements, the rest fused), / sqrtf(hs); pairs above
+//   the causal diagonal are skipped.
+constexpr int kSbKeys = 64, kSbQueries = 32, kSbThreads = 256;
+constexpr int kSbPer = kSbQueries * kSbKeys / kSbThreads;   // chains per thread (8)
+__host__ __device__ constexpr size_t attn_scores_b_lds_bytes(int hs) {
+    return (size_t)(kSbKeys + kSbQueries) * (hs + 4) * sizeof(float);
+}
+__global__ __launch_bounds__(kSbThreads) void k_attn_scores_b(
+    const float* __restrict__ q, const float* __restrict__ kcache, float* __restrict__ scores, int pos0, int T,
+    int kv_mul, int n_heads, int hs, int max_t, int q_stride, int k_il) {
+#pragma clang fp contract(off)
+    extern __shared__ __attribute__((aligned(16))) float sm[];
+    const int hsp = hs + 4;
+    float* kt = sm;                      // [kSbKeys][hsp]
+    float* qs = kt + kSbKeys * hsp;      // [kSbQueries][hsp]
+    const int h = blockIdx.x, t0 = blockIdx.y * kSbKeys, q0 = blockIdx.z * kSbQueries;
+    const int tid = threadIdx.x;
+    const int nk = pos0 + T;
+    // the tile's first key is past the block's last query's position: no pair
+    if (t0 > pos0 + min(q0 + kSbQueries, T) - 1) return;
+    const int g = h / kv_mul, f4 = hs / 4;
+    const int nt = min(kSbKeys, nk - t0);
+    for (int f = tid; f < kSbKeys * f4; f += kSbThreads) {
+        int r, c4;
+        if (k_il) { c4 = f / kSbKeys; r = f - c4 * kSbKeys; }   // consecutive lanes, consecutive keys
+        else { r = f / f4; c4 = f - r * f4; }
+        const float4 v = *reinterpret_cast<const float4*>(kcache + k_index(k_il, g, t0 + min(r, nt - 1), 4 * c4, hs, max_t));
+        *reinterpret_cast<float4*>(kt + r * hsp + 4 * c4) = v;
+    }
+    for (int f = tid; f < kSbQueries * f4; f += kSbThreads) {
+        const int r = f / f4, c4 = f - r * f4;
+        const float4 v = *reinterpret_cast<const float4*>(q + (size_t)min(q0 + r, T - 1) * q_stride +
+                                                          (size_t)h * hs + 4 * c4);
+        *reinterpret_cast<float4*>(qs + r * hsp + 4 * c4) = v;
+    }
+    __syncthreads();
+    const int tl = tid % kSbKeys, qg = tid / kSbKeys;
+    const float4* k4 = reinterpret_cast<const float4*>(kt + tl * hsp);
+    float sc[kSbPer];
+#pragma unroll
+    for (int j = 0; j < kSbPer; j++) sc[j] = 0.0f;
+    const int nv = (hs & ~7) >> 2;   // float4 blocks added unfused
+    for (int c = 0; c < f4; c++) {
+        const float4 kv = k4[c];
+#pragma unroll
+        for (int j = 0; j < kSbPer; j++) {
+            const float4 qv = reinterpret_cast<const float4*>(qs + (qg * kSbPer + j) * hsp)[c];
+            if (c < nv) {
+                sc[j] = sc[j] + qv.x * kv.x;
+                sc[j] = sc[j] + qv.y * kv.y;
+                sc[j] = sc[j] + qv.z * kv.z;
+                sc[j] = sc[j] + qv.w * kv.w;
+            } else {
+                sc[j] = __builtin_fmaf(qv.x, kv.x, sc[j]);
+                sc[j] = __builtin_fmaf(qv.y, kv.y, sc[j]);
+                sc[j] = __builtin_fmaf(qv.z, kv.z, sc[j]);
+                sc[j] = __builtin_fmaf(qv.w, kv.w, sc[j]);
+            }
+        }
+    }
+    const int t = t0 + tl;
+    const float rs = sqrtf((float)hs);
+#pragma unroll
+    for (int j = 0; j < kSbPer; j++) {
+        const int qi = q0 + qg * kSbPer + j;
+        if (qi < T && t < nk && t <= pos0 + qi) scores[((size_t)qi * n_heads + h) * max_t + t] = sc[j] / rs;
+    }
+}
+
+// k_attn_softmax_b: one wave per (query, head): max, e_t = exp_runq(s_t -
+// max) into LDS, the sum of e_t in position order (one lane, serial_sum),
+// p_t = e_t / sum written over the scores (k_attn_softmax_v's softmax).
+constexpr int kSmThreads = L2Q_WAVE;
+__host__ __device__ constexpr size_t attn_softmax_b_lds_bytes(int max_t) {
+    return ((size_t)(max_t + 3) / 4 * 4 + kRingSlack + 4) * sizeof(float);
+}
+__global__ __launch_bounds__(kSmThreads) void k_attn_softmax_b(float* __restrict__ scores, int pos0, int n_heads,
+                                                               int max_t) {
+#pragma clang fp contract(off)
+    extern __shared__ __attribute__((aligned(16))) float sm[];
+    float* p = sm;                                         // [n] e_t
+    float* red = sm + (max_t + 3) / 4 * 4 + kRingSlack;    // [1] sum
+    const int qi = blockIdx.x, h = blockIdx.y, lane = threadIdx.x;
+    const int n = pos0 + qi + 1;
+    float* row = scores + ((size_t)qi * n_heads + h) * max_t;
+    float m = -INFINITY;
+    for (int t = lane; t < n; t += kSmThreads) {
+        const float v = row[t];
+        p[t] = v;
+        m = fmaxf(m, v);
+    }
+    m = group_max<L2Q_WAVE>(m);
+    for (int t = lane; t < n; t += kSmThreads) p[t] = exp_runq(p[t] - m);
+    __syncthreads();
+    if (lane == 0) red[0] = serial_sum(p, n);
+    __syncthreads();
+    const float sum = red[0];
+    for (int t = lane; t < n; t += kSmThreads) row[t] = p[t] / sum;
+}
+
+// k_attn_pv_b: workgroup (head, 16-element slice, 128-query block): thread
+// (query ql, element quad) accumulates acc_i = fma(p_t, v_t[i], acc_i) over
+// t = 0..pos+ql in position order for four elements (k_attn_softmax_v's
+// serial_pv), over 64-key chunks of V and of the block's p rows staged in
+// LDS, the next chunk's loads in flight while the current one is folded.
+constexpr int kPvKeys = 64, kPvQueries = 128, kPvThreads = 512;
+constexpr int kPvPitch = kPvKeys + 1;   // odd: the 16 queries of a wave read distinct banks
+__global__ __launch_bounds__(kPvThreads) void k_attn_pv_b(const float* __restrict__ p, const float* __restrict__ vcache,
+                                                          float* __restrict__ out, int pos0, int T, int kv_mul,
+                                                          int n_heads, int hs, int max_t) {
+    __shared__ float pt[kPvQueries * kPvPitch];
+    __shared__ float4 vt[kPvKeys][kVDims / 4];
+    const int h = blockIdx.x, d0 = blockIdx.y * kVDims, q0 = blockIdx.z * kPvQueries;
+    const int tid = threadIdx.x, ql = tid >> 2, quad = tid & 3;
+    const int width = min(kVDims, hs - d0);
+    const int qi = q0 + ql;
+    const int n = qi < T ? pos0 + qi + 1 : 0;              // keys of this thread's query
+    const int nblk = pos0 + min(q0 + kPvQueries, T);       // keys of the block's last query
+    const int nchunks = (nblk + kPvKeys - 1) / kPvKeys;
+    const float* vb = vcache + (size_t)(h / kv_mul) * max_t * hs + d0;
+    // staging: V row r (float4 column c4) by thread r*4 + c4 (< 256); p row
+    // of query r, float4 column c4, four per thread
+    constexpr int PPT = kPvQueries * kPvKeys / 4 / kPvThreads;
+    float4 rv, rp[PPT];
+    auto fetch = [&](int c) {
+        const int t0 = c * kPvKeys;
+        if (tid < kPvKeys * 4) {
+            const int r = tid >> 2, c4 = tid & 3;
+            rv = 4 * c4 < width ? *reinterpret_cast<const float4*>(vb + (size_t)min(t0 + r, nblk - 1) * hs + 4 * c4)
+                                : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        }
+#pragma unroll
+        for (int k = 0; k < PPT; k++) {
+            const int f = tid + kPvThreads * k, r = f / (kPvKeys / 4), c4 = f % (kPvKeys / 4);
+            rp[k] = *reinterpret_cast<const float4*>(p + ((size_t)min(q0 + r, T - 1) * n_heads + h) * max_t +
+                                                     min(t0 + 4 * c4, max_t - 4));
+        }
+    };
+    auto stage = [&]() {
+        if (tid < kPvKeys * 4) vt[tid >> 2][tid & 3] = rv;
+#pragma unroll
+        for (int k = 0; k < PPT; k++) {
+            const int f = tid + kPvThreads * k, r = f / (kPvKeys / 4), c4 = f % (kPvKeys / 4);
+            float* d = pt + r * kPvPitch + 4 * c4;
+            d[0] = rp[k].x; d[1] = rp[k].y; d[2] = rp[k].z; d[3] = rp[k].w;
+        }
+    };
+    float4 acc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    if (nchunks > 0) fetch(0);
+    for (int c = 0; c < nchunks; c++) {
+        stage();
+        __syncthreads();
+        if (c + 1 < nchunks) fetch(c + 1);
+        const int tn = min(kPvKeys, n - c * kPvKeys);   // this thread's keys in the chunk
+        const float* pr = pt + ql * kPvPitch;
+        for (int t = 0; t < tn; t++) {
+            const float pv = pr[t];
+            const float4 v = vt[t][quad];
+            acc.x = __builtin_fmaf(pv, v.x, acc.x);
+            acc.y = __builtin_fmaf(pv, v.y, acc.y);
+            acc.z = __builtin_fmaf(pv, v.z, acc.z);
+            acc.w = __builtin_fmaf(pv, v.w, acc.w);
+        }
+        __syncthreads();
+    }
+    if (qi < T && 4 * quad < width) {
+        float* o = out + (size_t)qi * n_heads * hs + (size_t)h * hs + d0 + 4 * quad;
+        const float a[4] = {acc.x, acc.y, acc.z, acc.w};
+        for (int e = 0; e < 4 && 4 * quad + e < width; e++) o[e] = a[e];
+    }
+}
+
+// ---------------------------------------------------------------------------
 // Single-query attention in the reference's exact order in ONE kernel
 // (runq.c:367-391, softmax :307-318): the same operations as k_attn_scores
 // + k_attn_softmax_v, bit for bit, without the second launch and the scores'

@@ -350,6 +350,26 @@ int launch_attention_exact(const float* q, const float* kcache, const float* vca
             case 128: return go_attn_fused<128>(q, kcache, vcache, out, meta, pos, kv_mul, n_heads, max_t, k_il, st);
         }
     }
+    if (T > 1 && !meta && max_t % 4 == 0) {
+        // a batch of queries: K and V rows shared over the queries (same
+        // operations, same order as the per-query kernels below)
+        const int nk = pos + T;
+        const size_t lds = attn_scores_b_lds_bytes(hs);
+        if (int rc = raise_lds_limit(reinterpret_cast<const void*>(&k_attn_scores_b), lds,
+                                     "attention: raising the LDS limit"))
+            return rc;
+        hipLaunchKernelGGL(k_attn_scores_b, dim3(n_heads, (nk + kSbKeys - 1) / kSbKeys, (T + kSbQueries - 1) / kSbQueries),
+                           dim3(kSbThreads), lds, st, q, kcache, scores, pos, T, kv_mul, n_heads, hs, max_t, q_stride,
+                           k_il);
+        int rc = check_launch("attention_scores_b");
+        if (rc) return rc;
+        hipLaunchKernelGGL(k_attn_softmax_b, dim3(T, n_heads), dim3(kSmThreads), attn_softmax_b_lds_bytes(max_t), st,
+                           scores, pos, n_heads, max_t);
+        if ((rc = check_launch("attention_softmax_b"))) return rc;
+        hipLaunchKernelGGL(k_attn_pv_b, dim3(n_heads, (hs + kVDims - 1) / kVDims, (T + kPvQueries - 1) / kPvQueries),
+                           dim3(kPvThreads), 0, st, scores, vcache, out, pos, T, kv_mul, n_heads, hs, max_t);
+        return check_launch("attention_pv_b");
+    }
     // persistent score waves over (head, tile) items; a captured graph covers
     // every position the cache can hold, items past pos are not visited
     const int items = n_heads * ((meta ? max_t : pos + T) + kScoreTile - 1) / kScoreTile;
