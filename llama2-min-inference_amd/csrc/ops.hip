@@ -449,14 +449,20 @@ int launch_pf_gemm(int bits, int group, const void* w, const float* ws, int rows
         return L2Q_ERR_ARG;
     }
     // rows per workgroup (16, 32 or 64): the fewest rounds of workgroups
-    // over the CUs, times the rows each one folds; the larger tile on ties
-    // (each workgroup reads all the activations)
+    // over the CUs times a workgroup's time, modelled as 1.3 + its 16-row
+    // tiles (every workgroup restages all the step's activations, worth
+    // ~1.3 row tiles of folding: measured on the 7B shapes at T = 128, where
+    // this picks the fastest tile for each); the larger tile on ties
+    int ncu = 0, dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess ||
+        hipDeviceGetAttribute(&ncu, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || ncu <= 0)
+        ncu = 256;
     const long long rtiles = (rows + 15) / 16;
     int rtw = 4;
     long long best = -1;
     for (int r : {4, 2, 1}) {
         const long long wgs = (rtiles + r - 1) / r * ((T + kPf2Tokens - 1) / kPf2Tokens);
-        const long long cost = (wgs + 255) / 256 * r;
+        const long long cost = (wgs + ncu - 1) / ncu * (13 + 10 * r);
         if (best < 0 || cost < best) { best = cost; rtw = r; }
     }
     const dim3 grid((unsigned)((rows + 16 * rtw - 1) / (16 * rtw)), (unsigned)((T + kPf2Tokens - 1) / kPf2Tokens));

@@ -174,7 +174,7 @@ __global__ __launch_bounds__(kPf2Threads) void k_pf_gemm2(
             if (e < SN) {
                 S[g * kPf2Tokens + t] = R.rxs[k];
                 S[(KS + g) * kPf2Tokens + t] = R.rxt[k];
-                reinterpret_cast<int*>(S)[(2 * KS + g) * kPf2Tokens + t] = R.rsq[k] * (BITS == 4 ? 2048 : 128);
+                reinterpret_cast<int*>(S)[(2 * KS + g) * kPf2Tokens + t] = R.rsq[k] * 128;
             }
         }
 #pragma unroll
@@ -259,13 +259,13 @@ __global__ __launch_bounds__(kPf2Threads) void k_pf_gemm2(
 #pragma unroll
             for (int j = 0; j < TPW; j++) {
                 if (j >= nj) break;
-                const v4i32 c4 = {cin[g][j], cin[g][j], cin[g][j], cin[g][j]};
+                const v4i32 z4 = {0, 0, 0, 0};
 #pragma unroll
                 for (int i = 0; i < RTW; i++) {
                     if constexpr (G == 64)
-                        d[g][j][i] = __builtin_amdgcn_mfma_i32_16x16x64_i8(av[g][i], bv[g][j], c4, 0, 0, 0);
+                        d[g][j][i] = __builtin_amdgcn_mfma_i32_16x16x64_i8(av[g][i], bv[g][j], z4, 0, 0, 0);
                     else
-                        d[g][j][i] = __builtin_amdgcn_mfma_i32_16x16x32_i8(al[g][i], bl[g][j], c4, 0, 0, 0);
+                        d[g][j][i] = __builtin_amdgcn_mfma_i32_16x16x32_i8(al[g][i], bl[g][j], z4, 0, 0, 0);
                 }
             }
         }
@@ -281,7 +281,8 @@ __global__ __launch_bounds__(kPf2Threads) void k_pf_gemm2(
                     const float wr[4] = {wsv[g][i].x, wsv[g][i].y, wsv[g][i].z, wsv[g][i].w};
 #pragma unroll
                     for (int e = 0; e < 4; e++) {
-                        const int du8 = BITS == 4 ? d[g][j][i][e] >> 4 : d[g][j][i][e];   // = d + 128*sum(q), exact
+                        // d + 128*sum(q), exact (the INT4 dot is 16x the dot)
+                        const int du8 = (BITS == 4 ? d[g][j][i][e] >> 4 : d[g][j][i][e]) + cin[g][j];
                         acc[j][i][e] =
                             __builtin_fmaf(wr[e], __builtin_fmaf(gxs[g][j], (float)du8, -gxt[g][j]), acc[j][i][e]);
                     }
