@@ -118,8 +118,9 @@ def time_attention(torch, abi, host, ctx, mode, reps=50, n_heads=32, hs=128, max
     split-context, the config's 1e-5 tolerance) or "int8" (int8 cache); and
     its algorithmic bytes (K and V read, q read, output written).  Mode
     "split1" is the engine's tolerance-mode form (L2Q_ATTN_SPLIT_CONTEXT:
-    one kernel, the engine's K layout)."""
-    kv8 = mode == "int8"
+    one kernel, the engine's K layout); "int8split" the int8 cache split over
+    the context (the int8-KV engine's form)."""
+    kv8 = mode in ("int8", "int8split")
     g = torch.Generator(device="cuda")
     g.manual_seed(ctx)
     q = torch.randn(n_heads * hs, device="cuda", generator=g)
@@ -131,7 +132,8 @@ def time_attention(torch, abi, host, ctx, mode, reps=50, n_heads=32, hs=128, max
         ks = torch.rand(n_heads * max_t, device="cuda", generator=g) * 0.02
         vs = torch.rand(n_heads * max_t, device="cuda", generator=g) * 0.02
         args = (q.data_ptr(), k.data_ptr(), v.data_ptr(), ks.data_ptr(), vs.data_ptr(), out.data_ptr())
-        fn, nbytes = "l2q_attention_kv8", 2 * ctx * n_heads * (hs + 4)
+        fn = "l2q_attention_kv8_ex" if mode == "int8split" else "l2q_attention_kv8"
+        nbytes = 2 * ctx * n_heads * (hs + 4)
     else:
         k = torch.randn(n_heads * max_t * hs, device="cuda", generator=g)
         v = torch.randn(n_heads * max_t * hs, device="cuda", generator=g)
@@ -141,7 +143,8 @@ def time_attention(torch, abi, host, ctx, mode, reps=50, n_heads=32, hs=128, max
     nbytes += 2 * n_heads * hs * 4
     # exact, split1: the engine's K layout (and, exact, its choice of kernels)
     extra = {"exact": (abi.L2Q_ATTN_K_INTERLEAVED,),
-             "split1": (abi.L2Q_ATTN_K_INTERLEAVED | abi.L2Q_ATTN_SPLIT_CONTEXT,)}.get(mode, ())
+             "split1": (abi.L2Q_ATTN_K_INTERLEAVED | abi.L2Q_ATTN_SPLIT_CONTEXT,),
+             "int8split": (abi.L2Q_ATTN_SPLIT_CONTEXT,)}.get(mode, ())
 
     def launch():
         abi.call(fn, *args, ctx - 1, n_heads, n_heads, hs, max_t, *extra, torch.cuda.current_stream().cuda_stream)
@@ -486,7 +489,7 @@ def main():
         # the exact order and split over the context, int8 cache
         attention = {}
         for ctx in (256, 1024, 2048, 4096):
-            for name in ("exact", "split", "split1", "int8"):
+            for name in ("exact", "split", "split1", "int8", "int8split"):
                 ms, nbytes = time_attention(torch, abi, host, ctx, name)
                 attention[f"{name}_ctx{ctx}"] = {"us": round(ms * 1e3, 2), "bytes": nbytes,
                                                  "GB/s": round(nbytes / ms / 1e6, 1)}

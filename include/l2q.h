@@ -118,8 +118,13 @@ int l2q_engine_prefill(l2q_engine* e, const int* tokens, int n, int pos0,
                        float* logits);
 
 /* Engine options (l2q_engine_create_ex). */
-#define L2Q_ENGINE_KV_INT8 1   /* int8 KV cache (l2q_kv8_append / l2q_attention_kv8
-                                  semantics), the reference's -DINT8_KV=1 build */
+#define L2Q_ENGINE_KV_INT8 1   /* int8 KV cache (l2q_kv8_append semantics), the
+                                  reference's -DINT8_KV=1 build; its attention
+                                  is l2q_attention_kv8's (one workgroup per
+                                  head) up to L2Q_KV8_SPLIT_FROM positions and
+                                  l2q_attention_kv8_ex's split form (with
+                                  l2q_engine_attention_splits splits) beyond */
+#define L2Q_KV8_SPLIT_FROM 1024
 #define L2Q_ENGINE_STEP_KERNEL 2   /* run each decode step as one persistent
                                   kernel with grid barriers between its phases
                                   where the shape allows it (see
@@ -186,6 +191,15 @@ int l2q_engine_time_steps(l2q_engine* e, const int* tokens, int pos0,
 #define L2Q_GEMV_W2         3   /* w2: Q8 quantize prologue */
 #define L2Q_GEMV_CLASSIFIER 4   /* wcls: final RMSNorm prologue */
 int l2q_engine_time_gemv(l2q_engine* e, int kind, int n_launches, double* elapsed_ms);
+
+/* The number of context splits of the engine's decode attention when it
+ * runs split over the context (L2Q_ENGINE_KV_INT8 beyond L2Q_KV8_SPLIT_FROM
+ * positions: the order of the oracle's orc_attention_kv8_split with this
+ * many splits; L2Q_ENGINE_ATTN_SPLIT), 0 when it runs the reference's exact
+ * order.
+ * Chosen at creation from the head count, the cache length and the GPU's CU
+ * count.  No counterpart in the reference. */
+int l2q_engine_attention_splits(const l2q_engine* e);
 
 /* 1 when the engine runs each decode step as one persistent kernel
  * (L2Q_ENGINE_STEP_KERNEL was given and the shape has it: INT4 group 64, the
@@ -345,6 +359,19 @@ int l2q_kv8_append(const float* k, const float* v, int8_t* kcache8, int8_t* vcac
 int l2q_attention_kv8(const float* q, const int8_t* kcache8, const int8_t* vcache8,
                       const float* kscale, const float* vscale, float* out, int pos,
                       int n_heads, int n_kv_heads, int head_size, int max_t, void* stream);
+
+/* l2q_attention_kv8 with options.  flags 0 is l2q_attention_kv8 (one
+ * workgroup per head).  L2Q_ATTN_SPLIT_CONTEXT splits the context over about
+ * two workgroups per CU (the int8-KV engine's form): per-split softmax
+ * partials merged in split order by the last workgroup of each head, a
+ * fixed float order of its own (restated by the oracle's
+ * orc_attention_kv8_split), within the same 1e-5 of the double formula;
+ * partials and per-head counters in per-GPU library buffers, so calls that
+ * overlap on one GPU race.  No counterpart in the reference. */
+int l2q_attention_kv8_ex(const float* q, const int8_t* kcache8, const int8_t* vcache8,
+                         const float* kscale, const float* vscale, float* out, int pos,
+                         int n_heads, int n_kv_heads, int head_size, int max_t, int flags,
+                         void* stream);
 
 /* Greedy argmax on the device: out[0] = the first index of the maximum of
  * v[0..n), v 16-byte aligned (sample_argmax, runq.c:578-585; the engine's

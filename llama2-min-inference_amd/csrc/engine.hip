@@ -49,8 +49,11 @@ struct l2q_engine {
     int flags;               // L2Q_ENGINE_* options
     int device;
     hipStream_t stream = nullptr;
-    // captured steps [argmax][long context]: the long-context graphs (two-kernel
-    // attention) exist only when the cache outgrows attention_fused_max()
+    // captured steps [argmax][long context]: the long-context graphs exist
+    // only when the cache outgrows g_switch positions (fp32 cache: the
+    // two-kernel attention beyond attention_fused_max(); int8 cache: the
+    // split-context attention beyond L2Q_KV8_SPLIT_FROM)
+    int g_switch = 0;
     hipGraph_t graph[2][2] = {};
     hipGraphExec_t exec[2][2] = {};
     hipEvent_t ev0 = nullptr, ev1 = nullptr;
@@ -78,8 +81,9 @@ struct l2q_engine {
     unsigned* sync = nullptr;   // grp | top | rel | err | epoch (StepSync)
     size_t sync_bytes = 0;
     float* dbg = nullptr;       // [L+1][d]: the residual stream of forward_debug
-    // L2Q_ENGINE_ATTN_SPLIT: the one-kernel split-context attention's
-    // partials [n_heads][aS][hs + 2] and per-head counters (left zeroed)
+    // the split-context attentions (L2Q_ENGINE_ATTN_SPLIT, the int8 KV
+    // cache): partials [n_heads][aS][hs + 2] and per-head counters (left
+    // zeroed)
     float* apart = nullptr;
     unsigned* acnt = nullptr;
     int aS = 0;
@@ -219,9 +223,17 @@ int enqueue_step(l2q_engine* e, hipStream_t st, float* dbg_x, float* dbg_tmp, bo
         if (dbg_x && l == 0) HIPCHK(hipMemcpyAsync(dbg_x, e->xb, d * sizeof(float), hipMemcpyDeviceToHost, st), "copy x");
         if (e->flags & L2Q_ENGINE_KV_INT8) {
             const size_t co = (size_t)l * kv * e->max_t, so = (size_t)l * c.n_kv_heads * e->max_t;
-            // append the staged k, v rows and attend, in one kernel
-            rc = launch_attention_kv8(e->q, e->k8 + co, e->v8 + co, e->ks + so, e->vs + so, e->att, e->scores,
-                                      e->meta, 0, c.n_heads, c.n_kv_heads, e->hs, e->max_t, st, e->kvf, e->kvf + kv);
+            // append the staged k, v rows and attend in one kernel: one
+            // workgroup per head up to L2Q_KV8_SPLIT_FROM positions, split
+            // over the context beyond
+            if (fused)
+                rc = launch_attention_kv8(e->q, e->k8 + co, e->v8 + co, e->ks + so, e->vs + so, e->att, e->scores,
+                                          e->meta, 0, c.n_heads, c.n_kv_heads, e->hs, e->max_t, st, e->kvf,
+                                          e->kvf + kv);
+            else
+                rc = launch_attention_kv8_split(e->q, e->kvf, e->kvf + kv, e->k8 + co, e->v8 + co, e->ks + so,
+                                                e->vs + so, e->att, e->apart, e->acnt, e->aS, e->meta, 0, c.n_heads,
+                                                c.n_kv_heads, e->hs, e->max_t, st);
         } else if (e->flags & L2Q_ENGINE_ATTN_SPLIT) {
             rc = launch_attention_flash(e->q, kc, vc, e->att, e->apart, e->acnt, e->aS, e->meta, 0, c.n_heads,
                                         c.n_kv_heads, e->hs, e->max_t, 1, st);
@@ -460,9 +472,9 @@ int build(l2q_engine* e, const void* weights, size_t weights_bytes) {
     e->sync_bytes = (size_t)(8 * 16 + 16 + (size_t)(ncu > 0 ? ncu : 8) * 16 + 16 + 16) * sizeof(unsigned);
     const size_t o_sync = sa.take(e->sync_bytes), o_dbg = sa.take((L + 1) * d * 4);
     const bool asplit = e->flags & L2Q_ENGINE_ATTN_SPLIT;
-    e->aS = asplit ? attention_flash_splits(c.n_heads, e->max_t, ncu) : 0;
-    const size_t o_apart = sa.take(asplit ? attention_flash_part_floats(c.n_heads, e->aS, e->hs) * 4 : 0);
-    const size_t o_acnt = sa.take(asplit ? (size_t)c.n_heads * sizeof(unsigned) : 0);
+    e->aS = asplit || kv8 ? attention_flash_splits(c.n_heads, e->max_t, ncu) : 0;
+    const size_t o_apart = sa.take(e->aS ? attention_flash_part_floats(c.n_heads, e->aS, e->hs) * 4 : 0);
+    const size_t o_acnt = sa.take(e->aS ? (size_t)c.n_heads * sizeof(unsigned) : 0);
     e->sbytes = align_up(sa.used, 256);
     HIPCHK(hipMalloc(&e->sarena, e->sbytes), "hipMalloc(state)");
     char* S_ = e->sarena;
@@ -493,8 +505,9 @@ int build(l2q_engine* e, const void* weights, size_t weights_bytes) {
     HIPCHK(hipEventCreate(&e->ev1), "hipEventCreate");
     // short contexts: one-kernel attention where the head size has it
     // (the split-context attention serves every position in one graph)
-    const bool fused = e->step || asplit || (attention_fused_ok(e->hs) && !(e->flags & L2Q_ENGINE_KV_INT8));
-    const bool need_long = !e->step && !asplit && (!fused || e->max_t > attention_fused_max());
+    e->g_switch = kv8 ? L2Q_KV8_SPLIT_FROM : attention_fused_max();
+    const bool fused = e->step || asplit || kv8 || attention_fused_ok(e->hs);
+    const bool need_long = !e->step && !asplit && (!fused || e->max_t > e->g_switch);
     for (int a = 0; a < 2; a++) {
         if (fused && (rc = capture(e, a, true, &e->graph[a][0], &e->exec[a][0]))) return rc;
         if (need_long && (rc = capture(e, a, false, &e->graph[a][1], &e->exec[a][1]))) return rc;
@@ -512,11 +525,11 @@ int check_step(l2q_engine* e, int token, int pos) {
     return L2Q_OK;
 }
 
-// The captured step for this position: the one-kernel attention graph up to
-// attention_fused_max() positions, the two-kernel one beyond.
+// The captured step for this position: the short-context graph up to
+// g_switch positions, the long-context one beyond.
 hipGraphExec_t step_graph(const l2q_engine* e, bool argmax, int pos) {
     hipGraphExec_t const* g = e->exec[argmax ? 1 : 0];
-    return g[0] && (!g[1] || pos + 1 <= attention_fused_max()) ? g[0] : g[1];
+    return g[0] && (!g[1] || pos + 1 <= e->g_switch) ? g[0] : g[1];
 }
 
 int launch_step(l2q_engine* e, int token, int pos, hipGraphExec_t ex, int slot) {
@@ -818,6 +831,8 @@ int l2q_engine_time_gemv(l2q_engine* e, int kind, int n_launches, double* elapse
     *elapsed_ms = ms;
     return L2Q_OK;
 }
+
+int l2q_engine_attention_splits(const l2q_engine* e) { return e ? e->aS : 0; }
 
 int l2q_engine_uses_step_kernel(const l2q_engine* e) { return e && e->step ? 1 : 0; }
 

@@ -935,8 +935,11 @@ __global__ __launch_bounds__(kAfThreads) void k_attn_fused(
 // lane p mod 64.
 constexpr int kKv8Pairs = kAttnMaxHs / 2 / L2Q_WAVE;   // pairs per lane (hs <= 256)
 // One wave quantizes one row: src[0..hs) (rotated first when a RoPE table
-// is given) -> int8 row `dst` (global, may be null) and `ldst` (LDS, may be
-// null), scale to *scale / *lscale (lane 0).
+// is given) -> int8 row `dst` (global, may be null) and, with TO_LDS,
+// `ldst` (LDS), scale to *scale / *lscale (lane 0).  (TO_LDS is a template
+// argument: a run-time null test of a generic pointer that holds an LDS
+// address miscompiles on gfx950 in some kernels.)
+template <bool TO_LDS>
 __device__ __forceinline__ void kv8_quant_row(const float* __restrict__ src, const float* __restrict__ rope, int pos,
                                               int hs, int lane, int8_t* dst, float* scale, int8_t* ldst,
                                               float* lscale) {
@@ -966,12 +969,12 @@ __device__ __forceinline__ void kv8_quant_row(const float* __restrict__ src, con
             const int q0 = q8_value(val[i].x, sc), q1 = q8_value(val[i].y, sc);
             const uint16_t w = (uint16_t)((q0 & 0xff) | ((q1 & 0xff) << 8));
             if (dst) *reinterpret_cast<uint16_t*>(dst + 2 * p) = w;
-            if (ldst) *reinterpret_cast<uint16_t*>(ldst + 2 * p) = w;
+            if constexpr (TO_LDS) *reinterpret_cast<uint16_t*>(ldst + 2 * p) = w;
         }
     }
     if (lane == 0) {
         if (scale) *scale = sc;
-        if (lscale) *lscale = sc;
+        if constexpr (TO_LDS) *lscale = sc;
     }
 }
 
@@ -982,7 +985,7 @@ __global__ __launch_bounds__(L2Q_WAVE) void k_kv8_append(
     const int g = blockIdx.x, isv = blockIdx.y, lane = threadIdx.x;
     const int pos = meta_pos(meta, pos_arg);
     const size_t row = (size_t)g * max_t + pos;
-    kv8_quant_row((isv ? v : k) + (size_t)g * hs, isv ? nullptr : rope, pos, hs, lane, (isv ? v8 : k8) + row * hs,
+    kv8_quant_row<false>((isv ? v : k) + (size_t)g * hs, isv ? nullptr : rope, pos, hs, lane, (isv ? v8 : k8) + row * hs,
                   (isv ? vs : ks) + row, nullptr, nullptr);
 }
 
@@ -1038,10 +1041,10 @@ __global__ __launch_bounds__(kA8Threads) void k_attn8_fused(
     if (append && wv < 2) {
         const bool first = h % kv_mul == 0;
         if (wv == 0)
-            kv8_quant_row(kst + (size_t)hk * hs, nullptr, pos, hs, lane, first ? k8 + prow * hs : nullptr,
+            kv8_quant_row<true>(kst + (size_t)hk * hs, nullptr, pos, hs, lane, first ? k8 + prow * hs : nullptr,
                           first ? ks + prow : nullptr, krow, red + 2 * kA8Waves);
         else
-            kv8_quant_row(vst + (size_t)hk * hs, nullptr, pos, hs, lane, first ? v8 + prow * hs : nullptr,
+            kv8_quant_row<true>(vst + (size_t)hk * hs, nullptr, pos, hs, lane, first ? v8 + prow * hs : nullptr,
                           first ? vs + prow : nullptr, vrow, red + 2 * kA8Waves + 1);
     }
 
@@ -1145,6 +1148,221 @@ __global__ __launch_bounds__(kA8Threads) void k_attn8_fused(
         for (int sl = 0; sl < slices; sl++) s2 += part[(size_t)sl * hs + d];
         out[(size_t)h * hs + d] = s2 / sum;
     }
+}
+
+// ---------------------------------------------------------------------------
+// int8-KV attention split over the context (the int8-KV engine's decode
+// attention and l2q_attention_kv8_ex with L2Q_ATTN_SPLIT_CONTEXT): the
+// v5-cuda-fused/run.cu:350-410 formula with the cache read by n_heads x S
+// workgroups instead of one per head.  Workgroup (head h, split s) of 256
+// threads covers positions [s*C, min((s+1)*C, n)), C = ceil(n/S) <= 256;
+// its float order is restated by the oracle's orc_attention_kv8_split:
+//   append   the split holding pos quantizes the step's staged k and v rows
+//            into LDS (waves 0 and 1, kv8_quant_row); the kv group's first
+//            head also writes them to the cache;
+//   scores   k_attn8_fused's per-position order (four lanes per position,
+//            chain `sub` over the chunks 4*sub + 16*i with FMAs, butterfly
+//            (a0+a1)+(a2+a3), then / sqrtf(hs) * ks_t), 64 positions per
+//            round with the next round's K in flight;
+//   softmax  m_s = the split's max; e_t = expf(s_t - m_s) (exp_runq_t);
+//            l_s = thread j's e_{t0+j}, wave butterflies, (w0+w1)+(w2+w3);
+//   p*V      256/(hs/4) slices x hs/4 element groups: fma(e_t*vs_t, v8_t,
+//            acc) over t = t0 + slice, + slices, ...; slices added in order;
+//   merge    as k_attn_flash: wave 0 stores (m_s, l_s, o_s) with agent-scope
+//            stores, waits for them, arrives on the head's counter; the S-th
+//            arrival merges in split order: w_s = expf(m_s - M),
+//            L = sum w_s*l_s, out = (sum fma(w_s, o_s)) / L, and resets the
+//            counter.  No workgroup waits on another.
+constexpr int kA8sThreads = 256;
+constexpr int kA8sMaxC = 256;
+__host__ __device__ constexpr size_t attn8_split_lds_bytes(int S, int hs) {
+    return ((size_t)kA8sMaxC + 4 * kA8sThreads + 16 + 2 * kAttnMaxHs / 4 + 64 + (size_t)S * (hs + 2)) * sizeof(float);
+}
+__global__ __launch_bounds__(kA8sThreads) void k_attn8_split(
+    const float* __restrict__ q, const float* __restrict__ kst, const float* __restrict__ vst,
+    int8_t* __restrict__ k8, int8_t* __restrict__ v8, float* __restrict__ ks, float* __restrict__ vs,
+    float* __restrict__ out, float* __restrict__ part, unsigned* __restrict__ cnt, const int* __restrict__ meta,
+    int pos_arg, int kv_mul, int hs, int max_t) {
+    extern __shared__ __attribute__((aligned(16))) float smf[];
+    float* sc = smf;                                   // [C] scores, then e_t * vs_t
+    float* psl = sc + kA8sMaxC;                        // [slices][hs] p*V partials, then the partial
+    float* red = psl + 4 * kA8sThreads;                // [4] wave maxima, [4] wave sums, [2] row scales
+    int8_t* krow = reinterpret_cast<int8_t*>(red + 16);   // [hs] appended k row, then [hs] v row
+    int8_t* vrow = krow + kAttnMaxHs;
+    uint64_t* etab = reinterpret_cast<uint64_t*>(vrow + kAttnMaxHs);   // [32] exp table
+    float* mrg = reinterpret_cast<float*>(etab + 32);  // [S][hs + 2] merge staging
+    __shared__ int is_last;
+    const int h = blockIdx.x, s = blockIdx.y, S = gridDim.y, hk = h / kv_mul;
+    const int tid = threadIdx.x, lane = tid & (L2Q_WAVE - 1), wv = tid / L2Q_WAVE, sub = tid & 3;
+    const int pos = meta_pos(meta, pos_arg);
+    const int n = pos + 1;
+    const int C = (n + S - 1) / S;
+    const int t0 = min(s * C, n), t1 = min(n, t0 + C), mn = t1 - t0;
+    const bool append = kst != nullptr && t0 <= pos && pos < t1;
+    const size_t prow = (size_t)hk * max_t + pos;
+    if (append && wv < 2) {   // wave 0 the k row, wave 1 the v row (one call with per-wave arguments)
+        const bool first = h % kv_mul == 0;
+        const float* src = (wv == 0 ? kst : vst) + (size_t)hk * hs;
+        int8_t* cache = wv == 0 ? k8 : v8;
+        float* scale = wv == 0 ? ks : vs;
+        kv8_quant_row<true>(src, nullptr, pos, hs, lane, first ? cache + prow * hs : nullptr, first ? scale + prow : nullptr,
+                      wv == 0 ? krow : vrow, red + 8 + wv);
+    }
+    const float rs = sqrtf((float)hs);
+    const int nch = hs / 16;
+    const float* qh = q + (size_t)h * hs;
+    float4 qr[kA8Chunks];
+#pragma unroll
+    for (int i = 0; i < kA8Chunks; i++)
+        qr[i] = i < nch ? *reinterpret_cast<const float4*>(qh + 4 * sub + 16 * i) : make_float4(0, 0, 0, 0);
+    const int8_t* kb = k8 + (size_t)hk * max_t * hs;
+    const int tl = max(t1 - 1, 0);
+    int kw[kA8Chunks];
+    auto load_round = [&](int r0, int (&w)[kA8Chunks]) {
+        const int tc = min(t0 + r0 + tid / 4, tl);
+#pragma unroll
+        for (int i = 0; i < kA8Chunks; i++)
+            if (i < nch) w[i] = *reinterpret_cast<const int*>(kb + (size_t)tc * hs + 4 * sub + 16 * i);
+    };
+    if (mn > 0) load_round(0, kw);
+    if (wv == 2) {   // the exp table through the scalar cache (uniform loads)
+        uint64_t tabv = 0;
+#pragma unroll
+        for (int i = 0; i < 32; i++) tabv = (lane & 31) == i ? kExp2Tab[i] : tabv;
+        etab[lane & 31] = tabv;
+    }
+    __syncthreads();   // the appended rows and the exp table in LDS
+    for (int r0 = 0; r0 < mn; r0 += kA8sThreads / 4) {
+        int kn[kA8Chunks];
+        load_round(min(r0 + kA8sThreads / 4, mn - 1), kn);
+        const int t = t0 + r0 + tid / 4;
+        const bool own = append && min(t, tl) == pos;
+        float acc = 0.0f;
+#pragma unroll
+        for (int i = 0; i < kA8Chunks; i++) {
+            if (i < nch) {
+                const int w = own ? *reinterpret_cast<const int*>(krow + 4 * sub + 16 * i) : kw[i];
+                acc = __builtin_fmaf(qr[i].x, sbyte(w, 0), acc);
+                acc = __builtin_fmaf(qr[i].y, sbyte(w, 1), acc);
+                acc = __builtin_fmaf(qr[i].z, sbyte(w, 2), acc);
+                acc = __builtin_fmaf(qr[i].w, sbyte(w, 3), acc);
+            }
+        }
+        acc += __shfl_xor(acc, 1);
+        acc += __shfl_xor(acc, 2);
+        // both scales read, the value selected (a select of the two addresses
+        // would become one generic load, which the compiler mishandles here)
+        const float kso = red[8], ksc = ks[(size_t)hk * max_t + min(t, tl)];
+        if (sub == 0 && t < t1) sc[t - t0] = acc / rs * (own ? kso : ksc);
+#pragma unroll
+        for (int i = 0; i < kA8Chunks; i++) kw[i] = kn[i];
+    }
+    __syncthreads();
+    // the split's softmax
+    float m = tid < mn ? sc[tid] : -INFINITY;
+    m = group_max<L2Q_WAVE>(m);
+    if (lane == 0) red[wv] = m;
+    __syncthreads();
+    m = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+    float l = 0.0f;
+    if (tid < mn) {
+        const int t = t0 + tid;
+        const float e = exp_runq_t(sc[tid] - m, etab);   // the host C library's expf, bit for bit
+        l = l + e;
+        const float vso = red[9], vsc = vs[(size_t)hk * max_t + t];
+        sc[tid] = e * (append && t == pos ? vso : vsc);
+    }
+    for (int o = 32; o > 0; o >>= 1) l += __shfl_xor(l, o);
+    if (lane == 0) red[4 + wv] = l;
+    __syncthreads();
+    l = (red[4] + red[5]) + (red[6] + red[7]);
+    // p*V slices
+    const int groups = hs / 4, slices = kA8sThreads / groups;
+    const int gi = tid % groups, sl = tid / groups;
+    if (sl < slices) {
+        float4 acc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        const int8_t* vb = v8 + (size_t)hk * max_t * hs + 4 * gi;
+        for (int j = sl; j < mn; j += slices) {
+            const int t = t0 + j;
+            const int wo = *reinterpret_cast<const int*>(vrow + 4 * gi);
+            const int wc = *reinterpret_cast<const int*>(vb + (size_t)t * hs);
+            const int w = append && t == pos ? wo : wc;
+            const float p = sc[j];
+            acc.x = __builtin_fmaf(p, sbyte(w, 0), acc.x);
+            acc.y = __builtin_fmaf(p, sbyte(w, 1), acc.y);
+            acc.z = __builtin_fmaf(p, sbyte(w, 2), acc.z);
+            acc.w = __builtin_fmaf(p, sbyte(w, 3), acc.w);
+        }
+        *reinterpret_cast<float4*>(psl + (size_t)sl * hs + 4 * gi) = acc;
+    }
+    __syncthreads();
+    float od[kAttnMaxHs / L2Q_WAVE];   // this lane's partial elements d = lane + 64k (wave 0)
+    if (wv == 0) {
+#pragma unroll
+        for (int k = 0; k < kAttnMaxHs / L2Q_WAVE; k++) {
+            const int d = lane + L2Q_WAVE * k;
+            float o = 0.0f;
+            if (d < hs)
+                for (int k2 = 0; k2 < slices; k2++) o = o + psl[(size_t)k2 * hs + d];
+            od[k] = o;
+        }
+    }
+    // the partial (wave 0, agent-scope stores), then the arrival
+    float* pp = part + ((size_t)h * S + s) * (hs + 2);
+    auto put = [](float* a, float v) { __hip_atomic_store(a, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); };
+    auto get = [](const float* a) {
+        return __hip_atomic_load(const_cast<float*>(a), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    };
+    if (wv == 0) {
+#pragma unroll
+        for (int k = 0; k < kAttnMaxHs / L2Q_WAVE; k++)
+            if (lane + L2Q_WAVE * k < hs) put(pp + lane + L2Q_WAVE * k, od[k]);
+        if (lane == 0) {
+            put(pp + hs, mn > 0 ? m : -INFINITY);
+            put(pp + hs + 1, mn > 0 ? l : 0.0f);
+        }
+        __atomic_signal_fence(__ATOMIC_SEQ_CST);
+        __builtin_amdgcn_s_waitcnt(0x0F70);   // vmcnt(0): this wave's partial stores are acknowledged
+        __atomic_signal_fence(__ATOMIC_SEQ_CST);
+        if (lane == 0)
+            is_last = __hip_atomic_fetch_add(cnt + h, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+                      (unsigned)(S - 1);
+    }
+    __syncthreads();
+    if (!is_last) return;
+    // merge in split order
+    const float* ph = part + (size_t)h * S * (hs + 2);
+    const int total = S * (hs + 2);
+    for (int e0 = 0; e0 < total; e0 += 8 * kA8sThreads) {
+        float v[8];
+#pragma unroll
+        for (int k = 0; k < 8; k++) {
+            const int e = e0 + k * kA8sThreads + tid;
+            v[k] = e < total ? get(ph + e) : 0.0f;
+        }
+#pragma unroll
+        for (int k = 0; k < 8; k++) {
+            const int e = e0 + k * kA8sThreads + tid;
+            if (e < total) mrg[e] = v[k];
+        }
+    }
+    __syncthreads();
+    float M = -INFINITY;
+    for (int k = 0; k < S; k++) M = fmaxf(M, mrg[k * (hs + 2) + hs]);
+    float* wsp = psl;   // [S] merge weights w_s (the p*V partials are no longer needed)
+    if (tid < S) {
+        const float ms = mrg[tid * (hs + 2) + hs];
+        wsp[tid] = ms == -INFINITY ? 0.0f : exp_runq_t(ms - M, etab);
+    }
+    __syncthreads();
+    float L = 0.0f;
+    for (int k = 0; k < S; k++) L = L + wsp[k] * mrg[k * (hs + 2) + hs + 1];
+    for (int d = tid; d < hs; d += kA8sThreads) {
+        float acc = 0.0f;
+        for (int k = 0; k < S; k++) acc = __builtin_fmaf(wsp[k], mrg[k * (hs + 2) + d], acc);
+        out[(size_t)h * hs + d] = acc / L;
+    }
+    if (tid == 0) __hip_atomic_store(cnt + h, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // Merge the S partials of each head: out = sum_s e^(m_s-M) o_s / sum_s e^(m_s-M) l_s.

@@ -420,6 +420,26 @@ int launch_attention_kv8(const float* q, int8_t* k8, int8_t* v8, float* ks, floa
     return check_launch("attention_kv8");
 }
 
+int launch_attention_kv8_split(const float* q, const float* kst, const float* vst, int8_t* k8, int8_t* v8,
+                               float* ks, float* vs, float* out, float* part, unsigned* cnt, int S, const int* meta,
+                               int pos, int n_heads, int n_kv_heads, int hs, int max_t, hipStream_t st) {
+    // positions a launch may cover: any of the cache's under a captured graph
+    const int nmax = meta ? max_t : pos + 1;
+    if (!kv8_shape_ok(n_heads, n_kv_heads, hs, max_t) || (!meta && (pos < 0 || pos >= max_t)) || (!kst != !vst) ||
+        S < 1 || S > kFlMaxSplits || (nmax + S - 1) / S > kA8sMaxC || !part || !cnt) {
+        set_error("attention kv8 split: bad shape heads=%d kv_heads=%d hs=%d pos=%d max_t=%d S=%d", n_heads,
+                  n_kv_heads, hs, pos, max_t, S);
+        return L2Q_ERR_ARG;
+    }
+    const size_t lds = attn8_split_lds_bytes(S, hs);
+    if (int rc = raise_lds_limit(reinterpret_cast<const void*>(&k_attn8_split), lds,
+                                 "attention kv8 split: raising the LDS limit"))
+        return rc;
+    hipLaunchKernelGGL(k_attn8_split, dim3(n_heads, S), dim3(kA8sThreads), lds, st, q, kst, vst, k8, v8, ks, vs, out,
+                       part, cnt, meta, pos, n_heads / n_kv_heads, hs, max_t);
+    return check_launch("attention_kv8_split");
+}
+
 // ---------------------------------------------------------------------------
 // batched prefill
 
@@ -763,6 +783,36 @@ int l2q_kv8_append(const float* k, const float* v, int8_t* kcache8, int8_t* vcac
                    const float* rope, int pos, int n_kv_heads, int head_size, int max_t, void* stream) {
     return launch_kv8_append(k, v, kcache8, vcache8, kscale, vscale, rope, nullptr, pos, n_kv_heads, head_size, max_t,
                              (hipStream_t)stream);
+}
+
+int l2q_attention_kv8_ex(const float* q, const int8_t* kcache8, const int8_t* vcache8, const float* kscale,
+                         const float* vscale, float* out, int pos, int n_heads, int n_kv_heads, int head_size,
+                         int max_t, int flags, void* stream) {
+    if (flags & ~L2Q_ATTN_SPLIT_CONTEXT) {
+        set_error("attention kv8: unknown flags %d", flags);
+        return L2Q_ERR_ARG;
+    }
+    if (!flags)
+        return l2q_attention_kv8(q, kcache8, vcache8, kscale, vscale, out, pos, n_heads, n_kv_heads, head_size,
+                                 max_t, stream);
+    if (!kv8_shape_ok(n_heads, n_kv_heads, head_size, max_t) || pos < 0 || pos >= max_t) {
+        set_error("attention kv8: bad shape heads=%d kv_heads=%d hs=%d pos=%d max_t=%d", n_heads, n_kv_heads,
+                  head_size, pos, max_t);
+        return L2Q_ERR_ARG;
+    }
+    int dev = 0, ncu = 0;
+    if (hipGetDevice(&dev) != hipSuccess ||
+        hipDeviceGetAttribute(&ncu, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
+        ncu = 0;
+    const int S = attention_flash_splits(n_heads, pos + 1, ncu);
+    float* scratch = nullptr;
+    unsigned* cnt = nullptr;
+    int rc;
+    if ((rc = attn_scratch(attention_flash_part_floats(n_heads, S, head_size), &scratch))) return rc;
+    if ((rc = flash_counters(n_heads, &cnt))) return rc;
+    return launch_attention_kv8_split(q, nullptr, nullptr, const_cast<int8_t*>(kcache8), const_cast<int8_t*>(vcache8),
+                                      const_cast<float*>(kscale), const_cast<float*>(vscale), out, scratch, cnt, S,
+                                      nullptr, pos, n_heads, n_kv_heads, head_size, max_t, (hipStream_t)stream);
 }
 
 int l2q_attention_kv8(const float* q, const int8_t* kcache8, const int8_t* vcache8, const float* kscale,

@@ -18,6 +18,7 @@ L2Q_ERR_STATE = -5
 L2Q_ENGINE_KV_INT8 = 1
 L2Q_ENGINE_STEP_KERNEL = 2
 L2Q_ENGINE_ATTN_SPLIT = 4
+L2Q_KV8_SPLIT_FROM = 1024
 L2Q_ATTN_K_INTERLEAVED = 1
 L2Q_ATTN_ONE_KERNEL = 2
 L2Q_ATTN_TWO_KERNELS = 4
@@ -55,6 +56,7 @@ SIGNATURES = {
     "l2q_engine_time_gemv": (I, [P, I, I, C.POINTER(C.c_double)]),
     "l2q_engine_device_bytes": (C.c_size_t, [P]),
     "l2q_engine_uses_step_kernel": (I, [P]),
+    "l2q_engine_attention_splits": (I, [P]),
     "l2q_engine_destroy": (None, [P]),
     "l2q_quantize_act": (I, [P, I, I, P, P, P]),
     "l2q_gemv_q8": (I, [P, P, P, P, P, I, I, I, P, P]),
@@ -71,6 +73,7 @@ SIGNATURES = {
     "l2q_attention_split_noalloc": (I, [P, P, P, P, I, I, I, I, I, P]),
     "l2q_kv8_append": (I, [P, P, P, P, P, P, P, I, I, I, I, P]),
     "l2q_attention_kv8": (I, [P, P, P, P, P, P, I, I, I, I, I, P]),
+    "l2q_attention_kv8_ex": (I, [P, P, P, P, P, P, I, I, I, I, I, I, P]),
     "l2q_expf": (I, [P, P, C.c_size_t, P]),
     "l2q_rope_table": (None, [P, I, I]),
 }

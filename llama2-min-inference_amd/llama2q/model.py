@@ -95,6 +95,11 @@ class Engine:
         return ids
 
     @property
+    def attention_splits(self) -> int:
+        """Context splits of the decode attention (0: the exact order)."""
+        return abi.lib().l2q_engine_attention_splits(self._h)
+
+    @property
     def step_kernel(self) -> bool:
         """Whether each step runs as the one persistent kernel."""
         return bool(abi.lib().l2q_engine_uses_step_kernel(self._h))

@@ -3,6 +3,7 @@
 #include "oracle.h"
 
 #include <math.h>
+#include <stdio.h>
 #include <stdlib.h>
 #include <string.h>
 
@@ -151,6 +152,8 @@ struct orc_model {
     orc_qmat wq, wk, wv, wo, w1, w2, w3, wcls;
     float *x, *xb, *xb2, *hb, *hb2, *q, *att, *logits, *kcache, *vcache;
     int kv8;                          /* 1: int8 KV cache (orc_model_set_kv8) */
+    int kv8_splits;                   /* > 0: its attention in the split order (orc_model_set_kv8_splits) */
+    int kv8_split_from;               /*      over more than this many positions */
     int8_t *k8, *v8;                  /* [L][max_t][kv_dim] */
     float *ks, *vs;                   /* [L][max_t][n_kv_heads] */
     int8_t* xq;
@@ -405,6 +408,107 @@ void orc_attention_kv8_ordered(const float* q, const int8_t* kc, const int8_t* v
     free(pe);
 }
 
+/* The int8-KV attention split over the context (the float order of this
+ * build's k_attn8_split, for bit-exact comparison; pinned to
+ * orc_attention_kv8 (double) by the tests).  n = pos + 1 positions in S
+ * splits of C = ceil(n / S): split s covers [min(sC, n), min(n, sC + C)).
+ * Per split:
+ *   score_t  as orc_attention_kv8_ordered: four FMA chains (chain j over the
+ *            4-element chunks c = 4j + 16i), (a0+a1)+(a2+a3), then
+ *            (dot / sqrtf(hs)) * ks_t
+ *   m_s      the split's maximum score; e_t = expf(score_t - m_s)
+ *   l_s      256 partial sums (thread j: t = t0 + j, t0 + j + 256, ...; at
+ *            most one position each since C <= 256), the 4 waves' 64 added by
+ *            the xor butterfly 32,16,...,1, the waves as (w0+w1)+(w2+w3)
+ *   o_s[d]   slices = 256/(hs/4); slice k: fma(e_t*vs_t, v8_t[d], acc) over
+ *            t = t0 + k, t0 + k + slices, ...; o = ((0+p_0)+p_1)+...
+ * Merge in split order: M = max m_s, w_s = expf(m_s - M) (0 for an empty
+ * split), L = ((0 + w_0*l_0) + w_1*l_1) + ..., out[d] = acc / L with
+ * acc = fmaf(w_s, o_s[d], acc) over s. */
+void orc_attention_kv8_split(const float* q, const int8_t* kc, const int8_t* vc, const float* ks,
+                             const float* vs, float* out, int pos, int n_heads, int n_kv_heads, int hs,
+                             size_t t_stride, size_t head_stride, size_t s_t_stride, size_t s_head_stride,
+                             int S) {
+    const int kv_mul = n_heads / n_kv_heads, n = pos + 1, C = (n + S - 1) / S;
+    if (S < 1 || C > 256) {
+        fprintf(stderr, "orc_attention_kv8_split: %d positions in %d splits exceed 256 per split\n", n, S);
+        abort();
+    }
+    const float rs = sqrtf((float)hs);
+    float* pm = (float*)malloc((size_t)S * sizeof(float));
+    float* pl = (float*)malloc((size_t)S * sizeof(float));
+    float* po = (float*)malloc((size_t)S * hs * sizeof(float));
+    float sc[256], pe[256];
+    for (int h = 0; h < n_heads; h++) {
+        const int g = h / kv_mul;
+        const float* qh = q + (size_t)h * hs;
+        for (int sp = 0; sp < S; sp++) {
+            const int t0 = sp * C < n ? sp * C : n;
+            const int t1 = t0 + C < n ? t0 + C : n, mn = t1 - t0;
+            float m = -INFINITY;
+            for (int t = t0; t < t1; t++) {
+                const int8_t* kt = kc + (size_t)g * head_stride + (size_t)t * t_stride;
+                float a[4];
+                for (int j = 0; j < 4; j++) {
+                    a[j] = 0.0f;
+                    for (int c = 4 * j; c < hs; c += 16)
+                        for (int e = 0; e < 4; e++) a[j] = fmaf(qh[c + e], (float)kt[c + e], a[j]);
+                }
+                const float dot = (a[0] + a[1]) + (a[2] + a[3]);
+                sc[t - t0] = dot / rs * ks[(size_t)t * s_t_stride + (size_t)g * s_head_stride];
+                m = fmaxf(m, sc[t - t0]);
+            }
+            float part[256], wsum[4];
+            for (int j = 0; j < 256; j++) {
+                part[j] = 0.0f;
+                if (j < mn) {
+                    const int t = t0 + j;
+                    const float e = expf(sc[j] - m);
+                    part[j] = part[j] + e;
+                    pe[j] = e * vs[(size_t)t * s_t_stride + (size_t)g * s_head_stride];
+                }
+            }
+            for (int w = 0; w < 4; w++) wsum[w] = butterfly64(part + 64 * w);
+            pm[sp] = mn > 0 ? m : -INFINITY;
+            pl[sp] = mn > 0 ? (wsum[0] + wsum[1]) + (wsum[2] + wsum[3]) : 0.0f;
+            const int slices = 256 / (hs / 4);
+            for (int d = 0; d < hs; d++) {
+                float o = 0.0f;
+                for (int k = 0; k < slices; k++) {
+                    float acc = 0.0f;
+                    for (int j = k; j < mn; j += slices)
+                        acc = fmaf(pe[j], (float)vc[(size_t)g * head_stride + (size_t)(t0 + j) * t_stride + d], acc);
+                    o = o + acc;
+                }
+                po[(size_t)sp * hs + d] = o;
+            }
+        }
+        float M = -INFINITY;
+        for (int sp = 0; sp < S; sp++) M = fmaxf(M, pm[sp]);
+        float L = 0.0f;
+        for (int sp = 0; sp < S; sp++) {
+            const float w = pm[sp] == -INFINITY ? 0.0f : expf(pm[sp] - M);
+            pm[sp] = w;
+            L = L + w * pl[sp];
+        }
+        for (int d = 0; d < hs; d++) {
+            float acc = 0.0f;
+            for (int sp = 0; sp < S; sp++) acc = fmaf(pm[sp], po[(size_t)sp * hs + d], acc);
+            out[(size_t)h * hs + d] = acc / L;
+        }
+    }
+    free(pm);
+    free(pl);
+    free(po);
+}
+
+int orc_model_set_kv8_splits(orc_model* m, int splits, int split_from) {
+    if (splits < 0 || splits > 64 || split_from < 0) return -1;
+    m->kv8_splits = splits;
+    m->kv8_split_from = split_from;
+    return 0;
+}
+
 int orc_model_set_kv8(orc_model* m, int on) {
     if (!on) { m->kv8 = 0; return 0; }
     const size_t n = (size_t)m->n_layers * m->max_t * m->kv_dim;
@@ -457,9 +561,14 @@ const float* orc_forward(orc_model* m, int token, int pos, float* x_layers) {
                 orc_kv_quant(v + (size_t)g * hs, hs, m->v8 + loff + (size_t)pos * kv_dim + (size_t)g * hs, m->vs + soff + g);
             }
             const size_t sl = (size_t)l * m->max_t * m->n_kv_heads;
-            orc_attention_kv8_ordered(m->q, m->k8 + loff, m->v8 + loff, m->ks + sl, m->vs + sl, m->xb, pos,
-                                      m->n_heads, m->n_kv_heads, hs, (size_t)kv_dim, (size_t)hs,
-                                      (size_t)m->n_kv_heads, 1);
+            if (m->kv8_splits > 0 && pos + 1 > m->kv8_split_from)
+                orc_attention_kv8_split(m->q, m->k8 + loff, m->v8 + loff, m->ks + sl, m->vs + sl, m->xb, pos,
+                                        m->n_heads, m->n_kv_heads, hs, (size_t)kv_dim, (size_t)hs,
+                                        (size_t)m->n_kv_heads, 1, m->kv8_splits);
+            else
+                orc_attention_kv8_ordered(m->q, m->k8 + loff, m->v8 + loff, m->ks + sl, m->vs + sl, m->xb, pos,
+                                          m->n_heads, m->n_kv_heads, hs, (size_t)kv_dim, (size_t)hs,
+                                          (size_t)m->n_kv_heads, 1);
         } else {
             orc_attention(m->q, m->kcache + loff, m->vcache + loff, m->xb, pos, m->n_heads,
                           m->n_kv_heads, hs, (size_t)kv_dim, (size_t)hs, m->att, m->max_t);

@@ -20,6 +20,8 @@
  *   orc_attention_kv8  v5-cuda-fused/run.cu:350-410 (attention over it; in
  *                      double, the value every float order approximates)
  *   orc_attention_kv8_ordered  the same in the GPU kernels' float order
+ *   orc_attention_kv8_split    the same split over the context (the
+ *                      split kernel's float order)
  *   orc_swiglu         runq.c:405-410
  *   orc_forward        runq.c:320-421
  * Floating-point contraction follows a GCC -O3 -march=native build of
@@ -79,6 +81,14 @@ void orc_attention_kv8_ordered(const float* q, const int8_t* kc, const int8_t* v
                                const float* vs, float* out, int pos, int n_heads, int n_kv_heads, int hs,
                                size_t t_stride, size_t head_stride, size_t s_t_stride, size_t s_head_stride);
 
+/* orc_attention_kv8 split over the context in S splits (S <= 64), in the
+ * float order of this build's split kernel (see oracle.c); same arguments
+ * plus S. */
+void orc_attention_kv8_split(const float* q, const int8_t* kc, const int8_t* vc, const float* ks,
+                             const float* vs, float* out, int pos, int n_heads, int n_kv_heads, int hs,
+                             size_t t_stride, size_t head_stride, size_t s_t_stride, size_t s_head_stride,
+                             int S);
+
 /* SwiGLU (runq.c:405-410); out may alias h. */
 void orc_swiglu(float* out, const float* h, const float* h2, int n);
 
@@ -97,6 +107,13 @@ void orc_model_free(orc_model* m);
  * orc_kv_quant and attention runs through orc_attention_kv8.  Returns 0, or
  * -1 when the caches cannot be allocated. */
 int orc_model_set_kv8(orc_model* m, int on);
+
+/* With the int8 KV cache: attention over more than `split_from` positions
+ * in the split order with `splits` splits (orc_attention_kv8_split), over
+ * fewer in orc_attention_kv8_ordered, as the GPU engine runs it; splits 0
+ * (the default) keeps orc_attention_kv8_ordered everywhere.  Returns 0, or
+ * -1 for splits outside 0..64. */
+int orc_model_set_kv8_splits(orc_model* m, int splits, int split_from);
 
 /* forward(token, pos) -> logits[vocab] (owned by the model).  If x_layers
  * is not NULL it receives the residual stream after the embedding and after

@@ -53,6 +53,8 @@ def olib():
             "orc_attention_kv8": (None, [P, P, P, P, P, P, I, I, I, I] + [C.c_size_t] * 4),
             "orc_model_set_kv8": (I, [P, I]),
             "orc_attention_kv8_ordered": (None, [P, P, P, P, P, P, I, I, I, I] + [C.c_size_t] * 4),
+            "orc_attention_kv8_split": (None, [P, P, P, P, P, P, I, I, I, I] + [C.c_size_t] * 4 + [I]),
+            "orc_model_set_kv8_splits": (I, [P, I, I]),
         }
         for n, (r, a) in sig.items():
             f = getattr(L, n)
@@ -142,10 +144,12 @@ def kv_quant(row: np.ndarray):
 
 
 def attention_kv8(q: np.ndarray, k8: np.ndarray, v8: np.ndarray, ks: np.ndarray, vs: np.ndarray, pos: int,
-                  n_heads: int, n_kv_heads: int, head_size: int, ordered: bool = False) -> np.ndarray:
-    """v5-cuda-fused/run.cu:350-410 (in double, or with ordered=True in the
-    GPU kernels' float order) over int8 caches laid out
-    [n_kv_heads][max_t][head_size] with scales [n_kv_heads][max_t]."""
+                  n_heads: int, n_kv_heads: int, head_size: int, ordered: bool = False,
+                  splits: int = 0) -> np.ndarray:
+    """v5-cuda-fused/run.cu:350-410 (in double, with ordered=True in the
+    one-workgroup GPU kernel's float order, with splits=S in the split
+    kernel's) over int8 caches laid out [n_kv_heads][max_t][head_size] with
+    scales [n_kv_heads][max_t]."""
     q = np.ascontiguousarray(q, dtype=np.float32)
     k8 = np.ascontiguousarray(k8, dtype=np.int8)
     v8 = np.ascontiguousarray(v8, dtype=np.int8)
@@ -153,9 +157,12 @@ def attention_kv8(q: np.ndarray, k8: np.ndarray, v8: np.ndarray, ks: np.ndarray,
     vs = np.ascontiguousarray(vs, dtype=np.float32)
     max_t = k8.shape[1]
     out = np.empty(n_heads * head_size, dtype=np.float32)
-    fn = olib().orc_attention_kv8_ordered if ordered else olib().orc_attention_kv8
-    fn(_p(q), _p(k8), _p(v8), _p(ks), _p(vs), _p(out), pos, n_heads, n_kv_heads, head_size,
-       head_size, max_t * head_size, 1, max_t)
+    args = (_p(q), _p(k8), _p(v8), _p(ks), _p(vs), _p(out), pos, n_heads, n_kv_heads, head_size,
+            head_size, max_t * head_size, 1, max_t)
+    if splits:
+        olib().orc_attention_kv8_split(*args, splits)
+    else:
+        (olib().orc_attention_kv8_ordered if ordered else olib().orc_attention_kv8)(*args)
     return out
 
 
@@ -178,7 +185,11 @@ def expf_host(x: np.ndarray) -> np.ndarray:
 class Oracle:
     """CPU restatement of forward() over a checkpoint image (host memory)."""
 
-    def __init__(self, cfg_list, weights: np.ndarray, wbits: int, group: int, max_t: int = 0, kv8: bool = False):
+    def __init__(self, cfg_list, weights: np.ndarray, wbits: int, group: int, max_t: int = 0, kv8: bool = False,
+                 kv8_splits: int = 0, kv8_split_from: int = 0):
+        """kv8: the int8 KV cache; kv8_splits > 0: its attention over more
+        than kv8_split_from positions in the split kernel's order with that
+        many splits (the one-workgroup order below, and everywhere with 0)."""
         self.cfg = list(cfg_list)
         self.dim, self.n_layers, self.vocab = self.cfg[0], self.cfg[2], self.cfg[5]
         self._w = weights   # keep the buffer alive
@@ -188,6 +199,8 @@ class Oracle:
             raise ValueError("oracle: weights image too short for the config")
         if kv8 and olib().orc_model_set_kv8(self._m, 1) != 0:
             raise MemoryError("oracle: int8 KV cache")
+        if kv8 and olib().orc_model_set_kv8_splits(self._m, kv8_splits, kv8_split_from) != 0:
+            raise ValueError("oracle: splits outside 0..64")
 
     def forward(self, token: int, pos: int, layers: bool = False):
         xl = np.empty((self.n_layers + 1, self.dim), dtype=np.float32) if layers else None

@@ -162,6 +162,17 @@ def test_gpu_library_exports_every_declared_symbol():
     assert set(names) <= set(abi.SIGNATURES), set(names) - set(abi.SIGNATURES)
 
 
+def test_abi_constants_equal_the_header_defines():
+    """Every L2Q_* integer the Python binding names equals the header's."""
+    text = open(os.path.join(REPO, "include", "l2q.h")).read()
+    defines = {k: int(v) for k, v in re.findall(r"#define\s+(L2Q_\w+)\s+(-?\d+)", text)}
+    names = [n for n in dir(abi) if n.startswith("L2Q_") and isinstance(getattr(abi, n), int)]
+    assert len(names) >= 10
+    for n in names:
+        assert n in defines, n
+        assert getattr(abi, n) == defines[n], n
+
+
 def test_missing_library_fails_loudly(monkeypatch):
     monkeypatch.setattr(abi, "_lib", None)
     monkeypatch.setattr(abi, "GPU_LIB", os.path.join(BUILD_DIR, "nonexistent.so"))

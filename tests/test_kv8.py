@@ -10,8 +10,12 @@ fails it; the oracle's restatement in the GPU kernels' float order agrees
 with the double one.  GPU parity: l2q_kv8_append is bit-exact (int8 rows
 and scales, RoPE included); l2q_attention_kv8 is within 2e-5 relative
 (floor: output RMS) of the double-precision oracle at the c4 shapes and
-bit-exact against the ordered restatement; the engine with
-L2Q_ENGINE_KV_INT8 reproduces the oracle's int8-KV forward bit for bit.
+bit-exact against the ordered restatement; its split-context form
+(l2q_attention_kv8_ex with L2Q_ATTN_SPLIT_CONTEXT, the engine's) is within
+the same 2e-5 and bit-exact against orc_attention_kv8_split, the oracle's
+restatement of its order; the engine with L2Q_ENGINE_KV_INT8 reproduces the
+oracle's int8-KV forward (in the split order, with the engine's split
+count) bit for bit.
 """
 import numpy as np
 import pytest
@@ -70,6 +74,42 @@ def test_attention_kv8_oracle_equals_fp32_attention_on_dequantized(n_heads, n_kv
     # the GPU-order float restatement agrees with the double one
     ordered = O.attention_kv8(q, k8, v8, ks, vs, pos, n_heads, n_kv, hs, ordered=True)
     assert_close(ordered, got, 2e-5, what="kv8 ordered vs double")
+
+
+@pytest.mark.parametrize("n_heads,n_kv,hs,pos,S", [
+    (6, 6, 48, 0, 64), (6, 6, 48, 70, 64), (8, 2, 64, 130, 16), (4, 4, 128, 255, 1), (4, 4, 128, 255, 2),
+    (4, 4, 128, 600, 8), (32, 8, 128, 1000, 16), (2, 2, 128, 4095, 16)])
+def test_attention_kv8_split_oracle_equals_double(n_heads, n_kv, hs, pos, S):
+    """The split restatement (the split kernel's float order: per-split
+    softmax partials merged in split order) is within 2e-5 of the double
+    oracle for one split, splits of one position, empty splits (S > n),
+    GQA and 4096 positions; the split order also differs from the
+    one-workgroup order's bits, so the two restatements are distinct."""
+    max_t = pos + 3
+    k8, v8, ks, vs = random_kv8(n_kv, max_t, hs, pos + hs + S)
+    q = host.gauss(n_heads * hs, pos, 4, 1.0)
+    ref = O.attention_kv8(q, k8, v8, ks, vs, pos, n_heads, n_kv, hs)
+    got = O.attention_kv8(q, k8, v8, ks, vs, pos, n_heads, n_kv, hs, splits=S)
+    assert_close(got, ref, 2e-5, what=f"kv8 split S={S} vs double")
+
+
+def test_attention_kv8_split_oracle_scale_invariances():
+    """Closed-form checks the double pin cannot separate: scaling every V
+    scale by 2 doubles the output exactly (powers of two commute with every
+    rounding), and adding a constant to every score (a K row equal for all
+    positions scaled per position is not constant, so use q = 0) gives the
+    uniform average of the dequantized V rows."""
+    n_heads = n_kv = 2
+    hs, pos, S = 64, 300, 16
+    k8, v8, ks, vs = random_kv8(n_kv, pos + 1, hs, 5)
+    q = host.gauss(n_heads * hs, 5, 4, 1.0)
+    a = O.attention_kv8(q, k8, v8, ks, vs, pos, n_heads, n_kv, hs, splits=S)
+    b = O.attention_kv8(q, k8, v8, ks, (vs * np.float32(2.0)).astype(np.float32), pos, n_heads, n_kv, hs, splits=S)
+    np.testing.assert_array_equal(b, a * np.float32(2.0))
+    z = O.attention_kv8(np.zeros_like(q), k8, v8, ks, vs, pos, n_heads, n_kv, hs, splits=S)
+    vd = (v8.astype(np.float64) * vs[:, :, None].astype(np.float64))[:, :pos + 1]
+    want = np.repeat(vd.mean(axis=1), n_heads // n_kv, axis=0).reshape(-1)
+    assert_close(z, want.astype(np.float32), 1e-5, what="uniform softmax")
 
 
 def test_oracle_kv8_forward_tracks_fp32_forward():
@@ -194,6 +234,46 @@ def test_gpu_attention_kv8(gpu_lib, torch_cuda, n_heads, n_kv, hs, max_t, ctx):
 
 
 @pytest.mark.gpu
+def flash_splits(n_heads, n, ncu):
+    """The library's split count for n positions (about two workgroups per
+    CU, at most 256 positions per split, 1..64 splits)."""
+    S = max(-(-2 * ncu // n_heads), -(-n // 256))
+    return min(max(S, 1), 64)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("n_heads,n_kv,hs,max_t,ctx", [(32, 32, 128, 4096, 1), (32, 32, 128, 4096, 64),
+                                                      (32, 32, 128, 4096, 257), (32, 32, 128, 4096, 1024),
+                                                      (32, 32, 128, 4096, 4096), (6, 6, 48, 256, 200),
+                                                      (8, 2, 64, 512, 333), (32, 8, 128, 8192, 8192),
+                                                      (2, 2, 256, 300, 300)])
+def test_gpu_attention_kv8_split(gpu_lib, torch_cuda, n_heads, n_kv, hs, max_t, ctx):
+    """The split-context form: 2e-5 of the double formula, and bit for bit
+    the oracle's restatement of its order (per-split softmax partials, one
+    to several 64-position rounds per split, empty splits, GQA, head sizes
+    48 to 256, 8192 positions); two calls in a row (the counters the first
+    leaves zeroed serve the second)."""
+    t = torch_cuda
+    print(f"attention kv8 split heads={n_heads}/{n_kv} hs={hs} ctx={ctx}", flush=True)
+    pos = ctx - 1
+    k8, v8, ks, vs = random_kv8(n_kv, max_t, hs, ctx + hs + 1)
+    q = host.gauss(n_heads * hs, ctx, 5, 1.0)
+    S = flash_splits(n_heads, ctx, t.cuda.get_device_properties(0).multi_processor_count)
+    ref = O.attention_kv8(q, k8, v8, ks, vs, pos, n_heads, n_kv, hs)
+    want = O.attention_kv8(q, k8, v8, ks, vs, pos, n_heads, n_kv, hs, splits=S)
+    out = t.empty(n_heads * hs, dtype=t.float32, device="cuda")
+    d = [dev(t, a) for a in (q, k8, v8, ks, vs)]
+    for rep in range(2):
+        out.fill_(np.nan)
+        abi.call("l2q_attention_kv8_ex", *[x.data_ptr() for x in d], out.data_ptr(), pos, n_heads, n_kv, hs, max_t,
+                 abi.L2Q_ATTN_SPLIT_CONTEXT, stream(t))
+        t.cuda.synchronize()
+        got = out.cpu().numpy()
+        assert_close(got, ref, 2e-5, what=f"attention kv8 split ctx={ctx} S={S}")
+        np.testing.assert_array_equal(got, want, err_msg=f"call {rep}, S={S}")
+
+
+@pytest.mark.gpu
 def test_gpu_attention_kv8_rejects_bad_shapes(gpu_lib, torch_cuda):
     t = torch_cuda
     buf = t.zeros(1 << 16, dtype=t.float32, device="cuda")
@@ -201,18 +281,28 @@ def test_gpu_attention_kv8_rejects_bad_shapes(gpu_lib, torch_cuda):
     for hs, max_t, pos in ((40, 64, 0), (128, 64, 64), (128, 9000, 0)):
         rc = abi.lib().l2q_attention_kv8(p, p, p, p, p, p, pos, 1, 1, hs, max_t, stream(t))
         assert rc == abi.L2Q_ERR_ARG
+        rc = abi.lib().l2q_attention_kv8_ex(p, p, p, p, p, p, pos, 1, 1, hs, max_t, abi.L2Q_ATTN_SPLIT_CONTEXT,
+                                            stream(t))
+        assert rc == abi.L2Q_ERR_ARG
+    assert abi.lib().l2q_attention_kv8_ex(p, p, p, p, p, p, 0, 1, 1, 128, 64, 2, stream(t)) == abi.L2Q_ERR_ARG
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize("shape", ["c1_q8_g32", "7b2_q4_g64", "gqa_hs64_q4_g32"])
+@pytest.mark.parametrize("shape", ["c1_q8_g32", "7b2_q4_g64", "gqa_hs64_q4_g32", "c1_q8_g32_long"])
 def test_gpu_engine_kv8_follows_oracle(gpu_lib, torch_cuda, shape):
     """Engine with the int8 KV cache against the oracle's int8-KV forward
-    (attention in the kernels' float order): logits bit for bit at every
-    step of a greedy decode, so the token ids are identical."""
+    (attention in the one-workgroup order up to L2Q_KV8_SPLIT_FROM positions
+    and in the split order with the engine's split count beyond): logits bit
+    for bit at every step of a greedy decode, so the token ids are
+    identical; the long case crosses the switch (positions 0..1099)."""
     from llama2q.model import Engine
     if shape == "c1_q8_g32":
         ck = host.synth_checkpoint(host.config_15m(), 8, 32, seed=21)
         steps = 64
+    elif shape == "c1_q8_g32_long":   # c1's widths, two layers, a 2048-position context
+        cfg = host.make_config(288, 768, 2, 6, 6, 512, 2048)
+        ck = host.synth_checkpoint(cfg, 8, 32, seed=25)
+        steps = 1100
     elif shape == "gqa_hs64_q4_g32":   # 4 heads over 2 kv heads: the group's first head appends
         cfg = host.make_config(256, 512, 2, 4, 2, 512, 64)
         ck = host.synth_checkpoint(cfg, 4, 32, seed=24, q4_divisor=7.0)
@@ -222,8 +312,10 @@ def test_gpu_engine_kv8_follows_oracle(gpu_lib, torch_cuda, shape):
         ck = host.synth_checkpoint(cfg, 4, 64, seed=22, q4_divisor=7.0)
         steps = 12
     print(f"engine kv8 {shape}", flush=True)
-    orc = O.Oracle(ck.cfg.as_list(), ck.weights, ck.wbits, ck.group, max_t=steps, kv8=True)
     eng = Engine(ck, max_steps=steps, kv8=True)
+    assert eng.attention_splits > 0
+    orc = O.Oracle(ck.cfg.as_list(), ck.weights, ck.wbits, ck.group, max_t=steps, kv8=True,
+                   kv8_splits=eng.attention_splits, kv8_split_from=abi.L2Q_KV8_SPLIT_FROM)
     token = 3
     for pos in range(steps):
         lo = orc.forward(token, pos)
