@@ -604,18 +604,39 @@ __global__ __launch_bounds__(kSbThreads) void k_attn_scores_b(
     if (t0 > pos0 + min(q0 + kSbQueries, T) - 1) return;
     const int g = h / kv_mul, f4 = hs / 4;
     const int nt = min(kSbKeys, nk - t0);
-    for (int f = tid; f < kSbKeys * f4; f += kSbThreads) {
-        int r, c4;
+    // the tile's and the q block's loads in batches of four per thread, all
+    // of a batch in flight before its stores (clamped indices; a load per
+    // iteration followed by its store would wait one memory latency each)
+    const int nkf = kSbKeys * f4, nqf = kSbQueries * f4;
+    auto k_addr = [&](int f, int& r, int& c4) {
+        f = min(f, nkf - 1);
         if (k_il) { c4 = f / kSbKeys; r = f - c4 * kSbKeys; }   // consecutive lanes, consecutive keys
         else { r = f / f4; c4 = f - r * f4; }
-        const float4 v = *reinterpret_cast<const float4*>(kcache + k_index(k_il, g, t0 + min(r, nt - 1), 4 * c4, hs, max_t));
-        *reinterpret_cast<float4*>(kt + r * hsp + 4 * c4) = v;
+        return reinterpret_cast<const float4*>(kcache + k_index(k_il, g, t0 + min(r, nt - 1), 4 * c4, hs, max_t));
+    };
+    for (int b = 0; b < nkf; b += 4 * kSbThreads) {
+        int r0, c0, r1, c1, r2, c2, r3, c3;
+        const float4 v0 = *k_addr(b + tid, r0, c0), v1 = *k_addr(b + tid + kSbThreads, r1, c1);
+        const float4 v2 = *k_addr(b + tid + 2 * kSbThreads, r2, c2), v3 = *k_addr(b + tid + 3 * kSbThreads, r3, c3);
+        if (b + tid < nkf) *reinterpret_cast<float4*>(kt + r0 * hsp + 4 * c0) = v0;
+        if (b + tid + kSbThreads < nkf) *reinterpret_cast<float4*>(kt + r1 * hsp + 4 * c1) = v1;
+        if (b + tid + 2 * kSbThreads < nkf) *reinterpret_cast<float4*>(kt + r2 * hsp + 4 * c2) = v2;
+        if (b + tid + 3 * kSbThreads < nkf) *reinterpret_cast<float4*>(kt + r3 * hsp + 4 * c3) = v3;
     }
-    for (int f = tid; f < kSbQueries * f4; f += kSbThreads) {
-        const int r = f / f4, c4 = f - r * f4;
-        const float4 v = *reinterpret_cast<const float4*>(q + (size_t)min(q0 + r, T - 1) * q_stride +
-                                                          (size_t)h * hs + 4 * c4);
-        *reinterpret_cast<float4*>(qs + r * hsp + 4 * c4) = v;
+    auto q_addr = [&](int f) {
+        f = min(f, nqf - 1);
+        return reinterpret_cast<const float4*>(q + (size_t)min(q0 + f / f4, T - 1) * q_stride + (size_t)h * hs +
+                                               4 * (f % f4));
+    };
+    for (int b = 0; b < nqf; b += 4 * kSbThreads) {
+        const float4 v0 = *q_addr(b + tid), v1 = *q_addr(b + tid + kSbThreads);
+        const float4 v2 = *q_addr(b + tid + 2 * kSbThreads), v3 = *q_addr(b + tid + 3 * kSbThreads);
+        const float4 vv[4] = {v0, v1, v2, v3};
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+            const int f = b + tid + k * kSbThreads;
+            if (f < nqf) *reinterpret_cast<float4*>(qs + (f / f4) * hsp + 4 * (f % f4)) = vv[k];
+        }
     }
     __syncthreads();
     const int tl = tid % kSbKeys, qg = tid / kSbKeys;
@@ -623,23 +644,34 @@ __global__ __launch_bounds__(kSbThreads) void k_attn_scores_b(
     float sc[kSbPer];
 #pragma unroll
     for (int j = 0; j < kSbPer; j++) sc[j] = 0.0f;
-    const int nv = (hs & ~7) >> 2;   // float4 blocks added unfused
-    for (int c = 0; c < f4; c++) {
+    const int nv = (hs & ~7) >> 2;   // float4 blocks added unfused, then the fused rest
+    const float4* qb = reinterpret_cast<const float4*>(qs + qg * kSbPer * hsp);
+    const int qp = hsp / 4;          // q row pitch in float4
+    for (int c = 0; c < nv; c++) {
+        // the step's LDS reads issued together, then the adds
         const float4 kv = k4[c];
+        float4 qv[kSbPer];
+#pragma unroll
+        for (int j = 0; j < kSbPer; j++) qv[j] = qb[j * qp + c];
 #pragma unroll
         for (int j = 0; j < kSbPer; j++) {
-            const float4 qv = reinterpret_cast<const float4*>(qs + (qg * kSbPer + j) * hsp)[c];
-            if (c < nv) {
-                sc[j] = sc[j] + qv.x * kv.x;
-                sc[j] = sc[j] + qv.y * kv.y;
-                sc[j] = sc[j] + qv.z * kv.z;
-                sc[j] = sc[j] + qv.w * kv.w;
-            } else {
-                sc[j] = __builtin_fmaf(qv.x, kv.x, sc[j]);
-                sc[j] = __builtin_fmaf(qv.y, kv.y, sc[j]);
-                sc[j] = __builtin_fmaf(qv.z, kv.z, sc[j]);
-                sc[j] = __builtin_fmaf(qv.w, kv.w, sc[j]);
-            }
+            sc[j] = sc[j] + qv[j].x * kv.x;
+            sc[j] = sc[j] + qv[j].y * kv.y;
+            sc[j] = sc[j] + qv[j].z * kv.z;
+            sc[j] = sc[j] + qv[j].w * kv.w;
+        }
+    }
+    for (int c = nv; c < f4; c++) {
+        const float4 kv = k4[c];
+        float4 qv[kSbPer];
+#pragma unroll
+        for (int j = 0; j < kSbPer; j++) qv[j] = qb[j * qp + c];
+#pragma unroll
+        for (int j = 0; j < kSbPer; j++) {
+            sc[j] = __builtin_fmaf(qv[j].x, kv.x, sc[j]);
+            sc[j] = __builtin_fmaf(qv[j].y, kv.y, sc[j]);
+            sc[j] = __builtin_fmaf(qv[j].z, kv.z, sc[j]);
+            sc[j] = __builtin_fmaf(qv[j].w, kv.w, sc[j]);
         }
     }
     const int t = t0 + tl;
@@ -668,10 +700,18 @@ __global__ __launch_bounds__(kSmThreads) void k_attn_softmax_b(float* __restrict
     const int n = pos0 + qi + 1;
     float* row = scores + ((size_t)qi * n_heads + h) * max_t;
     float m = -INFINITY;
-    for (int t = lane; t < n; t += kSmThreads) {
-        const float v = row[t];
-        p[t] = v;
-        m = fmaxf(m, v);
+    for (int t0 = 0; t0 < n; t0 += 8 * kSmThreads) {   // eight loads in flight per lane
+        float v[8];
+#pragma unroll
+        for (int k = 0; k < 8; k++) v[k] = row[min(t0 + lane + kSmThreads * k, n - 1)];
+#pragma unroll
+        for (int k = 0; k < 8; k++) {
+            const int t = t0 + lane + kSmThreads * k;
+            if (t < n) {
+                p[t] = v[k];
+                m = fmaxf(m, v[k]);
+            }
+        }
     }
     m = group_max<L2Q_WAVE>(m);
     for (int t = lane; t < n; t += kSmThreads) p[t] = exp_runq(p[t] - m);
