@@ -777,7 +777,24 @@ __global__ __launch_bounds__(kPvThreads) void k_attn_pv_b(const float* __restric
         if (c + 1 < nchunks) fetch(c + 1);
         const int tn = min(kPvKeys, n - c * kPvKeys);   // this thread's keys in the chunk
         const float* pr = pt + ql * kPvPitch;
-        for (int t = 0; t < tn; t++) {
+        int t = 0;
+        for (; t + 8 <= tn; t += 8) {   // a block's LDS reads issued together, then its chains
+            float pv[8];
+            float4 v[8];
+#pragma unroll
+            for (int k = 0; k < 8; k++) {
+                pv[k] = pr[t + k];
+                v[k] = vt[t + k][quad];
+            }
+#pragma unroll
+            for (int k = 0; k < 8; k++) {
+                acc.x = __builtin_fmaf(pv[k], v[k].x, acc.x);
+                acc.y = __builtin_fmaf(pv[k], v[k].y, acc.y);
+                acc.z = __builtin_fmaf(pv[k], v[k].z, acc.z);
+                acc.w = __builtin_fmaf(pv[k], v[k].w, acc.w);
+            }
+        }
+        for (; t < tn; t++) {
             const float pv = pr[t];
             const float4 v = vt[t][quad];
             acc.x = __builtin_fmaf(pv, v.x, acc.x);
