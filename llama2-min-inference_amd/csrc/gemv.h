@@ -92,8 +92,11 @@ __host__ __device__ constexpr int gemv_sweeps(int bits, int cols) { return (cols
 // One workgroup of 8 waves (2 per SIMD) per CU: the workgroup-wide prologue
 // is then shared by every wave of the CU instead of being recomputed by
 // several workgroups.  (12 waves for short rows measured ~1% slower in the
-// decode step: a 4096-row matrix then fills only 171 of the 256 CUs.)
+// decode step: a 4096-row matrix then fills only 171 of the 256 CUs.)  Rows
+// of two sweeps may run 11 waves where that fills the grid's last round of
+// units better (see go_gemv).
 __host__ __device__ constexpr int gemv_waves(int) { return 8; }
+constexpr int kGemvWavesWide = 11;
 
 // Rows folded at once per wave (F lanes run F ordered FMA chains side by
 // side): the fold's instructions are issued for the whole wave whatever the
@@ -144,8 +147,9 @@ __host__ __device__ constexpr size_t gemv_fold_floats(int nb, int waves) {
 // SIMD; the INT4 form is stored pre-split per 32-element chunk as
 // [even-column dwords E0..E3 | odd-column dwords O0..O3] (see act_split_addr).
 __host__ __device__ constexpr bool gemv_act_lds(int NS) { return NS > 4; }
-__host__ __device__ constexpr size_t gemv_lds_bytes(int pro, int cols, int group, int bits, int PR) {
-    return gemv_fold_floats(cols / group, gemv_waves(gemv_sweeps(bits, cols))) * sizeof(float) +
+__host__ __device__ constexpr size_t gemv_lds_bytes(int pro, int cols, int group, int bits, int PR,
+                                                    int waves = gemv_waves(0)) {
+    return gemv_fold_floats(cols / group, waves) * sizeof(float) +
            (pro == kPreq && !gemv_act_lds(gemv_sweeps(bits, cols))
                 ? 0
                 : (size_t)(cols + 31) / 32 * 32 + (size_t)(cols / group + 3) / 4 * 16) +
@@ -552,9 +556,9 @@ __device__ __forceinline__ void wave_lds_sync() {
 // (F/PR units) are collected before one ordered fold on F lanes.  A wave
 // without units loads row 0 (never used), so every path issues the same
 // loads and no wait covers younger loads than it must.
-template <int BITS, int G, int NS, int PRO, int EPI, int PR>
-__global__ __launch_bounds__(gemv_waves(NS) * L2Q_WAVE) void k_gemv(GemvArgs a) {
-    constexpr int WAVES = gemv_waves(NS);
+template <int BITS, int G, int NS, int PRO, int EPI, int PR, int W>
+__global__ __launch_bounds__(W * L2Q_WAVE) void k_gemv(GemvArgs a) {
+    constexpr int WAVES = W;
     constexpr int THREADS = WAVES * L2Q_WAVE;
     static_assert(PR == gemv_unit_rows(NS, EPI), "unit size");
     using C = Chunk<BITS, G>;

@@ -90,19 +90,45 @@ static int raise_lds_limit(const void* fn, size_t lds, const char* what) {
 constexpr int kGemvBlocksPerCu = 1;
 constexpr size_t kGemvMaxLds = 160 * 1024;   // gfx950 LDS per workgroup
 
-template <int BITS, int G, int NS, int PRO, int EPI>
-static int go_gemv(const GemvArgs& a, hipStream_t st) {
+template <int BITS, int G, int NS, int PRO, int EPI, int W>
+static int go_gemv_w(const GemvArgs& a, hipStream_t st) {
     constexpr int PR = gemv_unit_rows(NS, EPI);
-    const size_t lds = gemv_lds_bytes(PRO, a.cols, G, BITS, PR);
-    constexpr int W = gemv_waves(NS);
-    const void* fn = reinterpret_cast<const void*>(&k_gemv<BITS, G, NS, PRO, EPI, PR>);
+    const size_t lds = gemv_lds_bytes(PRO, a.cols, G, BITS, PR, W);
+    const void* fn = reinterpret_cast<const void*>(&k_gemv<BITS, G, NS, PRO, EPI, PR, W>);
     if (int rc = raise_lds_limit(fn, lds, "gemv: raising the LDS limit")) return rc;
     const int maxb = resident_blocks(fn, W * L2Q_WAVE, lds, kGemvBlocksPerCu);
     const int nunits = (a.rows + PR - 1) / PR;
     int blocks = (nunits + W - 1) / W;
     if (blocks > maxb) blocks = maxb;
-    hipLaunchKernelGGL((k_gemv<BITS, G, NS, PRO, EPI, PR>), dim3(blocks), dim3(W * L2Q_WAVE), lds, st, a);
+    hipLaunchKernelGGL((k_gemv<BITS, G, NS, PRO, EPI, PR, W>), dim3(blocks), dim3(W * L2Q_WAVE), lds, st, a);
     return check_launch("gemv");
+}
+
+// Share of the grid's wave-rounds that carry a unit when `waves` waves
+// (one workgroup per CU) deal `units` units round-robin: the last round
+// runs only the remainder.
+static double gemv_round_fill(long units, long waves) {
+    const long rounds = (units + waves - 1) / waves;
+    return rounds ? (double)units / (double)(rounds * waves) : 1.0;
+}
+
+template <int BITS, int G, int NS, int PRO, int EPI>
+static int go_gemv(const GemvArgs& a, hipStream_t st) {
+    if constexpr (NS == 2) {
+        // rows of two sweeps: 11 waves per CU where that fills the last round
+        // of units clearly better than 8 (the 7B w1|w3 GEMV: 11008 units,
+        // 0.90 of the rounds busy with 8 waves, 0.98 with 11)
+        constexpr int PR = gemv_unit_rows(NS, EPI);
+        int dev = 0, cus = 0;
+        if (hipGetDevice(&dev) != hipSuccess ||
+            hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus < 1)
+            cus = 256;
+        const long units = (a.rows + PR - 1) / PR;
+        if (units > (long)cus * gemv_waves(NS) &&
+            gemv_round_fill(units, (long)cus * kGemvWavesWide) > gemv_round_fill(units, (long)cus * gemv_waves(NS)) + 0.05)
+            return go_gemv_w<BITS, G, NS, PRO, EPI, kGemvWavesWide>(a, st);
+    }
+    return go_gemv_w<BITS, G, NS, PRO, EPI, gemv_waves(NS)>(a, st);
 }
 
 template <int BITS, int G, int PRO, int EPI>
