@@ -174,6 +174,40 @@ __device__ __forceinline__ float q8_bias_term(float s, int sumq) {
     return s * 128.0f * (float)sumq;
 }
 
+// The batched-prefill GEMM operand of quantized activations: xqp holds q in
+// the MFMA chunk order (INT4 weights: per chunk of G/4 columns, the odd
+// columns then the even ones; INT8: natural order), sq the sum of each
+// group's q and xt its bias term q8_bias_term(xs, sq).  Producers that
+// quantize write it directly (xqp == nullptr: not wanted).
+struct PfOperand {
+    int8_t* xqp;
+    int* sq;
+    float* xt;
+    int bits;
+};
+
+// Emit element i (of a flattened [T][K] activation, K % G == 0) with value
+// q and group scale s.  Every lane of the wave calls it together, element i
+// on lane i % 64 with its group's G lanes consecutive; `in` false marks a
+// lane past the end, which contributes 0 and stores nothing.
+template <int G>
+__device__ __forceinline__ void pf_emit(const PfOperand& p, size_t i, int q, float s, bool in) {
+    const int sum = group_isum<G>(in ? q : 0);   // exact in any order
+    if (!in) return;
+    constexpr int CH = G / 4;
+    const int j = (int)(i % G);
+    int pj = j;
+    if (p.bits == 4) {
+        const int jj = j % CH;
+        pj = j - jj + ((jj & 1) ? jj / 2 : CH / 2 + jj / 2);
+    }
+    p.xqp[i - j + pj] = (int8_t)q;
+    if (j == 0) {
+        p.sq[i / G] = sum;
+        p.xt[i / G] = q8_bias_term(s, sum);
+    }
+}
+
 // runq.c:155 for one group, as GCC -O3 -march=native compiles it (two FMAs):
 //   sum = fma(ws, t, sum),  t = fma(xs, (float)d_u8, -xt),  d_u8 = d + 128*sum(q)
 // d_u8 is the dot the reference's VPDPBUSD produces on +128-biased weights;

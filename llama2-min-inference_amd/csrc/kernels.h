@@ -17,15 +17,18 @@ __device__ __forceinline__ int meta_pos(const int* meta, int pos) { return meta 
 // ---------------------------------------------------------------------------
 // Q8 quantize (runq.c:117-139).  One thread per element, groups of G
 // consecutive lanes (G divides 64, so a group never straddles a wave).
+// pf.xqp set: also the prefill GEMM operand (pf_emit); xq may then be null.
 template <int G>
 __global__ __launch_bounds__(256) void k_quantize(const float* __restrict__ x, int n,
-                                                  int8_t* __restrict__ xq, float* __restrict__ xs) {
+                                                  int8_t* __restrict__ xq, float* __restrict__ xs, PfOperand pf) {
     const int i = blockIdx.x * blockDim.x + threadIdx.x;
     const bool in = i < n;
     const float v = in ? x[i] : 0.0f;
     const float s = q8_scale(group_max<G>(fabsf(v)));
+    const int q = q8_value_fast(v, s, q8_recip(s));
+    if (pf.xqp) pf_emit<G>(pf, i, q, s, in);
     if (in) {
-        xq[i] = (int8_t)q8_value_fast(v, s, q8_recip(s));
+        if (xq) xq[i] = (int8_t)q;
         if ((i % G) == 0) xs[i / G] = s;
     }
 }
@@ -47,7 +50,7 @@ template <int G>
 __global__ __launch_bounds__(kNormThreads) void k_rmsnorm_quant(
     const float* __restrict__ x, const float* __restrict__ emb, const int* __restrict__ meta,
     const float* __restrict__ resid, float* __restrict__ xout, const float* __restrict__ w, int n,
-    int8_t* __restrict__ xq, float* __restrict__ xs) {
+    int8_t* __restrict__ xq, float* __restrict__ xs, PfOperand pf) {
     __shared__ float vs[kNormThreads * kNormMaxPer];
     __shared__ float inv_s;
     const int tid = threadIdx.x;
@@ -57,8 +60,13 @@ __global__ __launch_bounds__(kNormThreads) void k_rmsnorm_quant(
         x += to;
         if (resid) resid += to;
         if (xout) xout += to;
-        xq += to;
+        if (xq) xq += to;
         xs += to / G;
+        if (pf.xqp) {
+            pf.xqp += to;
+            pf.sq += to / G;
+            pf.xt += to / G;
+        }
     }
     const float* src = emb ? emb + (size_t)meta[0] * n : x;
     float v[kNormMaxPer];
@@ -87,9 +95,11 @@ __global__ __launch_bounds__(kNormThreads) void k_rmsnorm_quant(
         const bool in = i < n;
         const float o = in ? w[i] * (inv * v[k]) : 0.0f;
         const float s = q8_scale(group_max<G>(fabsf(o)));
+        const int q = q8_value_fast(o, s, q8_recip(s));
+        if (pf.xqp) pf_emit<G>(pf, i, q, s, in);
         if (in) {
             if (xout) xout[i] = v[k];
-            xq[i] = (int8_t)q8_value_fast(o, s, q8_recip(s));
+            if (xq) xq[i] = (int8_t)q;
             if ((i % G) == 0) xs[i / G] = s;
         }
     }

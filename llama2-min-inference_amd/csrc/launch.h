@@ -21,13 +21,16 @@ int check_launch(const char* what);             // hipGetLastError after a launc
 int launch_gemv_fused(int bits, int group, int pro, int epi, const GemvArgs& a, hipStream_t st);
 int launch_gemv(int bits, int group, const GemvArgs& a, hipStream_t st);   // kPreq + kStore
 
-int launch_quantize(const float* x, int n, int group, int8_t* xq, float* xs, hipStream_t st);
+// pf (optional): also write the batched-prefill GEMM operand (PfOperand,
+// device.h), replacing launch_pf_prep; xq may then be null.
+int launch_quantize(const float* x, int n, int group, int8_t* xq, float* xs, hipStream_t st,
+                    const PfOperand* pf = nullptr);
 
 // emb/meta: layer-0 form (x = emb[meta[0]]); otherwise x.
 // T > 1: T consecutive vectors of n (x, resid, xout, xq rows of n; xs rows of n/group).
 int launch_rmsnorm_quant(const float* x, const float* emb, const int* meta, const float* resid,
                          float* xout, const float* w, int n, int group, int8_t* xq, float* xs,
-                         hipStream_t st, int T = 1);
+                         hipStream_t st, int T = 1, const PfOperand* pf = nullptr);
 
 int launch_swiglu_quant(const float* hb, const float* hb2, int n, int group, int8_t* xq, float* xs,
                         float* gout, hipStream_t st);
@@ -104,7 +107,8 @@ int launch_pf_prep(int bits, int group, const int8_t* xq, const float* xs, int K
 int launch_pf_gemm(int bits, int group, const void* w, const float* ws, int rows, int cols, const int8_t* xqp,
                    const float* xs, const int* sq, const float* xt, int T, float* out, int ldo, hipStream_t st);
 int launch_pf_embed(const float* emb, const int* tokens, float* x, int dim, int T, hipStream_t st);
-int launch_pf_swiglu_quant(const float* h13, int n, int T, int group, int8_t* xq, float* xs, hipStream_t st);
+int launch_pf_swiglu_quant(const float* h13, int n, int T, int group, int8_t* xq, float* xs, hipStream_t st,
+                           const PfOperand* pf = nullptr);
 
 int launch_argmax(const float* v, int n, int* out, hipStream_t st);
 

@@ -205,25 +205,45 @@ int launch_gemv(int bits, int group, const GemvArgs& a, hipStream_t st) {
 
 // ---------------------------------------------------------------------------
 
-int launch_quantize(const float* x, int n, int group, int8_t* xq, float* xs, hipStream_t st) {
+// The optional prefill operand of a producer: checked, or all null.
+static int pf_operand(const PfOperand* pf, int8_t* xq, PfOperand* out, const char* what) {
+    *out = PfOperand{nullptr, nullptr, nullptr, 8};
+    if (!pf) {
+        if (!xq) { set_error("%s: no output", what); return L2Q_ERR_ARG; }
+        return L2Q_OK;
+    }
+    if (!pf->xqp || !pf->sq || !pf->xt || (pf->bits != 4 && pf->bits != 8)) {
+        set_error("%s: bad prefill operand (bits=%d)", what, pf->bits);
+        return L2Q_ERR_ARG;
+    }
+    *out = *pf;
+    return L2Q_OK;
+}
+
+int launch_quantize(const float* x, int n, int group, int8_t* xq, float* xs, hipStream_t st, const PfOperand* pf) {
     if (n <= 0 || (group != 32 && group != 64) || n % group) { set_error("quantize: bad n=%d group=%d", n, group); return L2Q_ERR_ARG; }
+    PfOperand po;
+    if (int rc = pf_operand(pf, xq, &po, "quantize")) return rc;
     const int blocks = (n + 255) / 256;
-    if (group == 32) hipLaunchKernelGGL(k_quantize<32>, dim3(blocks), dim3(256), 0, st, x, n, xq, xs);
-    else hipLaunchKernelGGL(k_quantize<64>, dim3(blocks), dim3(256), 0, st, x, n, xq, xs);
+    if (group == 32) hipLaunchKernelGGL(k_quantize<32>, dim3(blocks), dim3(256), 0, st, x, n, xq, xs, po);
+    else hipLaunchKernelGGL(k_quantize<64>, dim3(blocks), dim3(256), 0, st, x, n, xq, xs, po);
     return check_launch("quantize");
 }
 
 int launch_rmsnorm_quant(const float* x, const float* emb, const int* meta, const float* resid, float* xout,
-                         const float* w, int n, int group, int8_t* xq, float* xs, hipStream_t st, int T) {
+                         const float* w, int n, int group, int8_t* xq, float* xs, hipStream_t st, int T,
+                         const PfOperand* pf) {
     if (n <= 0 || n > kNormThreads * kNormMaxPer || (group != 32 && group != 64) || n % group || T < 1 ||
         (T > 1 && emb)) {
         set_error("rmsnorm_quant: bad n=%d group=%d T=%d", n, group, T);
         return L2Q_ERR_ARG;
     }
+    PfOperand po;
+    if (int rc = pf_operand(pf, xq, &po, "rmsnorm_quant")) return rc;
     if (group == 32)
-        hipLaunchKernelGGL(k_rmsnorm_quant<32>, dim3(T), dim3(kNormThreads), 0, st, x, emb, meta, resid, xout, w, n, xq, xs);
+        hipLaunchKernelGGL(k_rmsnorm_quant<32>, dim3(T), dim3(kNormThreads), 0, st, x, emb, meta, resid, xout, w, n, xq, xs, po);
     else
-        hipLaunchKernelGGL(k_rmsnorm_quant<64>, dim3(T), dim3(kNormThreads), 0, st, x, emb, meta, resid, xout, w, n, xq, xs);
+        hipLaunchKernelGGL(k_rmsnorm_quant<64>, dim3(T), dim3(kNormThreads), 0, st, x, emb, meta, resid, xout, w, n, xq, xs, po);
     return check_launch("rmsnorm_quant");
 }
 
@@ -539,12 +559,15 @@ int launch_pf_embed(const float* emb, const int* tokens, float* x, int dim, int 
     return check_launch("prefill_embed");
 }
 
-int launch_pf_swiglu_quant(const float* h13, int n, int T, int group, int8_t* xq, float* xs, hipStream_t st) {
+int launch_pf_swiglu_quant(const float* h13, int n, int T, int group, int8_t* xq, float* xs, hipStream_t st,
+                           const PfOperand* pf) {
     if (n <= 0 || n % group || (group != 32 && group != 64)) { set_error("prefill swiglu: bad n=%d", n); return L2Q_ERR_ARG; }
+    PfOperand po;
+    if (int rc = pf_operand(pf, xq, &po, "prefill swiglu")) return rc;
     const size_t total = (size_t)T * n;
     const unsigned blocks = (unsigned)((total + 255) / 256);
-    if (group == 32) hipLaunchKernelGGL(k_pf_swiglu_quant<32>, dim3(blocks), dim3(256), 0, st, h13, n, T, xq, xs);
-    else hipLaunchKernelGGL(k_pf_swiglu_quant<64>, dim3(blocks), dim3(256), 0, st, h13, n, T, xq, xs);
+    if (group == 32) hipLaunchKernelGGL(k_pf_swiglu_quant<32>, dim3(blocks), dim3(256), 0, st, h13, n, T, xq, xs, po);
+    else hipLaunchKernelGGL(k_pf_swiglu_quant<64>, dim3(blocks), dim3(256), 0, st, h13, n, T, xq, xs, po);
     return check_launch("prefill_swiglu_quant");
 }
 

@@ -335,10 +335,12 @@ __global__ void k_pf_embed(const float* __restrict__ emb, const int* __restrict_
 }
 
 // SwiGLU + Q8 quantize of T tokens from interleaved (w1, w3) rows:
-// h13 [T][2n] -> xq [T][n], xs [T][n/G], as k_swiglu_quant per token.
+// h13 [T][2n] -> xq [T][n], xs [T][n/G], as k_swiglu_quant per token
+// (pf.xqp set: also the GEMM operand, pf_emit; xq may then be null).
 template <int G>
 __global__ __launch_bounds__(256) void k_pf_swiglu_quant(const float* __restrict__ h13, int n, int T,
-                                                         int8_t* __restrict__ xq, float* __restrict__ xs) {
+                                                         int8_t* __restrict__ xq, float* __restrict__ xs,
+                                                         PfOperand pf) {
     const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;   // element of the flattened [T][n]
     const bool in = i < (size_t)T * n;
     float g = 0.0f;
@@ -349,8 +351,10 @@ __global__ __launch_bounds__(256) void k_pf_swiglu_quant(const float* __restrict
         g = h * h13[t * 2 * n + 2 * j + 1];
     }
     const float s = q8_scale(group_max<G>(fabsf(g)));
+    const int q = q8_value_fast(g, s, q8_recip(s));
+    if (pf.xqp) pf_emit<G>(pf, i, q, s, in);
     if (in) {
-        xq[i] = (int8_t)q8_value_fast(g, s, q8_recip(s));
+        if (xq) xq[i] = (int8_t)q;
         if ((i % G) == 0) xs[i / G] = s;
     }
 }
