@@ -174,38 +174,51 @@ __device__ __forceinline__ float q8_bias_term(float s, int sumq) {
     return s * 128.0f * (float)sumq;
 }
 
-// The batched-prefill GEMM operand of quantized activations: xqp holds q in
-// the MFMA chunk order (INT4 weights: per chunk of G/4 columns, the odd
-// columns then the even ones; INT8: natural order), sq the sum of each
-// group's q and xt its bias term q8_bias_term(xs, sq).  Producers that
+// The batched-prefill GEMM operand of quantized activations [T][K]: xqp
+// holds q in the MFMA chunk order (INT4 weights: per chunk of G/4 columns,
+// the odd columns then the even ones; INT8: natural order) and rec [K/G][T]
+// one 32-byte record per (group, token), pf_record.  Producers that
 // quantize write it directly (xqp == nullptr: not wanted).
-struct PfOperand {
-    int8_t* xqp;
-    int* sq;
-    float* xt;
-    int bits;
+struct PfRecord {
+    int4 c;     // the MFMA accumulator input, four copies
+    float4 s;   // xs, xt, 0, 0
 };
 
-// Emit element i (of a flattened [T][K] activation, K % G == 0) with value
-// q and group scale s.  Every lane of the wave calls it together, element i
-// on lane i % 64 with its group's G lanes consecutive; `in` false marks a
-// lane past the end, which contributes 0 and stores nothing.
+struct PfOperand {
+    int8_t* xqp;
+    PfRecord* rec;
+    int bits;
+    int K;
+    int T;
+};
+
+// The record: xt = q8_bias_term(xs, sum(q)) (runq.c:137) and c =
+// 128*sum(q), the MFMA's accumulator input, so that D = d + 128*sum(q)
+// comes out of the MFMA.  INT4 weights enter the MFMA as 16x their value,
+// so there c is 16x as well and D >> 4 (exact: D is a multiple of 16) is
+// the dot.
+__device__ __forceinline__ PfRecord pf_record(float xs, int sumq, int bits) {
+    const int c = sumq * (bits == 4 ? 2048 : 128);
+    return PfRecord{make_int4(c, c, c, c), make_float4(xs, q8_bias_term(xs, sumq), 0.0f, 0.0f)};
+}
+
+// Emit element i of token t (i < K, K % G == 0) with value q and group scale
+// s.  Every lane of the wave calls it together, with each group's G elements
+// on G consecutive lanes; `in` false marks a lane past the end, which
+// contributes 0 and stores nothing.
 template <int G>
-__device__ __forceinline__ void pf_emit(const PfOperand& p, size_t i, int q, float s, bool in) {
+__device__ __forceinline__ void pf_emit(const PfOperand& p, int t, int i, int q, float s, bool in) {
     const int sum = group_isum<G>(in ? q : 0);   // exact in any order
     if (!in) return;
     constexpr int CH = G / 4;
-    const int j = (int)(i % G);
+    const int j = i % G;
     int pj = j;
     if (p.bits == 4) {
         const int jj = j % CH;
         pj = j - jj + ((jj & 1) ? jj / 2 : CH / 2 + jj / 2);
     }
-    p.xqp[i - j + pj] = (int8_t)q;
-    if (j == 0) {
-        p.sq[i / G] = sum;
-        p.xt[i / G] = q8_bias_term(s, sum);
-    }
+    p.xqp[(size_t)t * p.K + (i - j + pj)] = (int8_t)q;
+    if (j == 0) p.rec[(size_t)(i / G) * p.T + t] = pf_record(s, sum, p.bits);
 }
 
 // runq.c:155 for one group, as GCC -O3 -march=native compiles it (two FMAs):

@@ -93,9 +93,10 @@ struct l2q_engine {
     // batched prefill (allocated at the first l2q_engine_prefill): T tokens per chunk
     char* pfarena = nullptr;
     int pf_T = 0;
-    float *pf_xa, *pf_xb, *pf_qkv, *pf_att, *pf_wo, *pf_h13, *pf_ffn, *pf_scores, *pf_xs, *pf_xt;
+    float *pf_xa, *pf_xb, *pf_qkv, *pf_att, *pf_wo, *pf_h13, *pf_ffn, *pf_scores;
     int8_t* pf_xqp;
-    int *pf_sq, *pf_tok;
+    l2q::PfRecord* pf_rec;
+    int* pf_tok;
 };
 
 using namespace l2q;
@@ -552,16 +553,14 @@ int prefill_alloc(l2q_engine* e) {
     const size_t o_xa = a.take(T * d * 4), o_xb = a.take(T * d * 4), o_qkv = a.take(T * qkv * 4);
     const size_t o_att = a.take(T * d * 4), o_wo = a.take(T * d * 4), o_h13 = a.take(T * 2 * h * 4);
     const size_t o_ffn = a.take(T * d * 4), o_sc = a.take(T * c.n_heads * (size_t)e->max_t * 4);
-    const size_t o_xqp = a.take(T * kmax);
-    const size_t o_xs = a.take(T * nbmax * 4), o_xt = a.take(T * nbmax * 4), o_sq = a.take(T * nbmax * 4);
+    const size_t o_xqp = a.take(T * kmax), o_rec = a.take(T * nbmax * sizeof(PfRecord));
     const size_t o_tok = a.take(T * 4);
     HIPCHK(hipMalloc(&e->pfarena, align_up(a.used, 256)), "hipMalloc(prefill)");
     char* P = e->pfarena;
     e->pf_xa = (float*)(P + o_xa); e->pf_xb = (float*)(P + o_xb); e->pf_qkv = (float*)(P + o_qkv);
     e->pf_att = (float*)(P + o_att); e->pf_wo = (float*)(P + o_wo); e->pf_h13 = (float*)(P + o_h13);
     e->pf_ffn = (float*)(P + o_ffn); e->pf_scores = (float*)(P + o_sc);
-    e->pf_xqp = (int8_t*)(P + o_xqp);
-    e->pf_xs = (float*)(P + o_xs); e->pf_xt = (float*)(P + o_xt); e->pf_sq = (int*)(P + o_sq);
+    e->pf_xqp = (int8_t*)(P + o_xqp); e->pf_rec = (PfRecord*)(P + o_rec);
     e->pf_tok = (int*)(P + o_tok);
     e->pf_T = (int)T;
     return L2Q_OK;
@@ -579,17 +578,17 @@ int prefill_chunk(l2q_engine* e, const int* tokens, int T, int pos0, bool want_l
     int rc;
     HIPCHK(hipMemcpyAsync(e->pf_tok, tokens, T * sizeof(int), hipMemcpyHostToDevice, st), "upload tokens");
     if ((rc = launch_pf_embed(e->emb, e->pf_tok, e->pf_xa, d, T, st))) return rc;
-    // every quantizing producer writes the GEMM operand (permuted q, sum(q), bias terms) itself
-    const PfOperand po{e->pf_xqp, e->pf_sq, e->pf_xt, bits};
+    // every quantizing producer writes the GEMM operand (permuted q, records) itself
+    const PfOperand pod{e->pf_xqp, e->pf_rec, bits, d, T}, poh{e->pf_xqp, e->pf_rec, bits, h, T};
     auto gemm = [&](const uint8_t* w, const float* ws, int rows, int cols, float* out) {
-        return launch_pf_gemm(bits, G, w, ws, rows, cols, e->pf_xqp, e->pf_xs, e->pf_sq, e->pf_xt, T, out, rows, st);
+        return launch_pf_gemm(bits, G, w, ws, rows, cols, e->pf_xqp, e->pf_rec, T, out, rows, st);
     };
     for (int l = 0; l < c.n_layers; l++) {
         float* kc = e->kcache + (size_t)l * kv * e->max_t;
         float* vc = e->vcache + (size_t)l * kv * e->max_t;
         // x = (l == 0 ? emb rows : xa + ffn) -> xb; RMSNorm; q, k, v; RoPE + append; attention
         if ((rc = launch_rmsnorm_quant(e->pf_xa, nullptr, nullptr, l == 0 ? nullptr : e->pf_ffn, e->pf_xb,
-                                       e->rms_att + (size_t)l * d, d, G, nullptr, e->pf_xs, st, T, &po)))
+                                       e->rms_att + (size_t)l * d, d, G, nullptr, nullptr, st, T, &pod)))
             return rc;
         if ((rc = gemm(e->qkv_w + (size_t)l * qkv_rows * e->rowb_d, e->qkv_s + (size_t)l * qkv_rows * nbd, qkv_rows,
                        d, e->pf_qkv)))
@@ -601,16 +600,16 @@ int prefill_chunk(l2q_engine* e, const int* tokens, int T, int pos0, bool want_l
                                          c.n_kv_heads, e->hs, e->max_t, st, T, qkv_rows, -1, 1)))
             return rc;
         // wo
-        if ((rc = launch_quantize(e->pf_att, T * d, G, nullptr, e->pf_xs, st, &po))) return rc;
+        if ((rc = launch_quantize(e->pf_att, T * d, G, nullptr, nullptr, st, &pod))) return rc;
         if ((rc = gemm(e->wo_w + (size_t)l * d * e->rowb_d, e->wo_s + (size_t)l * d * nbd, d, d, e->pf_wo))) return rc;
         // x = xb + wo -> xa; RMSNorm; SwiGLU(w1 x, w3 x); w2
         if ((rc = launch_rmsnorm_quant(e->pf_xb, nullptr, nullptr, e->pf_wo, e->pf_xa, e->rms_ffn + (size_t)l * d, d,
-                                       G, nullptr, e->pf_xs, st, T, &po)))
+                                       G, nullptr, nullptr, st, T, &pod)))
             return rc;
         if ((rc = gemm(e->w13_w + (size_t)l * 2 * h * e->rowb_d, e->w13_s + (size_t)l * 2 * h * nbd, 2 * h, d,
                        e->pf_h13)))
             return rc;
-        if ((rc = launch_pf_swiglu_quant(e->pf_h13, h, T, G, nullptr, e->pf_xs, st, &po))) return rc;
+        if ((rc = launch_pf_swiglu_quant(e->pf_h13, h, T, G, nullptr, nullptr, st, &poh))) return rc;
         if ((rc = gemm(e->w2_w + (size_t)l * d * e->rowb_h, e->w2_s + (size_t)l * d * nbh, d, h, e->pf_ffn))) return rc;
     }
     if (!want_logits) return L2Q_OK;

@@ -26,10 +26,13 @@ __global__ __launch_bounds__(256) void k_quantize(const float* __restrict__ x, i
     const float v = in ? x[i] : 0.0f;
     const float s = q8_scale(group_max<G>(fabsf(v)));
     const int q = q8_value_fast(v, s, q8_recip(s));
-    if (pf.xqp) pf_emit<G>(pf, i, q, s, in);
+    if (pf.xqp) {
+        const int t = i / pf.K;
+        pf_emit<G>(pf, t, i - t * pf.K, q, s, in);
+    }
     if (in) {
         if (xq) xq[i] = (int8_t)q;
-        if ((i % G) == 0) xs[i / G] = s;
+        if (xs && (i % G) == 0) xs[i / G] = s;
     }
 }
 
@@ -61,12 +64,7 @@ __global__ __launch_bounds__(kNormThreads) void k_rmsnorm_quant(
         if (resid) resid += to;
         if (xout) xout += to;
         if (xq) xq += to;
-        xs += to / G;
-        if (pf.xqp) {
-            pf.xqp += to;
-            pf.sq += to / G;
-            pf.xt += to / G;
-        }
+        if (xs) xs += to / G;
     }
     const float* src = emb ? emb + (size_t)meta[0] * n : x;
     float v[kNormMaxPer];
@@ -96,11 +94,11 @@ __global__ __launch_bounds__(kNormThreads) void k_rmsnorm_quant(
         const float o = in ? w[i] * (inv * v[k]) : 0.0f;
         const float s = q8_scale(group_max<G>(fabsf(o)));
         const int q = q8_value_fast(o, s, q8_recip(s));
-        if (pf.xqp) pf_emit<G>(pf, i, q, s, in);
+        if (pf.xqp) pf_emit<G>(pf, blockIdx.x, i, q, s, in);
         if (in) {
             if (xout) xout[i] = v[k];
             if (xq) xq[i] = (int8_t)q;
-            if ((i % G) == 0) xs[i / G] = s;
+            if (xs && (i % G) == 0) xs[i / G] = s;
         }
     }
 }

@@ -206,14 +206,15 @@ int launch_gemv(int bits, int group, const GemvArgs& a, hipStream_t st) {
 // ---------------------------------------------------------------------------
 
 // The optional prefill operand of a producer: checked, or all null.
-static int pf_operand(const PfOperand* pf, int8_t* xq, PfOperand* out, const char* what) {
-    *out = PfOperand{nullptr, nullptr, nullptr, 8};
+static int pf_operand(const PfOperand* pf, int8_t* xq, const float* xs, int K, int T, PfOperand* out,
+                      const char* what) {
+    *out = PfOperand{nullptr, nullptr, 8, 1, 1};
     if (!pf) {
-        if (!xq) { set_error("%s: no output", what); return L2Q_ERR_ARG; }
+        if (!xq || !xs) { set_error("%s: no output", what); return L2Q_ERR_ARG; }
         return L2Q_OK;
     }
-    if (!pf->xqp || !pf->sq || !pf->xt || (pf->bits != 4 && pf->bits != 8)) {
-        set_error("%s: bad prefill operand (bits=%d)", what, pf->bits);
+    if (!pf->xqp || !pf->rec || (pf->bits != 4 && pf->bits != 8) || pf->K != K || pf->T != T) {
+        set_error("%s: bad prefill operand (bits=%d K=%d T=%d for %d x %d)", what, pf->bits, pf->K, pf->T, T, K);
         return L2Q_ERR_ARG;
     }
     *out = *pf;
@@ -222,8 +223,9 @@ static int pf_operand(const PfOperand* pf, int8_t* xq, PfOperand* out, const cha
 
 int launch_quantize(const float* x, int n, int group, int8_t* xq, float* xs, hipStream_t st, const PfOperand* pf) {
     if (n <= 0 || (group != 32 && group != 64) || n % group) { set_error("quantize: bad n=%d group=%d", n, group); return L2Q_ERR_ARG; }
+    if (pf && (pf->K <= 0 || pf->K % group || n % pf->K)) { set_error("quantize: prefill operand rows of %d", pf->K); return L2Q_ERR_ARG; }
     PfOperand po;
-    if (int rc = pf_operand(pf, xq, &po, "quantize")) return rc;
+    if (int rc = pf_operand(pf, xq, xs, pf ? pf->K : n, pf ? n / pf->K : 1, &po, "quantize")) return rc;
     const int blocks = (n + 255) / 256;
     if (group == 32) hipLaunchKernelGGL(k_quantize<32>, dim3(blocks), dim3(256), 0, st, x, n, xq, xs, po);
     else hipLaunchKernelGGL(k_quantize<64>, dim3(blocks), dim3(256), 0, st, x, n, xq, xs, po);
@@ -239,7 +241,7 @@ int launch_rmsnorm_quant(const float* x, const float* emb, const int* meta, cons
         return L2Q_ERR_ARG;
     }
     PfOperand po;
-    if (int rc = pf_operand(pf, xq, &po, "rmsnorm_quant")) return rc;
+    if (int rc = pf_operand(pf, xq, xs, n, T, &po, "rmsnorm_quant")) return rc;
     if (group == 32)
         hipLaunchKernelGGL(k_rmsnorm_quant<32>, dim3(T), dim3(kNormThreads), 0, st, x, emb, meta, resid, xout, w, n, xq, xs, po);
     else
@@ -489,68 +491,82 @@ int launch_attention_kv8_split(const float* q, const float* kst, const float* vs
 // ---------------------------------------------------------------------------
 // batched prefill
 
-int launch_pf_prep(int bits, int group, const int8_t* xq, const float* xs, int K, int T, int8_t* xqp, int* sq,
-                   float* xt, hipStream_t st) {
+int launch_pf_prep(int bits, int group, const int8_t* xq, const float* xs, int K, int T, int8_t* xqp, PfRecord* rec,
+                   hipStream_t st) {
     if (T < 1 || K <= 0 || (group != 32 && group != 64) || K % group || (bits != 4 && bits != 8)) {
         set_error("prefill prep: bad K=%d T=%d group=%d bits=%d", K, T, group, bits);
         return L2Q_ERR_ARG;
     }
     const int n = T * (K / group), blocks = (n + 255) / 256;
-    if (bits == 4 && group == 64) hipLaunchKernelGGL((k_pf_prep<4, 64>), dim3(blocks), dim3(256), 0, st, xq, xs, K, T, xqp, sq, xt);
-    if (bits == 4 && group == 32) hipLaunchKernelGGL((k_pf_prep<4, 32>), dim3(blocks), dim3(256), 0, st, xq, xs, K, T, xqp, sq, xt);
-    if (bits == 8 && group == 64) hipLaunchKernelGGL((k_pf_prep<8, 64>), dim3(blocks), dim3(256), 0, st, xq, xs, K, T, xqp, sq, xt);
-    if (bits == 8 && group == 32) hipLaunchKernelGGL((k_pf_prep<8, 32>), dim3(blocks), dim3(256), 0, st, xq, xs, K, T, xqp, sq, xt);
+    if (bits == 4 && group == 64) hipLaunchKernelGGL((k_pf_prep<4, 64>), dim3(blocks), dim3(256), 0, st, xq, xs, K, T, xqp, rec);
+    if (bits == 4 && group == 32) hipLaunchKernelGGL((k_pf_prep<4, 32>), dim3(blocks), dim3(256), 0, st, xq, xs, K, T, xqp, rec);
+    if (bits == 8 && group == 64) hipLaunchKernelGGL((k_pf_prep<8, 64>), dim3(blocks), dim3(256), 0, st, xq, xs, K, T, xqp, rec);
+    if (bits == 8 && group == 32) hipLaunchKernelGGL((k_pf_prep<8, 32>), dim3(blocks), dim3(256), 0, st, xq, xs, K, T, xqp, rec);
     return check_launch("prefill_prep");
 }
 
+namespace {
+
+// One workgroup shape of the batched GEMM: waves WR x WT of RTW x TPW
+// 16x16 tiles, SC columns per step.
+template <int B_, int G_, int RTW, int TPW, int WR, int WT, int SC, int NST, bool PIPE>
+void pf3_launch(const uint8_t* w, const float* ws, int rows, int cols, const int8_t* xqp, const PfRecord* rec, int T,
+                float* out, int ldo, hipStream_t st) {
+    using P = Pf3<B_, G_, RTW, TPW, WR, WT, SC>;
+    const dim3 grid((unsigned)((rows + P::RT - 1) / P::RT), (unsigned)((T + P::TT - 1) / P::TT));
+    hipLaunchKernelGGL((k_pf_gemm3<B_, G_, RTW, TPW, WR, WT, SC, NST, PIPE>), grid, dim3(P::NT), 0, st, w, ws, rows,
+                       cols, xqp, rec, T, out, ldo);
+}
+
+// The three workgroup shapes of the batched GEMM (16x16 MFMA tiles; SC =
+// columns per step, a multiple of the group):
+//   big    64 rows x 64 tokens, waves 2 x 2 of 32 x 32, one group per step
+//   mid    32 rows x 64 tokens, waves 2 x 2 of 16 x 32, two groups per step
+//   small  32 rows x 32 tokens, waves 2 x 2 of 16 x 16, four groups per step
+// A step's fixed costs (barrier, DMA wait, LDS and MFMA latency) are spread
+// over the waves resident on a SIMD and over the work of the step: large
+// tiles do the least LDS traffic and unpacking per output, small tiles
+// with long steps keep every SIMD busy when there are few rows (the ordered
+// fold cannot split the columns).  Measured on MI355X at the 7B shapes, T =
+// 127: w1|w3 (22016 rows) big, qkv (12288) mid, wo and w2 (4096) small.
+enum PfShape { kPfBig, kPfMid, kPfSmall };
+
+template <int B_, int G_>
+void pf3_shape(PfShape shp, const uint8_t* w, const float* ws, int rows, int cols, const int8_t* xqp,
+               const PfRecord* rec, int T, float* out, int ldo, hipStream_t st) {
+    if (shp == kPfBig) pf3_launch<B_, G_, 2, 2, 2, 2, G_, 4, false>(w, ws, rows, cols, xqp, rec, T, out, ldo, st);
+    else if (shp == kPfMid) pf3_launch<B_, G_, 1, 2, 2, 2, 2 * G_, 3, false>(w, ws, rows, cols, xqp, rec, T, out, ldo, st);
+    else pf3_launch<B_, G_, 1, 1, 2, 2, 4 * G_, 4, false>(w, ws, rows, cols, xqp, rec, T, out, ldo, st);
+}
+
+}  // namespace
+
 int launch_pf_gemm(int bits, int group, const void* w, const float* ws, int rows, int cols, const int8_t* xqp,
-                   const float* xs, const int* sq, const float* xt, int T, float* out, int ldo, hipStream_t st) {
+                   const PfRecord* rec, int T, float* out, int ldo, hipStream_t st) {
     if (T < 1 || rows < 1 || cols <= 0 || (group != 32 && group != 64) || cols % group || (bits != 4 && bits != 8) ||
-        cols % 8 || ldo < rows) {
+        cols % 32 || ldo < rows) {
         set_error("prefill gemm: bad rows=%d cols=%d T=%d group=%d bits=%d", rows, cols, T, group, bits);
         return L2Q_ERR_ARG;
     }
-    if (reinterpret_cast<uintptr_t>(w) % 16 || reinterpret_cast<uintptr_t>(xqp) % 16) {
-        set_error("prefill gemm: weights and activations must be 16-byte aligned");
+    if (reinterpret_cast<uintptr_t>(w) % 16 || reinterpret_cast<uintptr_t>(xqp) % 16 ||
+        reinterpret_cast<uintptr_t>(rec) % 16 || (size_t)cols * bits / 8 % 16) {
+        set_error("prefill gemm: weights, activations and records must be 16-byte aligned (rows of 16n bytes)");
         return L2Q_ERR_ARG;
     }
-    // rows per workgroup (16, 32 or 64): the fewest rounds of workgroups
-    // over the CUs times a workgroup's time, modelled as 1.3 + its 16-row
-    // tiles (every workgroup restages all the step's activations, worth
-    // ~1.3 row tiles of folding: measured on the 7B shapes at T = 128, where
-    // this picks the fastest tile for each); the larger tile on ties
+    // the largest tile that still gives every CU 2.5 workgroups
     int ncu = 0, dev = 0;
     if (hipGetDevice(&dev) != hipSuccess ||
         hipDeviceGetAttribute(&ncu, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || ncu <= 0)
         ncu = 256;
-    const long long rtiles = (rows + 15) / 16;
-    int rtw = 4;
-    long long best = -1;
-    for (int r : {4, 2, 1}) {
-        const long long wgs = (rtiles + r - 1) / r * ((T + kPf2Tokens - 1) / kPf2Tokens);
-        const long long cost = (wgs + ncu - 1) / ncu * (13 + 10 * r);
-        if (best < 0 || cost < best) { best = cost; rtw = r; }
-    }
-    const dim3 grid((unsigned)((rows + 16 * rtw - 1) / (16 * rtw)), (unsigned)((T + kPf2Tokens - 1) / kPf2Tokens));
+    const long long want = (long long)ncu * 5 / 2;
+    const long long wg_big = (long long)((rows + 63) / 64) * ((T + 63) / 64);
+    const long long wg_mid = (long long)((rows + 31) / 32) * ((T + 63) / 64);
+    const PfShape shp = wg_big >= want ? kPfBig : wg_mid >= want ? kPfMid : kPfSmall;
     const uint8_t* wb = static_cast<const uint8_t*>(w);
-    int rc = L2Q_OK;
-    auto go = [&](auto kern, size_t lds) {
-        if ((rc = raise_lds_limit(reinterpret_cast<const void*>(kern), lds, "prefill gemm: raising the LDS limit")))
-            return;
-        hipLaunchKernelGGL(kern, grid, dim3(kPf2Threads), lds, st, wb, ws, rows, cols, xqp, xs, sq, xt, T, out, ldo);
-    };
-#define L2Q_PF2(B_, G_)                                                                    \
-    do {                                                                                  \
-        if (rtw == 4) go(k_pf_gemm2<B_, G_, 4>, pf2_lds_bytes<B_, G_, 4>());              \
-        else if (rtw == 2) go(k_pf_gemm2<B_, G_, 2>, pf2_lds_bytes<B_, G_, 2>());         \
-        else go(k_pf_gemm2<B_, G_, 1>, pf2_lds_bytes<B_, G_, 1>());                       \
-    } while (0)
-    if (bits == 4 && group == 64) L2Q_PF2(4, 64);
-    if (bits == 4 && group == 32) L2Q_PF2(4, 32);
-    if (bits == 8 && group == 64) L2Q_PF2(8, 64);
-    if (bits == 8 && group == 32) L2Q_PF2(8, 32);
-#undef L2Q_PF2
-    if (rc) return rc;
+    if (bits == 4 && group == 64) pf3_shape<4, 64>(shp, wb, ws, rows, cols, xqp, rec, T, out, ldo, st);
+    if (bits == 4 && group == 32) pf3_shape<4, 32>(shp, wb, ws, rows, cols, xqp, rec, T, out, ldo, st);
+    if (bits == 8 && group == 64) pf3_shape<8, 64>(shp, wb, ws, rows, cols, xqp, rec, T, out, ldo, st);
+    if (bits == 8 && group == 32) pf3_shape<8, 32>(shp, wb, ws, rows, cols, xqp, rec, T, out, ldo, st);
     return check_launch("prefill_gemm");
 }
 
@@ -563,7 +579,7 @@ int launch_pf_swiglu_quant(const float* h13, int n, int T, int group, int8_t* xq
                            const PfOperand* pf) {
     if (n <= 0 || n % group || (group != 32 && group != 64)) { set_error("prefill swiglu: bad n=%d", n); return L2Q_ERR_ARG; }
     PfOperand po;
-    if (int rc = pf_operand(pf, xq, &po, "prefill swiglu")) return rc;
+    if (int rc = pf_operand(pf, xq, xs, n, T, &po, "prefill swiglu")) return rc;
     const size_t total = (size_t)T * n;
     const unsigned blocks = (unsigned)((total + 255) / 256);
     if (group == 32) hipLaunchKernelGGL(k_pf_swiglu_quant<32>, dim3(blocks), dim3(256), 0, st, h13, n, T, xq, xs, po);
@@ -814,18 +830,18 @@ int l2q_gemm_q(int wbits, float* out, const int8_t* xq, const float* xs, const v
         set_error("gemm: bad arguments bits=%d rows=%d cols=%d group=%d T=%d", wbits, rows, cols, group, T);
         return L2Q_ERR_ARG;
     }
-    // scratch: permuted activations, then sum(q) and bias terms per group
+    // scratch: permuted activations (rounded up to 16 bytes), then one
+    // record per (group, token)
     const size_t nbt = (size_t)T * (cols / group);
-    const size_t words = ((size_t)T * cols + 3) / 4 + 2 * nbt;
+    const size_t xwords = ((size_t)T * cols + 15) / 16 * 4;
     float* scratch = nullptr;
-    int rc = attn_scratch(words, &scratch);
+    int rc = attn_scratch(xwords + nbt * sizeof(PfRecord) / 4, &scratch);
     if (rc) return rc;
     int8_t* xqp = reinterpret_cast<int8_t*>(scratch);
-    int* sq = reinterpret_cast<int*>(scratch + ((size_t)T * cols + 3) / 4);
-    float* xt = reinterpret_cast<float*>(sq + nbt);
+    PfRecord* rec = reinterpret_cast<PfRecord*>(scratch + xwords);
     hipStream_t st = (hipStream_t)stream;
-    if ((rc = launch_pf_prep(wbits, group, xq, xs, cols, T, xqp, sq, xt, st))) return rc;
-    return launch_pf_gemm(wbits, group, w, ws, rows, cols, xqp, xs, sq, xt, T, out, rows, st);
+    if ((rc = launch_pf_prep(wbits, group, xq, xs, cols, T, xqp, rec, st))) return rc;
+    return launch_pf_gemm(wbits, group, w, ws, rows, cols, xqp, rec, T, out, rows, st);
 }
 
 int l2q_kv8_append(const float* k, const float* v, int8_t* kcache8, int8_t* vcache8, float* kscale, float* vscale,

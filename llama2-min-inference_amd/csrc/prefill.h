@@ -26,15 +26,17 @@
 namespace l2q {
 
 typedef int v4i32 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) void lds_void_t;
+typedef __attribute__((address_space(1))) void glb_void_t;
 
-// Activation preparation: xq [T][K] natural order -> xqp [T][K] in the MFMA
-// chunk order (INT4: per chunk of G/4 columns, odd columns then even
-// columns; INT8: unchanged), sq [T][K/G] = sum of the group's q, xt [T][K/G]
-// = q8_bias_term(xs, sq) (runq.c:137).  One thread per (token, group).
+// Activation preparation from natural-order xq [T][K], xs [T][K/G]: xqp
+// [T][K] in the MFMA chunk order (INT4: per chunk of G/4 columns, odd
+// columns then even columns; INT8: unchanged) and the records rec [K/G][T].
+// One thread per (token, group).  The producers that quantize write the
+// same operand themselves (pf_emit); this serves callers that hold xq.
 template <int BITS, int G>
 __global__ __launch_bounds__(256) void k_pf_prep(const int8_t* __restrict__ xq, const float* __restrict__ xs,
-                                                 int K, int T, int8_t* __restrict__ xqp, int* __restrict__ sq,
-                                                 float* __restrict__ xt) {
+                                                 int K, int T, int8_t* __restrict__ xqp, PfRecord* __restrict__ rec) {
     const int nb = K / G;
     const int idx = blockIdx.x * blockDim.x + threadIdx.x;
     if (idx >= T * nb) return;
@@ -50,141 +52,157 @@ __global__ __launch_bounds__(256) void k_pf_prep(const int8_t* __restrict__ xq, 
             else dst[c * CH + j] = v;
         }
     }
-    sq[idx] = s;
-    xt[idx] = q8_bias_term(xs[idx], s);
+    const int t = idx / nb, b = idx - t * nb;
+    rec[(size_t)b * T + t] = pf_record(xs[idx], s, BITS);
 }
 
-// Batched GEMM, LDS-staged: workgroup (16*RTW-row tile, 128-token tile),
-// 8/TPW waves; wave w computes the RTW 16-row tiles against token tiles
-// w, w + 8/TPW, ... (TPW of them; RTW is chosen per shape so that the grid
-// covers the CUs).  The columns
-// advance in steps of 128 (128/G groups): weights, the permuted activations
-// and the step's per-group scalars (xs, xt, sum(q), ws) are loaded with
-// coalesced 16-byte loads into registers two steps ahead and written to one
-// of two LDS buffers while the other is consumed, one barrier per step.
-// Per group: MFMA with the accumulator input 128*sum(q) of the token (x16
-// for INT4, whose dot is x16), so D = d + 128*sum(q) (>> 4 for INT4,
-// exact), then the ordered fold acc = fma(ws, fma(xs, (float)D, -xt), acc)
-// of runq.c:150-156, so every output equals the decode GEMV's bit for bit.
-// A step's LDS reads are issued together, then its MFMAs, then the folds in
-// group order.
-constexpr int kPf2Tokens = 128;
-constexpr int kPf2Tpw = 2;                   // token tiles per wave
-constexpr int kPf2Threads = 8 / kPf2Tpw * L2Q_WAVE;
-constexpr int kPf2Cols = 128;                // columns per LDS step
-constexpr int kPf2BPitch = kPf2Cols + 16;    // bytes per token row of the activation stage
-template <int BITS>
-__host__ __device__ constexpr int pf2_apitch() { return kPf2Cols * BITS / 8 + 16; }
-template <int BITS, int G, int RTW>
-__host__ __device__ constexpr size_t pf2_stage_bytes() {
-    return (size_t)16 * RTW * pf2_apitch<BITS>() + (size_t)kPf2Tokens * kPf2BPitch +
-           (size_t)(kPf2Cols / G) * (3 * kPf2Tokens + 16 * RTW) * 4;
+// global -> LDS without registers (gfx950 global_load_lds_dword(x4)): lane
+// l of the wave writes its SIZE bytes read at src to dst + l * SIZE, dst
+// being wave-uniform.  Counted by vmcnt like any load.
+template <int SIZE>
+__device__ __forceinline__ void dma_lds(const void* src, uint8_t* dst) {
+    static_assert(SIZE == 4 || SIZE == 16, "DMA unit");
+    if constexpr (SIZE == 16) __builtin_amdgcn_global_load_lds((glb_void_t*)const_cast<void*>(src), (lds_void_t*)dst, 16, 0, 0);
+    else __builtin_amdgcn_global_load_lds((glb_void_t*)const_cast<void*>(src), (lds_void_t*)dst, 4, 0, 0);
 }
-template <int BITS, int G, int RTW>
-__host__ __device__ constexpr size_t pf2_lds_bytes() { return 2 * pf2_stage_bytes<BITS, G, RTW>(); }
 
-template <int BITS, int G, int RTW>
-__global__ __launch_bounds__(kPf2Threads) void k_pf_gemm2(
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+    static_assert(N >= 0 && N < 64, "vmcnt range");
+    __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (0x7 << 4) | (0xF << 8));
+}
+
+// Batched GEMM geometry.  A workgroup computes RT rows x TT tokens with
+// WR x WT waves, each RTW 16-row tiles x TPW 16-token tiles; the columns
+// advance in steps of SC (KS groups).  A step's stage in LDS:
+//   A   [KS][RT][GB]   weight bytes of each row and group (GB = G*BITS/8)
+//   B   [KS][TT][G]    the tokens' permuted activations
+//   R   [KS][TT]       32-byte records (pf_record)
+//   W   [KS][RT]       weight scales
+// each region filled by 64-lane DMA instructions (16-byte units; 4-byte
+// ones for W), instruction k of the stage issued by wave k % NW.
+template <int BITS, int G, int RTW, int TPW, int WR, int WT, int SC>
+struct Pf3 {
+    static constexpr int NW = WR * WT, NT = NW * L2Q_WAVE;
+    static constexpr int RT = 16 * RTW * WR, TT = 16 * TPW * WT;
+    static constexpr int KS = SC / G;
+    static constexpr int GB = G * BITS / 8;
+    static constexpr int AU = KS * RT * GB / 16, BU = KS * TT * G / 16, RU = 2 * KS * TT, WU = KS * RT;
+    static constexpr int NA = (AU + 63) / 64, NB = (BU + 63) / 64, NR = (RU + 63) / 64, NWS = (WU + 63) / 64;
+    static constexpr int N = NA + NB + NR + NWS;
+    static constexpr int OB = NA * 1024, OR = OB + NB * 1024, OWS = OR + NR * 1024;
+    static constexpr int STAGE = OWS + NWS * 256;
+    static constexpr int NK = (N + NW - 1) / NW;     // DMA instructions per wave and stage (at most)
+    static_assert(SC % G == 0 && SC % 16 == 0 && SC * BITS / 8 >= 16, "step geometry");
+};
+
+// Wait for this wave's DMA of every stage but the last K issued: waves
+// w < N % NW issue one instruction more per stage.
+template <class P, int K>
+__device__ __forceinline__ void wait_stages(int wv) {
+    if constexpr (P::N % P::NW == 0) {
+        wait_vmcnt<K * (P::N / P::NW)>();
+    } else {
+        if (wv < P::N % P::NW) wait_vmcnt<K * (P::N / P::NW + 1)>();
+        else wait_vmcnt<K * (P::N / P::NW)>();
+    }
+}
+
+// The batched GEMM out[t][r] = sum over groups b, in order, of
+// ws[r][b] * fma(xs[t][b], (float)(d + 128*sum(q)), -xt[t][b]), the decode
+// GEMV's fold (runq.c:150-156) for every (row, token), bit for bit.  Per
+// group: one MFMA per (row tile, token tile) with the record's accumulator
+// input, then 3 VALU operations per output (convert, two FMAs; INT4 adds
+// the shift).  Operands reach LDS by DMA, NST stages in rotation: stage
+// s + NST - 1 is requested while stage s is consumed, and one barrier per
+// step publishes stage s + 1.  The buffers are distinct LDS variables and
+// the loop is unrolled by NST, so the compiler sees which buffer every LDS
+// read uses and waits only for DMA into that one.  With PIPE the fold
+// trails the MFMAs by one step: step s issues its LDS reads, folds step
+// s - 1's MFMA results while they are in flight, then issues its MFMAs,
+// whose latency the barrier and the next step's reads cover.  Rows, tokens
+// and columns past the ends are clamped into the operands (those outputs
+// are never stored).
+template <int BITS, int G, int RTW, int TPW, int WR, int WT, int SC, int NST, bool PIPE>
+__global__ __launch_bounds__(WR * WT * L2Q_WAVE) void k_pf_gemm3(
     const uint8_t* __restrict__ w, const float* __restrict__ ws, int rows, int cols,
-    const int8_t* __restrict__ xqp, const float* __restrict__ xs, const int* __restrict__ sq,
-    const float* __restrict__ xt, int T, float* __restrict__ out, int ldo) {
-    constexpr int RT = 16 * RTW;                     // rows per workgroup
-    constexpr int KS = kPf2Cols / G;                 // groups per step
-    constexpr int AB = kPf2Cols * BITS / 8;          // weight bytes of a row per step
-    constexpr int AP = pf2_apitch<BITS>();
-    constexpr int GB = G * BITS / 8;                 // weight bytes per group
-    constexpr int CB = GB / 4;                       // weight bytes per MFMA lane chunk
-    constexpr int CX = G / 4;                        // activation bytes per MFMA lane chunk
-    constexpr int AN = RT * AB / 16;                                  // 16-byte weight loads per step
-    constexpr int APT = (AN + kPf2Threads - 1) / kPf2Threads;         // per thread
-    constexpr int BPT = kPf2Cols * kPf2Tokens / 16 / kPf2Threads;     // 16-byte activation loads per thread
-    constexpr int SN = KS * kPf2Tokens;                               // per-token scalars per step
-    constexpr int SPT = (SN + kPf2Threads - 1) / kPf2Threads;
-    constexpr int WN = KS * RT;                                       // weight scales per step
-    constexpr int WPT = (WN + kPf2Threads - 1) / kPf2Threads;
-    static_assert(BPT >= 1, "step geometry");
-    extern __shared__ __attribute__((aligned(16))) uint8_t pf2_lds[];
-    const int tid = threadIdx.x, lane = tid & (L2Q_WAVE - 1), wv = tid / L2Q_WAVE;
-    const int r0 = blockIdx.x * RT, t0 = blockIdx.y * kPf2Tokens;
-    const int nb = cols / G, nsteps = (nb + KS - 1) / KS;
+    const int8_t* __restrict__ xqp, const PfRecord* __restrict__ rec, int T, float* __restrict__ out, int ldo) {
+    using P = Pf3<BITS, G, RTW, TPW, WR, WT, SC>;
+    constexpr int KS = P::KS;
+    static_assert(NST >= 3 && NST <= 5, "pipeline depth");
+    __shared__ __attribute__((aligned(16))) uint8_t sb0[P::STAGE];
+    __shared__ __attribute__((aligned(16))) uint8_t sb1[P::STAGE];
+    __shared__ __attribute__((aligned(16))) uint8_t sb2[P::STAGE];
+    __shared__ __attribute__((aligned(16))) uint8_t sb3[NST > 3 ? P::STAGE : 16];
+    __shared__ __attribute__((aligned(16))) uint8_t sb4[NST > 4 ? P::STAGE : 16];
+    uint8_t* const bufs[5] = {sb0, sb1, sb2, sb3, sb4};
+    const int tid = threadIdx.x, lane = tid & (L2Q_WAVE - 1);
+    const int wv = __builtin_amdgcn_readfirstlane(tid / L2Q_WAVE);
+    const int r0 = blockIdx.x * P::RT, t0 = blockIdx.y * P::TT;
+    const int nb = cols / G, nsteps = (cols + SC - 1) / SC, nfull = cols / SC;
     const int rowbytes = cols * BITS / 8;
-    const int ntt = min(8, (T - t0 + 15) / 16);      // token tiles of this workgroup
-    auto stage = [&](int buf) { return pf2_lds + (size_t)buf * pf2_stage_bytes<BITS, G, RTW>(); };
 
-    // global -> registers for step s (clamped rows / tokens / groups); two
-    // register sets, so that step s + 2 is in flight while step s + 1 is
-    // written to LDS and step s is consumed.  Every load is unconditional
-    // (what lies past a row is zeroed when written to LDS): a load under a
-    // condition becomes "zero the register, then a masked load", and the
-    // zeroing waits for the loads in flight, which would make the prefetch
-    // synchronous.
-    struct Regs {
-        uint4 ra[APT], rb[BPT];
-        float rxs[SPT], rxt[SPT];
-        int rsq[SPT];
-        float rws[WPT];
+    // source of this lane's unit in DMA instruction k at step s (clamped)
+    auto src = [&](int k, int s) __attribute__((always_inline)) -> const uint8_t* {
+        if (k < P::NA) {
+            const int u = min(k * 64 + lane, P::AU - 1);
+            const int g = u / (P::RT * P::GB / 16), rem = u % (P::RT * P::GB / 16);
+            const int r = rem / (P::GB / 16), part = rem % (P::GB / 16);
+            const int col = s * SC + g * G;
+            const int off = col < cols ? col * BITS / 8 + part * 16 : rowbytes - 16;
+            return w + (size_t)min(r0 + r, rows - 1) * rowbytes + off;
+        }
+        k -= P::NA;
+        if (k < P::NB) {
+            const int u = min(k * 64 + lane, P::BU - 1);
+            const int g = u / (P::TT * G / 16), rem = u % (P::TT * G / 16);
+            const int t = rem / (G / 16), part = rem % (G / 16);
+            const int col = s * SC + g * G;
+            const int off = col < cols ? col + part * 16 : cols - 16;
+            return reinterpret_cast<const uint8_t*>(xqp) + (size_t)min(t0 + t, T - 1) * cols + off;
+        }
+        k -= P::NB;
+        if (k < P::NR) {
+            const int u = min(k * 64 + lane, P::RU - 1);
+            const int g = u / (2 * P::TT), t = (u / 2) % P::TT;
+            return reinterpret_cast<const uint8_t*>(rec + (size_t)min(s * KS + g, nb - 1) * T + min(t0 + t, T - 1)) +
+                   16 * (u & 1);
+        }
+        k -= P::NR;
+        const int u = min(k * 64 + lane, P::WU - 1);
+        const int g = u / P::RT, r = u % P::RT;
+        return reinterpret_cast<const uint8_t*>(ws + (size_t)min(r0 + r, rows - 1) * nb + min(s * KS + g, nb - 1));
     };
-    auto fetch = [&](int s, Regs& R) {
-#pragma unroll
-        for (int k = 0; k < APT; k++) {
-            const int e = min(tid + kPf2Threads * k, AN - 1), r = e / (AB / 16), p = e % (AB / 16);
-            const int off = min(s * AB + 16 * p, rowbytes - 16);
-            R.ra[k] = *reinterpret_cast<const uint4*>(w + (size_t)min(r0 + r, rows - 1) * rowbytes + off);
-        }
-#pragma unroll
-        for (int k = 0; k < BPT; k++) {
-            const int e = tid + kPf2Threads * k, t = e / (kPf2Cols / 16), p = e % (kPf2Cols / 16);
-            const int off = min(s * kPf2Cols + 16 * p, cols - 16);
-            R.rb[k] = *reinterpret_cast<const uint4*>(xqp + (size_t)min(t0 + t, T - 1) * cols + off);
-        }
-#pragma unroll
-        for (int k = 0; k < SPT; k++) {
-            const int e = min(tid + kPf2Threads * k, SN - 1), t = e / KS, g = s * KS + e % KS;
-            const size_t gi = (size_t)min(t0 + t, T - 1) * nb + min(g, nb - 1);
-            R.rxs[k] = xs[gi];
-            R.rxt[k] = xt[gi];
-            R.rsq[k] = sq[gi];
-        }
-#pragma unroll
-        for (int k = 0; k < WPT; k++) {
-            const int e = min(tid + kPf2Threads * k, WN - 1), r = e / KS, g = s * KS + e % KS;
-            R.rws[k] = ws[(size_t)min(r0 + r, rows - 1) * nb + min(g, nb - 1)];
-        }
+    // bytes one instruction's sources advance per full step
+    auto stride = [&](int k) __attribute__((always_inline)) -> size_t {
+        if (k < P::NA) return (size_t)SC * BITS / 8;
+        if (k < P::NA + P::NB) return (size_t)SC;
+        if (k < P::NA + P::NB + P::NR) return (size_t)KS * T * sizeof(PfRecord);
+        return (size_t)KS * 4;
     };
-    // registers -> LDS buffer: [A rows][AP] [B tokens][BPitch] [xs][xt][c: KS x 128] [ws: KS x RT]
-    auto put = [&](int s, int buf, const Regs& R) {
-        uint8_t* A = stage(buf);
-        uint8_t* B = A + RT * AP;
-        float* S = reinterpret_cast<float*>(B + kPf2Tokens * kPf2BPitch);
+    const uint8_t* p0[P::NK];
 #pragma unroll
-        for (int k = 0; k < APT; k++) {
-            const int e = tid + kPf2Threads * k, r = e / (AB / 16), p = e % (AB / 16);
-            const bool in = s * AB + 16 * p < rowbytes;
-            if (e < AN) *reinterpret_cast<uint4*>(A + r * AP + 16 * p) = in ? R.ra[k] : make_uint4(0, 0, 0, 0);
-        }
+    for (int kk = 0; kk < P::NK; kk++) p0[kk] = src(min(wv + P::NW * kk, P::N - 1), 0);
+    auto issue = [&](int s, uint8_t* buf) __attribute__((always_inline)) {
+        const bool fast = s < nfull;
 #pragma unroll
-        for (int k = 0; k < BPT; k++) {
-            const int e = tid + kPf2Threads * k, t = e / (kPf2Cols / 16), p = e % (kPf2Cols / 16);
-            const bool in = s * kPf2Cols + 16 * p < cols;
-            *reinterpret_cast<uint4*>(B + t * kPf2BPitch + 16 * p) = in ? R.rb[k] : make_uint4(0, 0, 0, 0);
-        }
-#pragma unroll
-        for (int k = 0; k < SPT; k++) {
-            const int e = tid + kPf2Threads * k, t = e / KS, g = e % KS;
-            if (e < SN) {
-                S[g * kPf2Tokens + t] = R.rxs[k];
-                S[(KS + g) * kPf2Tokens + t] = R.rxt[k];
-                reinterpret_cast<int*>(S)[(2 * KS + g) * kPf2Tokens + t] = R.rsq[k] * 128;
+        for (int kk = 0; kk < P::NK; kk++) {
+            const int k = wv + P::NW * kk;
+            if (k < P::N) {
+                const uint8_t* a = fast ? p0[kk] + (size_t)s * stride(k) : src(k, s);
+                if (k < P::NA) dma_lds<16>(a, buf + k * 1024);
+                else if (k < P::NA + P::NB) dma_lds<16>(a, buf + P::OB + (k - P::NA) * 1024);
+                else if (k < P::NA + P::NB + P::NR) dma_lds<16>(a, buf + P::OR + (k - P::NA - P::NB) * 1024);
+                else dma_lds<4>(a, buf + P::OWS + (k - P::NA - P::NB - P::NR) * 256);
             }
         }
-#pragma unroll
-        for (int k = 0; k < WPT; k++) {
-            const int e = tid + kPf2Threads * k;
-            if (e < WN) S[3 * KS * kPf2Tokens + (e % KS) * RT + e / KS] = R.rws[k];
-        }
     };
 
-    constexpr int TPW = kPf2Tpw, NW = 8 / TPW;
+    constexpr int CB = P::GB / 4, CX = G / 4;    // bytes per MFMA lane chunk: weights, activations
+    const int c = lane / 16, l16 = lane % 16;
+    const int rw0 = (wv % WR) * 16 * RTW, tw0 = (wv / WR) * 16 * TPW;
+    const int left = T - t0 - tw0;
+    const int nj = left <= 0 ? 0 : min(TPW, (left + 15) / 16);   // token tiles with tokens (wave-uniform)
     float acc[TPW][RTW][4];
 #pragma unroll
     for (int j = 0; j < TPW; j++)
@@ -192,137 +210,177 @@ __global__ __launch_bounds__(kPf2Threads) void k_pf_gemm2(
         for (int i = 0; i < RTW; i++)
 #pragma unroll
             for (int e = 0; e < 4; e++) acc[j][i][e] = 0.0f;
-    const int c = lane / 16, l16 = lane % 16;
-    // token tiles wv + NW*j exist for j < nj (wave-uniform)
-    const int nj = wv < ntt ? (ntt - wv + NW - 1) / NW : 0;
 
-    auto compute = [&](int s) {
-        if (nj == 0) return;
-        const uint8_t* A = stage(s & 1);
-        const uint8_t* B = A + RT * AP;
-        const float* S = reinterpret_cast<const float*>(B + kPf2Tokens * kPf2BPitch);
-        const int ng = min(KS, nb - s * KS);
-        // LDS reads of the step: A operands (INT4: x16 nibbles in place), B
-        // operand and scalars of every group
-        v4i32 av[KS][RTW], bv[KS][TPW];
+    // a step's operands read from LDS, and what its fold needs
+    struct Ops {
+        v4i32 av[KS][RTW], bv[KS][TPW], cin[KS][TPW];
         long al[KS][RTW], bl[KS][TPW];
-        float gxs[KS][TPW], gxt[KS][TPW];
-        int cin[KS][TPW];
+    };
+    struct Pend {
+        v4i32 d[KS][TPW][RTW];
+        float2 sc[KS][TPW];      // xs, xt
         float4 wsv[KS][RTW];
+        int ng;
+    };
+    auto read = [&](int s, const uint8_t* buf, Ops& o, Pend& pn) __attribute__((always_inline)) {
+        pn.ng = min(KS, nb - s * KS);
 #pragma unroll
         for (int g = 0; g < KS; g++) {
-            if (g >= ng) break;
 #pragma unroll
             for (int i = 0; i < RTW; i++) {
-                const uint8_t* pa = A + (16 * i + l16) * AP + g * GB + c * CB;
+                const uint8_t* pa = buf + (g * P::RT + rw0 + 16 * i + l16) * P::GB + c * CB;
                 if constexpr (G == 64) {
                     if constexpr (BITS == 8) {
                         const int4 v = *reinterpret_cast<const int4*>(pa);
-                        av[g][i] = v4i32{v.x, v.y, v.z, v.w};
+                        o.av[g][i] = v4i32{v.x, v.y, v.z, v.w};
                     } else {
                         const int2 v = *reinterpret_cast<const int2*>(pa);
-                        av[g][i] = v4i32{v.x & (int)0xF0F0F0F0, v.y & (int)0xF0F0F0F0, (v.x << 4) & (int)0xF0F0F0F0,
-                                         (v.y << 4) & (int)0xF0F0F0F0};
+                        o.av[g][i] = v4i32{v.x, v.y, 0, 0};
                     }
                 } else {
                     if constexpr (BITS == 8) {
                         const int2 v = *reinterpret_cast<const int2*>(pa);
-                        al[g][i] = (long)(unsigned)v.x | ((long)v.y << 32);
+                        o.al[g][i] = (long)(unsigned)v.x | ((long)v.y << 32);
                     } else {
-                        const int v = *reinterpret_cast<const int*>(pa);
-                        al[g][i] = (long)(unsigned)(v & (int)0xF0F0F0F0) | ((long)((v << 4) & (int)0xF0F0F0F0) << 32);
+                        o.al[g][i] = (long)(unsigned)*reinterpret_cast<const int*>(pa);
                     }
                 }
-                wsv[g][i] = *reinterpret_cast<const float4*>(S + 3 * KS * kPf2Tokens + g * RT + 16 * i + 4 * c);
+                pn.wsv[g][i] = *reinterpret_cast<const float4*>(buf + P::OWS + (g * P::RT + rw0 + 16 * i + 4 * c) * 4);
             }
 #pragma unroll
             for (int j = 0; j < TPW; j++) {
-                const int tl = 16 * (wv + NW * j) + l16;   // token of this lane (in the workgroup)
-                const uint8_t* pb = B + tl * kPf2BPitch + g * G + c * CX;
+                const int tl = tw0 + 16 * j + l16;
+                const uint8_t* pb = buf + P::OB + (g * P::TT + tl) * G + c * CX;
                 if constexpr (G == 64) {
                     const int4 v = *reinterpret_cast<const int4*>(pb);
-                    bv[g][j] = v4i32{v.x, v.y, v.z, v.w};
+                    o.bv[g][j] = v4i32{v.x, v.y, v.z, v.w};
                 } else {
                     const int2 v = *reinterpret_cast<const int2*>(pb);
-                    bl[g][j] = (long)(unsigned)v.x | ((long)v.y << 32);
+                    o.bl[g][j] = (long)(unsigned)v.x | ((long)v.y << 32);
                 }
-                gxs[g][j] = S[g * kPf2Tokens + tl];
-                gxt[g][j] = S[(KS + g) * kPf2Tokens + tl];
-                cin[g][j] = reinterpret_cast<const int*>(S)[(2 * KS + g) * kPf2Tokens + tl];
+                const uint8_t* pr = buf + P::OR + (g * P::TT + tl) * 32;
+                const int4 ci = *reinterpret_cast<const int4*>(pr);
+                o.cin[g][j] = v4i32{ci.x, ci.y, ci.z, ci.w};
+                const float4 sv = *reinterpret_cast<const float4*>(pr + 16);
+                pn.sc[g][j] = make_float2(sv.x, sv.y);
             }
         }
-        // MFMAs of the step
-        v4i32 d[KS][TPW][RTW];
+    };
+    auto mfma = [&](Ops& o, Pend& pn) __attribute__((always_inline)) {
 #pragma unroll
         for (int g = 0; g < KS; g++) {
-            if (g >= ng) break;
+            if (g < pn.ng) {
+                // INT4: 16x the odd / even nibbles in place (exact), matching the
+                // activations' [odd | even] order per chunk
+                if constexpr (BITS == 4) {
 #pragma unroll
-            for (int j = 0; j < TPW; j++) {
-                if (j >= nj) break;
-                const v4i32 z4 = {0, 0, 0, 0};
-#pragma unroll
-                for (int i = 0; i < RTW; i++) {
-                    if constexpr (G == 64)
-                        d[g][j][i] = __builtin_amdgcn_mfma_i32_16x16x64_i8(av[g][i], bv[g][j], z4, 0, 0, 0);
-                    else
-                        d[g][j][i] = __builtin_amdgcn_mfma_i32_16x16x32_i8(al[g][i], bl[g][j], z4, 0, 0, 0);
+                    for (int i = 0; i < RTW; i++) {
+                        if constexpr (G == 64) {
+                            const int x = o.av[g][i][0], y = o.av[g][i][1];
+                            o.av[g][i] = v4i32{x & (int)0xF0F0F0F0, y & (int)0xF0F0F0F0, (x << 4) & (int)0xF0F0F0F0,
+                                               (y << 4) & (int)0xF0F0F0F0};
+                        } else {
+                            const int v = (int)o.al[g][i];
+                            o.al[g][i] = (long)(unsigned)(v & (int)0xF0F0F0F0) |
+                                         ((long)((v << 4) & (int)0xF0F0F0F0) << 32);
+                        }
+                    }
                 }
-            }
-        }
-        // ordered folds
 #pragma unroll
-        for (int g = 0; g < KS; g++) {
-            if (g >= ng) break;
+                for (int j = 0; j < TPW; j++) {
+                    if (j < nj) {
 #pragma unroll
-            for (int j = 0; j < TPW; j++) {
-                if (j >= nj) break;
-#pragma unroll
-                for (int i = 0; i < RTW; i++) {
-                    const float wr[4] = {wsv[g][i].x, wsv[g][i].y, wsv[g][i].z, wsv[g][i].w};
-#pragma unroll
-                    for (int e = 0; e < 4; e++) {
-                        // d + 128*sum(q), exact (the INT4 dot is 16x the dot)
-                        const int du8 = (BITS == 4 ? d[g][j][i][e] >> 4 : d[g][j][i][e]) + cin[g][j];
-                        acc[j][i][e] =
-                            __builtin_fmaf(wr[e], __builtin_fmaf(gxs[g][j], (float)du8, -gxt[g][j]), acc[j][i][e]);
+                        for (int i = 0; i < RTW; i++) {
+                            if constexpr (G == 64)
+                                pn.d[g][j][i] = __builtin_amdgcn_mfma_i32_16x16x64_i8(o.av[g][i], o.bv[g][j], o.cin[g][j], 0, 0, 0);
+                            else
+                                pn.d[g][j][i] = __builtin_amdgcn_mfma_i32_16x16x32_i8(o.al[g][i], o.bl[g][j], o.cin[g][j], 0, 0, 0);
+                        }
                     }
                 }
             }
         }
     };
-    // step s: fetch s + 2 into the set that held s (written to LDS during
-    // step s - 1), consume LDS buffer s & 1, write s + 1 (fetched during
-    // step s - 1) to the other buffer.  The fetches are unconditional, past
-    // the last step they repeat it: every path then has the same loads in
-    // flight, and waiting for one set never waits for the other.
-    Regs R0, R1;
-    fetch(0, R0);
-    fetch(min(1, nsteps - 1), R1);
-    put(0, 0, R0);
-    __syncthreads();
-    for (int s = 0; s < nsteps; s += 2) {
-        fetch(min(s + 2, nsteps - 1), R0);
-        compute(s);
-        if (s + 1 < nsteps) put(s + 1, 1, R1);
-        __syncthreads();
-        if (s + 1 >= nsteps) break;
-        fetch(min(s + 3, nsteps - 1), R1);
-        compute(s + 1);
-        if (s + 2 < nsteps) put(s + 2, 0, R0);
-        __syncthreads();
+    auto fold = [&](const Pend& pn) __attribute__((always_inline)) {
+#pragma unroll
+        for (int g = 0; g < KS; g++) {
+            if (g < pn.ng) {
+#pragma unroll
+                for (int j = 0; j < TPW; j++) {
+                    if (j < nj) {
+#pragma unroll
+                        for (int i = 0; i < RTW; i++) {
+                            const float wr[4] = {pn.wsv[g][i].x, pn.wsv[g][i].y, pn.wsv[g][i].z, pn.wsv[g][i].w};
+#pragma unroll
+                            for (int e = 0; e < 4; e++) {
+                                const int dv = pn.d[g][j][i][e];
+                                acc[j][i][e] = __builtin_fmaf(
+                                    wr[e], __builtin_fmaf(pn.sc[g][j].x, (float)(BITS == 4 ? dv >> 4 : dv), -pn.sc[g][j].y),
+                                    acc[j][i][e]);
+                            }
+                        }
+                    }
+                }
+            }
+        }
+    };
+    auto barrier = []() __attribute__((always_inline)) { asm volatile("s_barrier" ::: "memory"); };
+    // step s (buffer k = s % NST): request stage s + NST - 1; read stage s;
+    // fold step s - 1; MFMAs of step s; wait for this wave's part of stage
+    // s + 1; barrier (every wave's part of s + 1 has landed and every wave
+    // is done reading stage s, which the next step refills)
+    Pend pa, pb;       // MFMA results of even / odd steps
+    pa.ng = pb.ng = 0;
+    auto step = [&](int s, int k, Pend& cur, Pend& prev) __attribute__((always_inline)) {
+        if (s + NST - 1 < nsteps) issue(s + NST - 1, bufs[(k + NST - 1) % NST]);
+        Ops o;
+        if (nj > 0) read(s, bufs[k], o, cur);
+        if constexpr (PIPE) {
+            if (nj > 0 && s > 0) fold(prev);
+            if (nj > 0) mfma(o, cur);
+        } else if (nj > 0) {
+            mfma(o, cur);
+            fold(cur);
+        }
+        if (s + 1 < nsteps) {
+            if (s + NST - 1 < nsteps) wait_stages<P, NST - 2>(wv);
+            else wait_vmcnt<0>();
+            barrier();
+        }
+    };
+#pragma unroll
+    for (int i = 0; i < NST - 1; i++)
+        if (i < nsteps) issue(i, bufs[i]);
+    if (nsteps >= NST - 1) wait_stages<P, NST - 2>(wv);
+    else wait_vmcnt<0>();
+    barrier();
+    // unrolled by 2 * NST: buffer and result set both known at compile time
+    for (int s = 0; s < nsteps; s += 2 * NST) {
+#pragma unroll
+        for (int k = 0; k < 2 * NST; k++)
+            if (s + k < nsteps) {
+                if (k % 2 == 0) step(s + k, k % NST, pa, pb);
+                else step(s + k, k % NST, pb, pa);
+            }
     }
-    // out[t][r]: rows 16i + 4c + e of tile i, token 16 (wv + NW j) + l16
+    if (PIPE && nj > 0) fold((nsteps - 1) % 2 == 0 ? pa : pb);
+    // out[t][r]: rows 16i + 4c + e of the wave's tile i, token 16j + l16
 #pragma unroll
     for (int j = 0; j < TPW; j++) {
-        const int t = t0 + 16 * (wv + NW * j) + l16;
+        const int t = t0 + tw0 + 16 * j + l16;
         if (j >= nj || t >= T) continue;
 #pragma unroll
-        for (int i = 0; i < RTW; i++)
+        for (int i = 0; i < RTW; i++) {
+            const int r = r0 + rw0 + 16 * i + 4 * c;
+            float* o = out + (size_t)t * ldo + r;
+            if (r + 3 < rows && (ldo & 3) == 0 && (reinterpret_cast<uintptr_t>(o) & 15) == 0) {
+                *reinterpret_cast<float4*>(o) = make_float4(acc[j][i][0], acc[j][i][1], acc[j][i][2], acc[j][i][3]);
+            } else {
 #pragma unroll
-            for (int e = 0; e < 4; e++) {
-                const int r = r0 + 16 * i + 4 * c + e;
-                if (r < rows) out[(size_t)t * ldo + r] = acc[j][i][e];
+                for (int e = 0; e < 4; e++)
+                    if (r + e < rows) o[e] = acc[j][i][e];
             }
+        }
     }
 }
 
@@ -352,10 +410,13 @@ __global__ __launch_bounds__(256) void k_pf_swiglu_quant(const float* __restrict
     }
     const float s = q8_scale(group_max<G>(fabsf(g)));
     const int q = q8_value_fast(g, s, q8_recip(s));
-    if (pf.xqp) pf_emit<G>(pf, i, q, s, in);
+    if (pf.xqp) {
+        const size_t t = i / n;
+        pf_emit<G>(pf, (int)t, (int)(i - t * n), q, s, in);
+    }
     if (in) {
         if (xq) xq[i] = (int8_t)q;
-        if ((i % G) == 0) xs[i / G] = s;
+        if (xs && (i % G) == 0) xs[i / G] = s;
     }
 }
 
