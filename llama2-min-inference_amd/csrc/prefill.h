@@ -72,12 +72,21 @@ __device__ __forceinline__ void wait_vmcnt() {
     __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (0x7 << 4) | (0xF << 8));
 }
 
+// LDS bank spreading: the 16-byte units of a row's (a token's) group are
+// stored XOR-permuted by a key from the row (token) index, so that the 8
+// lanes of a ds_read_b128 phase (16 of a b64 phase), which read the same
+// chunk of consecutive rows, fall in distinct banks (32 banks of 4 bytes).
+__host__ __device__ constexpr int pf_swz(int units, int x) {
+    return units == 4 ? (x >> 1) & 3 : units == 2 ? (x >> 2) & 1 : 0;
+}
+
 // Batched GEMM geometry.  A workgroup computes RT rows x TT tokens with
 // WR x WT waves, each RTW 16-row tiles x TPW 16-token tiles; the columns
 // advance in steps of SC (KS groups).  A step's stage in LDS:
 //   A   [KS][RT][GB]   weight bytes of each row and group (GB = G*BITS/8)
 //   B   [KS][TT][G]    the tokens' permuted activations
 //   R   [KS][TT]       32-byte records (pf_record)
+// with the 16-byte units of each row (token) and group permuted by pf_swz
 //   W   [KS][RT]       weight scales
 // each region filled by 64-lane DMA instructions (16-byte units; 4-byte
 // ones for W), instruction k of the stage issued by wave k % NW.
@@ -142,12 +151,13 @@ __global__ __launch_bounds__(WR * WT * L2Q_WAVE) void k_pf_gemm3(
     const int nb = cols / G, nsteps = (cols + SC - 1) / SC, nfull = cols / SC;
     const int rowbytes = cols * BITS / 8;
 
-    // source of this lane's unit in DMA instruction k at step s (clamped)
+    // source of this lane's unit in DMA instruction k at step s (clamped;
+    // only step 0 is asked for, later steps advance it by `stride`)
     auto src = [&](int k, int s) __attribute__((always_inline)) -> const uint8_t* {
         if (k < P::NA) {
             const int u = min(k * 64 + lane, P::AU - 1);
             const int g = u / (P::RT * P::GB / 16), rem = u % (P::RT * P::GB / 16);
-            const int r = rem / (P::GB / 16), part = rem % (P::GB / 16);
+            const int r = rem / (P::GB / 16), part = (rem % (P::GB / 16)) ^ pf_swz(P::GB / 16, r);
             const int col = s * SC + g * G;
             const int off = col < cols ? col * BITS / 8 + part * 16 : rowbytes - 16;
             return w + (size_t)min(r0 + r, rows - 1) * rowbytes + off;
@@ -156,7 +166,7 @@ __global__ __launch_bounds__(WR * WT * L2Q_WAVE) void k_pf_gemm3(
         if (k < P::NB) {
             const int u = min(k * 64 + lane, P::BU - 1);
             const int g = u / (P::TT * G / 16), rem = u % (P::TT * G / 16);
-            const int t = rem / (G / 16), part = rem % (G / 16);
+            const int t = rem / (G / 16), part = (rem % (G / 16)) ^ pf_swz(G / 16, t);
             const int col = s * SC + g * G;
             const int off = col < cols ? col + part * 16 : cols - 16;
             return reinterpret_cast<const uint8_t*>(xqp) + (size_t)min(t0 + t, T - 1) * cols + off;
@@ -166,7 +176,7 @@ __global__ __launch_bounds__(WR * WT * L2Q_WAVE) void k_pf_gemm3(
             const int u = min(k * 64 + lane, P::RU - 1);
             const int g = u / (2 * P::TT), t = (u / 2) % P::TT;
             return reinterpret_cast<const uint8_t*>(rec + (size_t)min(s * KS + g, nb - 1) * T + min(t0 + t, T - 1)) +
-                   16 * (u & 1);
+                   16 * ((u & 1) ^ pf_swz(2, t));
         }
         k -= P::NR;
         const int u = min(k * 64 + lane, P::WU - 1);
@@ -183,23 +193,43 @@ __global__ __launch_bounds__(WR * WT * L2Q_WAVE) void k_pf_gemm3(
     const uint8_t* p0[P::NK];
 #pragma unroll
     for (int kk = 0; kk < P::NK; kk++) p0[kk] = src(min(wv + P::NW * kk, P::N - 1), 0);
+    // step s: every unit's source is its step-0 source advanced s steps; in
+    // a last, partial step the units of groups past the end (whose sources
+    // would lie past the rows) are masked off: unit u of a region with UG
+    // units per group belongs to group u / UG, so a lane of instruction k
+    // (the region's k-th) is live when lane < ng * UG - 64 * k (wave-uniform
+    // bound)
     auto issue = [&](int s, uint8_t* buf) __attribute__((always_inline)) {
-        const bool fast = s < nfull;
+        const bool full = s < nfull;
+        const int ng = min(KS, nb - s * KS);
 #pragma unroll
         for (int kk = 0; kk < P::NK; kk++) {
             const int k = wv + P::NW * kk;
             if (k < P::N) {
-                const uint8_t* a = fast ? p0[kk] + (size_t)s * stride(k) : src(k, s);
-                if (k < P::NA) dma_lds<16>(a, buf + k * 1024);
-                else if (k < P::NA + P::NB) dma_lds<16>(a, buf + P::OB + (k - P::NA) * 1024);
-                else if (k < P::NA + P::NB + P::NR) dma_lds<16>(a, buf + P::OR + (k - P::NA - P::NB) * 1024);
-                else dma_lds<4>(a, buf + P::OWS + (k - P::NA - P::NB - P::NR) * 256);
+                const uint8_t* a = p0[kk] + (size_t)s * stride(k);
+                if (k < P::NA) {
+                    if (full || lane < ng * (P::RT * P::GB / 16) - 64 * k) dma_lds<16>(a, buf + k * 1024);
+                } else if (k < P::NA + P::NB) {
+                    const int kb = k - P::NA;
+                    if (full || lane < ng * (P::TT * G / 16) - 64 * kb) dma_lds<16>(a, buf + P::OB + kb * 1024);
+                } else if (k < P::NA + P::NB + P::NR) {
+                    const int kr = k - P::NA - P::NB;
+                    if (full || lane < ng * (2 * P::TT) - 64 * kr) dma_lds<16>(a, buf + P::OR + kr * 1024);
+                } else {
+                    const int kw = k - P::NA - P::NB - P::NR;
+                    if (full || lane < ng * P::RT - 64 * kw) dma_lds<4>(a, buf + P::OWS + kw * 256);
+                }
             }
         }
     };
 
     constexpr int CB = P::GB / 4, CX = G / 4;    // bytes per MFMA lane chunk: weights, activations
     const int c = lane / 16, l16 = lane % 16;
+    // this lane's chunk within its row's / token's group after pf_swz (rows
+    // and tokens of a lane differ by multiples of 16, which leave the key)
+    const int offa = 16 * ((c * CB / 16) ^ pf_swz(P::GB / 16, l16)) + c * CB % 16;
+    const int offb = 16 * ((c * CX / 16) ^ pf_swz(G / 16, l16)) + c * CX % 16;
+    const int offr = 16 * pf_swz(2, l16);
     const int rw0 = (wv % WR) * 16 * RTW, tw0 = (wv / WR) * 16 * TPW;
     const int left = T - t0 - tw0;
     const int nj = left <= 0 ? 0 : min(TPW, (left + 15) / 16);   // token tiles with tokens (wave-uniform)
@@ -228,7 +258,7 @@ __global__ __launch_bounds__(WR * WT * L2Q_WAVE) void k_pf_gemm3(
         for (int g = 0; g < KS; g++) {
 #pragma unroll
             for (int i = 0; i < RTW; i++) {
-                const uint8_t* pa = buf + (g * P::RT + rw0 + 16 * i + l16) * P::GB + c * CB;
+                const uint8_t* pa = buf + (g * P::RT + rw0 + 16 * i + l16) * P::GB + offa;
                 if constexpr (G == 64) {
                     if constexpr (BITS == 8) {
                         const int4 v = *reinterpret_cast<const int4*>(pa);
@@ -250,7 +280,7 @@ __global__ __launch_bounds__(WR * WT * L2Q_WAVE) void k_pf_gemm3(
 #pragma unroll
             for (int j = 0; j < TPW; j++) {
                 const int tl = tw0 + 16 * j + l16;
-                const uint8_t* pb = buf + P::OB + (g * P::TT + tl) * G + c * CX;
+                const uint8_t* pb = buf + P::OB + (g * P::TT + tl) * G + offb;
                 if constexpr (G == 64) {
                     const int4 v = *reinterpret_cast<const int4*>(pb);
                     o.bv[g][j] = v4i32{v.x, v.y, v.z, v.w};
@@ -259,9 +289,9 @@ __global__ __launch_bounds__(WR * WT * L2Q_WAVE) void k_pf_gemm3(
                     o.bl[g][j] = (long)(unsigned)v.x | ((long)v.y << 32);
                 }
                 const uint8_t* pr = buf + P::OR + (g * P::TT + tl) * 32;
-                const int4 ci = *reinterpret_cast<const int4*>(pr);
+                const int4 ci = *reinterpret_cast<const int4*>(pr + offr);
                 o.cin[g][j] = v4i32{ci.x, ci.y, ci.z, ci.w};
-                const float4 sv = *reinterpret_cast<const float4*>(pr + 16);
+                const float4 sv = *reinterpret_cast<const float4*>(pr + (16 ^ offr));
                 pn.sc[g][j] = make_float2(sv.x, sv.y);
             }
         }
