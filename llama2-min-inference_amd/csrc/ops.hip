@@ -518,24 +518,24 @@ void pf3_launch(const uint8_t* w, const float* ws, int rows, int cols, const int
                        cols, xqp, rec, T, out, ldo);
 }
 
-// The three workgroup shapes of the batched GEMM (16x16 MFMA tiles; SC =
+// The two workgroup shapes of the batched GEMM (16x16 MFMA tiles; SC =
 // columns per step, a multiple of the group):
-//   big    64 rows x 64 tokens, waves 2 x 2 of 32 x 32, one group per step
-//   mid    32 rows x 64 tokens, waves 2 x 2 of 16 x 32, two groups per step
-//   small  32 rows x 32 tokens, waves 2 x 2 of 16 x 16, four groups per step
+//   wide   64 rows x 64 tokens, 8 waves (2 x 4) of 32 x 16, two groups per step
+//   small  32 rows x 32 tokens, 4 waves (2 x 2) of 16 x 16, four groups per step
 // A step's fixed costs (barrier, DMA wait, LDS and MFMA latency) are spread
-// over the waves resident on a SIMD and over the work of the step: large
-// tiles do the least LDS traffic and unpacking per output, small tiles
-// with long steps keep every SIMD busy when there are few rows (the ordered
-// fold cannot split the columns).  Measured on MI355X at the 7B shapes, T =
-// 127: w1|w3 (22016 rows) big, qkv (12288) mid, wo and w2 (4096) small.
-enum PfShape { kPfBig, kPfMid, kPfSmall };
+// over the waves resident on a SIMD and over the work of the step: the
+// wide tile does less LDS traffic and unpacking per output, the small tile
+// with long steps keeps every SIMD busy when there are few rows (the
+// ordered fold cannot split the columns).  Measured on MI355X at the 7B
+// shapes, T = 127: qkv and w1|w3 wide, wo and w2 small (other shapes
+// tried: 64 x 64 with 4 waves of 32 x 32, 32 x 64 with 16 x 32, 8-wave
+// 64 x 128 and 128 x 64, one to eight groups per step, 3 to 5 stages).
+enum PfShape { kPfWide, kPfSmall };
 
 template <int B_, int G_>
 void pf3_shape(PfShape shp, const uint8_t* w, const float* ws, int rows, int cols, const int8_t* xqp,
                const PfRecord* rec, int T, float* out, int ldo, hipStream_t st) {
-    if (shp == kPfBig) pf3_launch<B_, G_, 2, 2, 2, 2, G_, 4, false>(w, ws, rows, cols, xqp, rec, T, out, ldo, st);
-    else if (shp == kPfMid) pf3_launch<B_, G_, 1, 2, 2, 2, 2 * G_, 3, false>(w, ws, rows, cols, xqp, rec, T, out, ldo, st);
+    if (shp == kPfWide) pf3_launch<B_, G_, 2, 1, 2, 4, 2 * G_, 3, false>(w, ws, rows, cols, xqp, rec, T, out, ldo, st);
     else pf3_launch<B_, G_, 1, 1, 2, 2, 4 * G_, 4, false>(w, ws, rows, cols, xqp, rec, T, out, ldo, st);
 }
 
@@ -553,15 +553,13 @@ int launch_pf_gemm(int bits, int group, const void* w, const float* ws, int rows
         set_error("prefill gemm: weights, activations and records must be 16-byte aligned (rows of 16n bytes)");
         return L2Q_ERR_ARG;
     }
-    // the largest tile that still gives every CU 2.5 workgroups
+    // the wide tile when it gives every CU a workgroup
     int ncu = 0, dev = 0;
     if (hipGetDevice(&dev) != hipSuccess ||
         hipDeviceGetAttribute(&ncu, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || ncu <= 0)
         ncu = 256;
-    const long long want = (long long)ncu * 5 / 2;
-    const long long wg_big = (long long)((rows + 63) / 64) * ((T + 63) / 64);
-    const long long wg_mid = (long long)((rows + 31) / 32) * ((T + 63) / 64);
-    const PfShape shp = wg_big >= want ? kPfBig : wg_mid >= want ? kPfMid : kPfSmall;
+    const long long wg_wide = (long long)((rows + 63) / 64) * ((T + 63) / 64);
+    const PfShape shp = wg_wide >= ncu ? kPfWide : kPfSmall;
     const uint8_t* wb = static_cast<const uint8_t*>(w);
     if (bits == 4 && group == 64) pf3_shape<4, 64>(shp, wb, ws, rows, cols, xqp, rec, T, out, ldo, st);
     if (bits == 4 && group == 32) pf3_shape<4, 32>(shp, wb, ws, rows, cols, xqp, rec, T, out, ldo, st);
