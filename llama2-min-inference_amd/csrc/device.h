@@ -17,6 +17,11 @@ constexpr int kNormMaxPer = 8;       // elements per thread -> n <= 8192
 constexpr int kAttnThreads = 256;    // attention workgroup
 constexpr int kAttnMaxHs = 256;      // largest head size
 
+// Row pitch of the batched attention's score / probability rows [T][heads]
+// [pitch]: max_t rounded up to 4, so the p rows read as float4 stay aligned
+// for every cache length.
+__host__ __device__ constexpr int attn_b_pitch(int max_t) { return (max_t + 3) / 4 * 4; }
+
 typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 
 // 128-bit weight load.

@@ -552,7 +552,7 @@ int prefill_alloc(l2q_engine* e) {
     Arena a;
     const size_t o_xa = a.take(T * d * 4), o_xb = a.take(T * d * 4), o_qkv = a.take(T * qkv * 4);
     const size_t o_att = a.take(T * d * 4), o_wo = a.take(T * d * 4), o_h13 = a.take(T * 2 * h * 4);
-    const size_t o_ffn = a.take(T * d * 4), o_sc = a.take(T * c.n_heads * (size_t)e->max_t * 4);
+    const size_t o_ffn = a.take(T * d * 4), o_sc = a.take(T * c.n_heads * (size_t)attn_b_pitch(e->max_t) * 4);
     const size_t o_xqp = a.take(T * kmax), o_rec = a.take(T * nbmax * sizeof(PfRecord));
     const size_t o_tok = a.take(T * 4);
     HIPCHK(hipMalloc(&e->pfarena, align_up(a.used, 256)), "hipMalloc(prefill)");

@@ -67,7 +67,7 @@ __global__ __launch_bounds__(kNormThreads) void k_rmsnorm_quant(
         if (xs) xs += to / G;
     }
     const float* src = emb ? emb + (size_t)meta[0] * n : x;
-    float v[kNormMaxPer];
+    float v[kNormMaxPer], wv[kNormMaxPer];
 #pragma unroll
     for (int k = 0; k < kNormMaxPer; k++) {
         const int i = tid + k * kNormThreads;
@@ -78,6 +78,7 @@ __global__ __launch_bounds__(kNormThreads) void k_rmsnorm_quant(
             vs[i] = t;
         }
         v[k] = t;
+        wv[k] = i < n ? w[i] : 0.0f;   // the norm weights ride with the inputs: one round trip, not two
     }
     __syncthreads();
     if (tid < L2Q_WAVE) {
@@ -91,7 +92,7 @@ __global__ __launch_bounds__(kNormThreads) void k_rmsnorm_quant(
         const int i = tid + k * kNormThreads;
         if (k * kNormThreads >= n) break;   // uniform across the workgroup
         const bool in = i < n;
-        const float o = in ? w[i] * (inv * v[k]) : 0.0f;
+        const float o = in ? wv[k] * (inv * v[k]) : 0.0f;
         const float s = q8_scale(group_max<G>(fabsf(o)));
         const int q = q8_value_fast(o, s, q8_recip(s));
         if (pf.xqp) pf_emit<G>(pf, blockIdx.x, i, q, s, in);
@@ -687,7 +688,7 @@ __global__ __launch_bounds__(kSbThreads) void k_attn_scores_b(
 #pragma unroll
     for (int j = 0; j < kSbPer; j++) {
         const int qi = q0 + qg * kSbPer + j;
-        if (qi < T && t < nk && t <= pos0 + qi) scores[((size_t)qi * n_heads + h) * max_t + t] = sc[j] / rs;
+        if (qi < T && t < nk && t <= pos0 + qi) scores[((size_t)qi * n_heads + h) * attn_b_pitch(max_t) + t] = sc[j] / rs;
     }
 }
 
@@ -706,7 +707,7 @@ __global__ __launch_bounds__(kSmThreads) void k_attn_softmax_b(float* __restrict
     float* red = sm + (max_t + 3) / 4 * 4 + kRingSlack;    // [1] sum
     const int qi = blockIdx.x, h = blockIdx.y, lane = threadIdx.x;
     const int n = pos0 + qi + 1;
-    float* row = scores + ((size_t)qi * n_heads + h) * max_t;
+    float* row = scores + ((size_t)qi * n_heads + h) * attn_b_pitch(max_t);
     float m = -INFINITY;
     for (int t0 = 0; t0 < n; t0 += 8 * kSmThreads) {   // eight loads in flight per lane
         float v[8];
@@ -764,8 +765,8 @@ __global__ __launch_bounds__(kPvThreads) void k_attn_pv_b(const float* __restric
 #pragma unroll
         for (int k = 0; k < PPT; k++) {
             const int f = tid + kPvThreads * k, r = f / (kPvKeys / 4), c4 = f % (kPvKeys / 4);
-            rp[k] = *reinterpret_cast<const float4*>(p + ((size_t)min(q0 + r, T - 1) * n_heads + h) * max_t +
-                                                     min(t0 + 4 * c4, max_t - 4));
+            rp[k] = *reinterpret_cast<const float4*>(p + ((size_t)min(q0 + r, T - 1) * n_heads + h) * attn_b_pitch(max_t) +
+                                                     min(t0 + 4 * c4, attn_b_pitch(max_t) - 4));
         }
     };
     auto stage = [&]() {

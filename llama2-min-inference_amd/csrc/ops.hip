@@ -398,7 +398,7 @@ int launch_attention_exact(const float* q, const float* kcache, const float* vca
             case 128: return go_attn_fused<128>(q, kcache, vcache, out, meta, pos, kv_mul, n_heads, max_t, k_il, st);
         }
     }
-    if (T > 1 && !meta && max_t % 4 == 0) {
+    if (T > 1 && !meta) {
         // a batch of queries: K and V rows shared over the queries (same
         // operations, same order as the per-query kernels below)
         const int nk = pos + T;

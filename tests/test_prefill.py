@@ -93,6 +93,16 @@ def test_engine_prefill_c1_q8(gpu_lib, c1_q8, n_prompt, split):
     prefill_then_greedy(c1_q8, prompt, 12, 256, split)
 
 
+@pytest.mark.parametrize("max_steps", [61, 150])
+def test_engine_prefill_cache_length_not_multiple_of_4(gpu_lib, c1_q8, max_steps):
+    """A KV cache of 61 / 150 positions: the batched attention's score rows
+    are padded to a multiple of 4 internally (its float4 reads), so such
+    engines run the same batched kernels and stay bit-exact."""
+    print(f"prefill c1 q8 max_steps={max_steps}", flush=True)
+    prompt = [int(v) for v in host.uniform_ints(min(50, max_steps - 8), 78, 100, 3, 32000)]
+    prefill_then_greedy(c1_q8, prompt, 6, max_steps)
+
+
 def test_engine_prefill_c1_q4_g32(gpu_lib):
     ck = host.synth_checkpoint(host.config_15m(), 4, 32, seed=99, q4_divisor=8.0)
     prompt = [int(v) for v in host.uniform_ints(40, 5, 100, 3, 32000)]
