@@ -70,10 +70,27 @@ __device__ __forceinline__ float dpp_f(float v) {
     return __int_as_float(dpp_i<CTRL>(__float_as_int(v)));
 }
 
+// The values of lanes l and l ^ 16 (l ^ 32), in some order, without an
+// LDS round trip: v_permlane16_swap / v_permlane32_swap (gfx950) of v with
+// itself leave {v[l], v[l ^ 16]} in the two results of every lane (checked
+// on the GPU), so a commutative reduction of the pair is the xor-16 (xor-32)
+// butterfly step.
+__device__ __forceinline__ void xor16_pair(unsigned v, unsigned& a, unsigned& b) {
+    const auto r = __builtin_amdgcn_permlane16_swap(v, v, false, false);
+    a = r[0];
+    b = r[1];
+}
+__device__ __forceinline__ void xor32_pair(unsigned v, unsigned& a, unsigned& b) {
+    const auto r = __builtin_amdgcn_permlane32_swap(v, v, false, false);
+    a = r[0];
+    b = r[1];
+}
+
 // Max / integer sum over aligned groups of `W` consecutive lanes (W a power
 // of two <= 64): every lane gets the result of its own group.  Both are
 // exact in any order; within a 16-lane row the butterfly is xor1, xor2,
-// half mirror, mirror (after the last two steps every lane has seen all 16).
+// half mirror, mirror (after the last two steps every lane has seen all 16),
+// across rows the permlane swaps.
 // group_max on unsigned values (the bit patterns of non-negative floats
 // order as the floats do): one integer max per step, with the lane move
 // folded into it.
@@ -83,8 +100,9 @@ __device__ __forceinline__ unsigned group_umax(unsigned v) {
     if (W >= 4) v = max(v, (unsigned)dpp_i<kDppXor2>((int)v));
     if (W >= 8) v = max(v, (unsigned)dpp_i<kDppHalfMirror>((int)v));
     if (W >= 16) v = max(v, (unsigned)dpp_i<kDppMirror>((int)v));
-    if (W >= 32) v = max(v, (unsigned)__shfl_xor((int)v, 16, L2Q_WAVE));
-    if (W >= 64) v = max(v, (unsigned)__shfl_xor((int)v, 32, L2Q_WAVE));
+    unsigned a, b;
+    if (W >= 32) { xor16_pair(v, a, b); v = max(a, b); }
+    if (W >= 64) { xor32_pair(v, a, b); v = max(a, b); }
     return v;
 }
 
@@ -94,8 +112,9 @@ __device__ __forceinline__ float group_max(float v) {
     if (W >= 4) v = fmaxf(v, dpp_f<kDppXor2>(v));
     if (W >= 8) v = fmaxf(v, dpp_f<kDppHalfMirror>(v));
     if (W >= 16) v = fmaxf(v, dpp_f<kDppMirror>(v));
-    if (W >= 32) v = fmaxf(v, __shfl_xor(v, 16, L2Q_WAVE));
-    if (W >= 64) v = fmaxf(v, __shfl_xor(v, 32, L2Q_WAVE));
+    unsigned a, b;
+    if (W >= 32) { xor16_pair(__float_as_uint(v), a, b); v = fmaxf(__uint_as_float(a), __uint_as_float(b)); }
+    if (W >= 64) { xor32_pair(__float_as_uint(v), a, b); v = fmaxf(__uint_as_float(a), __uint_as_float(b)); }
     return v;
 }
 
@@ -105,8 +124,9 @@ __device__ __forceinline__ int group_isum(int v) {
     if (W >= 4) v += dpp_i<kDppXor2>(v);
     if (W >= 8) v += dpp_i<kDppHalfMirror>(v);
     if (W >= 16) v += dpp_i<kDppMirror>(v);
-    if (W >= 32) v += __shfl_xor(v, 16, L2Q_WAVE);
-    if (W >= 64) v += __shfl_xor(v, 32, L2Q_WAVE);
+    unsigned a, b;
+    if (W >= 32) { xor16_pair((unsigned)v, a, b); v = (int)(a + b); }
+    if (W >= 64) { xor32_pair((unsigned)v, a, b); v = (int)(a + b); }
     return v;
 }
 

@@ -575,13 +575,15 @@ int launch_pf_embed(const float* emb, const int* tokens, float* x, int dim, int 
 
 int launch_pf_swiglu_quant(const float* h13, int n, int T, int group, int8_t* xq, float* xs, hipStream_t st,
                            const PfOperand* pf) {
-    if (n <= 0 || n % group || (group != 32 && group != 64)) { set_error("prefill swiglu: bad n=%d", n); return L2Q_ERR_ARG; }
+    if (n <= 0 || n % group || (group != 32 && group != 64) || T < 1 || T > 65535) {
+        set_error("prefill swiglu: bad n=%d T=%d", n, T);
+        return L2Q_ERR_ARG;
+    }
     PfOperand po;
     if (int rc = pf_operand(pf, xq, xs, n, T, &po, "prefill swiglu")) return rc;
-    const size_t total = (size_t)T * n;
-    const unsigned blocks = (unsigned)((total + 255) / 256);
-    if (group == 32) hipLaunchKernelGGL(k_pf_swiglu_quant<32>, dim3(blocks), dim3(256), 0, st, h13, n, T, xq, xs, po);
-    else hipLaunchKernelGGL(k_pf_swiglu_quant<64>, dim3(blocks), dim3(256), 0, st, h13, n, T, xq, xs, po);
+    const dim3 grid((unsigned)((n + 255) / 256), (unsigned)T);   // groups never straddle a 256-element block
+    if (group == 32) hipLaunchKernelGGL(k_pf_swiglu_quant<32>, grid, dim3(256), 0, st, h13, n, T, xq, xs, po);
+    else hipLaunchKernelGGL(k_pf_swiglu_quant<64>, grid, dim3(256), 0, st, h13, n, T, xq, xs, po);
     return check_launch("prefill_swiglu_quant");
 }
 

@@ -429,21 +429,20 @@ template <int G>
 __global__ __launch_bounds__(256) void k_pf_swiglu_quant(const float* __restrict__ h13, int n, int T,
                                                          int8_t* __restrict__ xq, float* __restrict__ xs,
                                                          PfOperand pf) {
-    const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;   // element of the flattened [T][n]
-    const bool in = i < (size_t)T * n;
+    // workgroup (x, token): elements j of one token, no division
+    const int t = blockIdx.y, j = blockIdx.x * blockDim.x + threadIdx.x;
+    const bool in = j < n;
+    const size_t i = (size_t)t * n + j;   // element of the flattened [T][n]
     float g = 0.0f;
     if (in) {
-        const size_t t = i / n, j = i - t * n;
-        float h = h13[t * 2 * n + 2 * j];   // (built with -ffp-contract=off, as k_swiglu_quant)
+        const float2 hh = reinterpret_cast<const float2*>(h13 + (size_t)t * 2 * n)[j];   // (w1, w3) of unit j
+        float h = hh.x;   // (built with -ffp-contract=off, as k_swiglu_quant)
         h *= (1.0f / (1.0f + exp_runq(-h)));
-        g = h * h13[t * 2 * n + 2 * j + 1];
+        g = h * hh.y;
     }
     const float s = q8_scale(group_max<G>(fabsf(g)));
     const int q = q8_value_fast(g, s, q8_recip(s));
-    if (pf.xqp) {
-        const size_t t = i / n;
-        pf_emit<G>(pf, (int)t, (int)(i - t * n), q, s, in);
-    }
+    if (pf.xqp) pf_emit<G>(pf, t, j, q, s, in);
     if (in) {
         if (xq) xq[i] = (int8_t)q;
         if (xs && (i % G) == 0) xs[i / G] = s;
