@@ -217,6 +217,18 @@ struct PfOperand {
     int T;
 };
 
+// The qkv GEMM's fused epilogue (EPI 1): rows [0, dim) are q, [dim, dim +
+// kv_dim) k and the rest v of token t at position pos0 + t; q and k pairs
+// (2i, 2i + 1) are rotated as k_rope_kv_append rotates them (runq.c:
+// 351-365) — q stored to out, k and v appended to the caches — so no
+// separate RoPE / append launch follows.
+struct PfRope {
+    const float* rope;
+    float* kcache;
+    float* vcache;
+    int pos0, dim, kv_dim, hs, max_t, k_il;
+};
+
 // The record: xt = q8_bias_term(xs, sum(q)) (runq.c:137) and c =
 // 128*sum(q), the MFMA's accumulator input, so that D = d + 128*sum(q)
 // comes out of the MFMA.  INT4 weights enter the MFMA as 16x their value,

@@ -580,8 +580,8 @@ int prefill_chunk(l2q_engine* e, const int* tokens, int T, int pos0, bool want_l
     if ((rc = launch_pf_embed(e->emb, e->pf_tok, e->pf_xa, d, T, st))) return rc;
     // every quantizing producer writes the GEMM operand (permuted q, records) itself
     const PfOperand pod{e->pf_xqp, e->pf_rec, bits, d, T}, poh{e->pf_xqp, e->pf_rec, bits, h, T};
-    auto gemm = [&](const uint8_t* w, const float* ws, int rows, int cols, float* out) {
-        return launch_pf_gemm(bits, G, w, ws, rows, cols, e->pf_xqp, e->pf_rec, T, out, rows, st);
+    auto gemm = [&](const uint8_t* w, const float* ws, int rows, int cols, float* out, const PfRope* rp = nullptr) {
+        return launch_pf_gemm(bits, G, w, ws, rows, cols, e->pf_xqp, e->pf_rec, T, out, rows, st, rp);
     };
     for (int l = 0; l < c.n_layers; l++) {
         float* kc = e->kcache + (size_t)l * kv * e->max_t;
@@ -590,11 +590,10 @@ int prefill_chunk(l2q_engine* e, const int* tokens, int T, int pos0, bool want_l
         if ((rc = launch_rmsnorm_quant(e->pf_xa, nullptr, nullptr, l == 0 ? nullptr : e->pf_ffn, e->pf_xb,
                                        e->rms_att + (size_t)l * d, d, G, nullptr, nullptr, st, T, &pod)))
             return rc;
+        // q, k, v rows with RoPE and the KV append fused into the GEMM's stores
+        const PfRope rp{e->rope, kc, vc, pos0, d, kv, e->hs, e->max_t, 1};
         if ((rc = gemm(e->qkv_w + (size_t)l * qkv_rows * e->rowb_d, e->qkv_s + (size_t)l * qkv_rows * nbd, qkv_rows,
-                       d, e->pf_qkv)))
-            return rc;
-        if ((rc = launch_rope_kv_append(e->pf_qkv, e->pf_qkv + d, e->pf_qkv + d + kv, kc, vc, e->rope, nullptr,
-                                        pos0, d, kv, e->hs, e->max_t, st, T, qkv_rows, 1)))
+                       d, e->pf_qkv, &rp)))
             return rc;
         if ((rc = launch_attention_exact(e->pf_qkv, kc, vc, e->pf_att, e->pf_scores, 0, nullptr, pos0, c.n_heads,
                                          c.n_kv_heads, e->hs, e->max_t, st, T, qkv_rows, -1, 1)))

@@ -104,8 +104,9 @@ inline int score_splits(int n) {
 constexpr int kPfMaxTokens = 128;    // tokens per prefill chunk
 int launch_pf_prep(int bits, int group, const int8_t* xq, const float* xs, int K, int T, int8_t* xqp, PfRecord* rec,
                    hipStream_t st);
+// rope (optional): the qkv form, q rotated to out, k and v appended to the caches (PfRope).
 int launch_pf_gemm(int bits, int group, const void* w, const float* ws, int rows, int cols, const int8_t* xqp,
-                   const PfRecord* rec, int T, float* out, int ldo, hipStream_t st);
+                   const PfRecord* rec, int T, float* out, int ldo, hipStream_t st, const PfRope* rope = nullptr);
 int launch_pf_embed(const float* emb, const int* tokens, float* x, int dim, int T, hipStream_t st);
 int launch_pf_swiglu_quant(const float* h13, int n, int T, int group, int8_t* xq, float* xs, hipStream_t st,
                            const PfOperand* pf = nullptr);

@@ -509,13 +509,13 @@ namespace {
 
 // One workgroup shape of the batched GEMM: waves WR x WT of RTW x TPW
 // 16x16 tiles, SC columns per step.
-template <int B_, int G_, int RTW, int TPW, int WR, int WT, int SC, int NST, bool PIPE>
+template <int B_, int G_, int RTW, int TPW, int WR, int WT, int SC, int NST, bool PIPE, int EPI>
 void pf3_launch(const uint8_t* w, const float* ws, int rows, int cols, const int8_t* xqp, const PfRecord* rec, int T,
-                float* out, int ldo, hipStream_t st) {
+                float* out, int ldo, const PfRope& rp, hipStream_t st) {
     using P = Pf3<B_, G_, RTW, TPW, WR, WT, SC>;
     const dim3 grid((unsigned)((rows + P::RT - 1) / P::RT), (unsigned)((T + P::TT - 1) / P::TT));
-    hipLaunchKernelGGL((k_pf_gemm3<B_, G_, RTW, TPW, WR, WT, SC, NST, PIPE>), grid, dim3(P::NT), 0, st, w, ws, rows,
-                       cols, xqp, rec, T, out, ldo);
+    hipLaunchKernelGGL((k_pf_gemm3<B_, G_, RTW, TPW, WR, WT, SC, NST, PIPE, EPI>), grid, dim3(P::NT), 0, st, w, ws,
+                       rows, cols, xqp, rec, T, out, ldo, rp);
 }
 
 // The two workgroup shapes of the batched GEMM (16x16 MFMA tiles; SC =
@@ -532,17 +532,28 @@ void pf3_launch(const uint8_t* w, const float* ws, int rows, int cols, const int
 // 64 x 128 and 128 x 64, one to eight groups per step, 3 to 5 stages).
 enum PfShape { kPfWide, kPfSmall };
 
-template <int B_, int G_>
+template <int B_, int G_, int EPI>
 void pf3_shape(PfShape shp, const uint8_t* w, const float* ws, int rows, int cols, const int8_t* xqp,
-               const PfRecord* rec, int T, float* out, int ldo, hipStream_t st) {
-    if (shp == kPfWide) pf3_launch<B_, G_, 2, 1, 2, 4, 2 * G_, 3, false>(w, ws, rows, cols, xqp, rec, T, out, ldo, st);
-    else pf3_launch<B_, G_, 1, 1, 2, 2, 4 * G_, 4, false>(w, ws, rows, cols, xqp, rec, T, out, ldo, st);
+               const PfRecord* rec, int T, float* out, int ldo, const PfRope& rp, hipStream_t st) {
+    if (shp == kPfWide)
+        pf3_launch<B_, G_, 2, 1, 2, 4, 2 * G_, 3, false, EPI>(w, ws, rows, cols, xqp, rec, T, out, ldo, rp, st);
+    else
+        pf3_launch<B_, G_, 1, 1, 2, 2, 4 * G_, 4, false, EPI>(w, ws, rows, cols, xqp, rec, T, out, ldo, rp, st);
+}
+
+template <int EPI>
+void pf3_bits(int bits, int group, PfShape shp, const uint8_t* w, const float* ws, int rows, int cols,
+              const int8_t* xqp, const PfRecord* rec, int T, float* out, int ldo, const PfRope& rp, hipStream_t st) {
+    if (bits == 4 && group == 64) pf3_shape<4, 64, EPI>(shp, w, ws, rows, cols, xqp, rec, T, out, ldo, rp, st);
+    if (bits == 4 && group == 32) pf3_shape<4, 32, EPI>(shp, w, ws, rows, cols, xqp, rec, T, out, ldo, rp, st);
+    if (bits == 8 && group == 64) pf3_shape<8, 64, EPI>(shp, w, ws, rows, cols, xqp, rec, T, out, ldo, rp, st);
+    if (bits == 8 && group == 32) pf3_shape<8, 32, EPI>(shp, w, ws, rows, cols, xqp, rec, T, out, ldo, rp, st);
 }
 
 }  // namespace
 
 int launch_pf_gemm(int bits, int group, const void* w, const float* ws, int rows, int cols, const int8_t* xqp,
-                   const PfRecord* rec, int T, float* out, int ldo, hipStream_t st) {
+                   const PfRecord* rec, int T, float* out, int ldo, hipStream_t st, const PfRope* rope) {
     if (T < 1 || rows < 1 || cols <= 0 || (group != 32 && group != 64) || cols % group || (bits != 4 && bits != 8) ||
         cols % 32 || ldo < rows) {
         set_error("prefill gemm: bad rows=%d cols=%d T=%d group=%d bits=%d", rows, cols, T, group, bits);
@@ -561,10 +572,18 @@ int launch_pf_gemm(int bits, int group, const void* w, const float* ws, int rows
     const long long wg_wide = (long long)((rows + 63) / 64) * ((T + 63) / 64);
     const PfShape shp = wg_wide >= ncu ? kPfWide : kPfSmall;
     const uint8_t* wb = static_cast<const uint8_t*>(w);
-    if (bits == 4 && group == 64) pf3_shape<4, 64>(shp, wb, ws, rows, cols, xqp, rec, T, out, ldo, st);
-    if (bits == 4 && group == 32) pf3_shape<4, 32>(shp, wb, ws, rows, cols, xqp, rec, T, out, ldo, st);
-    if (bits == 8 && group == 64) pf3_shape<8, 64>(shp, wb, ws, rows, cols, xqp, rec, T, out, ldo, st);
-    if (bits == 8 && group == 32) pf3_shape<8, 32>(shp, wb, ws, rows, cols, xqp, rec, T, out, ldo, st);
+    if (rope) {
+        const PfRope& r = *rope;
+        if (!r.rope || !r.kcache || !r.vcache || r.hs <= 0 || r.hs % 2 || r.dim % r.hs || r.kv_dim % r.hs ||
+            r.kv_dim > r.dim || rows != r.dim + 2 * r.kv_dim || r.pos0 < 0 || r.pos0 + T > r.max_t ||
+            (r.k_il && r.hs % 4)) {
+            set_error("prefill gemm: bad RoPE/KV epilogue arguments");
+            return L2Q_ERR_ARG;
+        }
+        pf3_bits<1>(bits, group, shp, wb, ws, rows, cols, xqp, rec, T, out, ldo, r, st);
+    } else {
+        pf3_bits<0>(bits, group, shp, wb, ws, rows, cols, xqp, rec, T, out, ldo, PfRope{}, st);
+    }
     return check_launch("prefill_gemm");
 }
 

@@ -132,10 +132,11 @@ __device__ __forceinline__ void wait_stages(int wv) {
 // whose latency the barrier and the next step's reads cover.  Rows, tokens
 // and columns past the ends are clamped into the operands (those outputs
 // are never stored).
-template <int BITS, int G, int RTW, int TPW, int WR, int WT, int SC, int NST, bool PIPE>
+template <int BITS, int G, int RTW, int TPW, int WR, int WT, int SC, int NST, bool PIPE, int EPI>
 __global__ __launch_bounds__(WR * WT * L2Q_WAVE) void k_pf_gemm3(
     const uint8_t* __restrict__ w, const float* __restrict__ ws, int rows, int cols,
-    const int8_t* __restrict__ xqp, const PfRecord* __restrict__ rec, int T, float* __restrict__ out, int ldo) {
+    const int8_t* __restrict__ xqp, const PfRecord* __restrict__ rec, int T, float* __restrict__ out, int ldo,
+    PfRope rp) {
     using P = Pf3<BITS, G, RTW, TPW, WR, WT, SC>;
     constexpr int KS = P::KS;
     static_assert(NST >= 3 && NST <= 5, "pipeline depth");
@@ -403,6 +404,38 @@ __global__ __launch_bounds__(WR * WT * L2Q_WAVE) void k_pf_gemm3(
         for (int i = 0; i < RTW; i++) {
             const int r = r0 + rw0 + 16 * i + 4 * c;
             float* o = out + (size_t)t * ldo + r;
+            if constexpr (EPI == 1) {
+                // pairs (r, r + 1), (r + 2, r + 3): r is a multiple of 4
+                const int pos = rp.pos0 + t;
+#pragma unroll
+                for (int m = 0; m < 2; m++) {
+                    const int rr = r + 2 * m;
+                    if (rr >= rows) continue;
+                    const float v0 = acc[j][i][2 * m], v1 = acc[j][i][2 * m + 1];
+                    if (rr < rp.dim + rp.kv_dim) {
+                        const int e = rr < rp.dim ? rr : rr - rp.dim;
+                        const int hd = e % rp.hs;
+                        const float cs = rp.rope[(size_t)pos * rp.hs + hd];
+                        const float sn = rp.rope[(size_t)pos * rp.hs + hd + 1];
+                        const float a0 = __builtin_fmaf(v0, cs, -(v1 * sn));
+                        const float a1 = __builtin_fmaf(v0, sn, v1 * cs);
+                        if (rr < rp.dim) {
+                            o[2 * m] = a0;
+                            o[2 * m + 1] = a1;
+                        } else {
+                            const size_t ko = k_index(rp.k_il, e / rp.hs, pos, hd, rp.hs, rp.max_t);
+                            rp.kcache[ko] = a0;
+                            rp.kcache[ko + 1] = a1;
+                        }
+                    } else {
+                        const int e = rr - rp.dim - rp.kv_dim;
+                        const size_t vo = ((size_t)(e / rp.hs) * rp.max_t + pos) * rp.hs + e % rp.hs;
+                        rp.vcache[vo] = v0;
+                        rp.vcache[vo + 1] = v1;
+                    }
+                }
+                continue;
+            }
             if (r + 3 < rows && (ldo & 3) == 0 && (reinterpret_cast<uintptr_t>(o) & 15) == 0) {
                 *reinterpret_cast<float4*>(o) = make_float4(acc[j][i][0], acc[j][i][1], acc[j][i][2], acc[j][i][3]);
             } else {
