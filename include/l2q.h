@@ -139,11 +139,17 @@ int l2q_engine_prefill(l2q_engine* e, const int* tokens, int n, int pos0,
                                   partials merged in split order), with the
                                   fp32 cache; equal to the reference's
                                   attention up to rounding (relative error
-                                  ~1e-6), not bit for bit.  The default is the
+                                  ~1e-6), not bit for bit, from
+                                  L2Q_ATTN_SPLIT_FROM positions on (shorter
+                                  contexts run the exact one-kernel attention,
+                                  the faster there).  The default is the
                                   reference's exact order (runq.c:367-391).
                                   head_size 48, 64 or 128; not with
                                   L2Q_ENGINE_KV_INT8.  No counterpart in the
                                   reference. */
+
+#define L2Q_ATTN_SPLIT_FROM 320   /* positions from which L2Q_ENGINE_ATTN_SPLIT
+                                     splits the attention */
 
 /* l2q_engine_create with option flags (0 gives l2q_engine_create). */
 int l2q_engine_create_ex(const l2q_config* cfg, const void* weights,

@@ -103,6 +103,13 @@ using namespace l2q;
 
 namespace {
 
+// Positions from which the tolerance mode runs the split-context attention:
+// measured on MI355X at the 7B shape, the exact one-kernel attention takes
+// 8.8 us at 256 positions and grows ~0.017 us per position, the split form
+// stays near 9 us (they cross near 280).
+constexpr int kAttnSplitFrom = L2Q_ATTN_SPLIT_FROM;
+
+
 #define HIPCHK(call, what)                            \
     do {                                              \
         hipError_t e_ = (call);                       \
@@ -235,7 +242,7 @@ int enqueue_step(l2q_engine* e, hipStream_t st, float* dbg_x, float* dbg_tmp, bo
                 rc = launch_attention_kv8_split(e->q, e->kvf, e->kvf + kv, e->k8 + co, e->v8 + co, e->ks + so,
                                                 e->vs + so, e->att, e->apart, e->acnt, e->aS, e->meta, 0, c.n_heads,
                                                 c.n_kv_heads, e->hs, e->max_t, st);
-        } else if (e->flags & L2Q_ENGINE_ATTN_SPLIT) {
+        } else if ((e->flags & L2Q_ENGINE_ATTN_SPLIT) && !fused) {
             rc = launch_attention_flash(e->q, kc, vc, e->att, e->apart, e->acnt, e->aS, e->meta, 0, c.n_heads,
                                         c.n_kv_heads, e->hs, e->max_t, 1, st);
         } else {
@@ -504,11 +511,14 @@ int build(l2q_engine* e, const void* weights, size_t weights_bytes) {
     if ((rc = step_setup(e, ncu))) return rc;
     HIPCHK(hipEventCreate(&e->ev0), "hipEventCreate");
     HIPCHK(hipEventCreate(&e->ev1), "hipEventCreate");
-    // short contexts: one-kernel attention where the head size has it
-    // (the split-context attention serves every position in one graph)
-    e->g_switch = kv8 ? L2Q_KV8_SPLIT_FROM : attention_fused_max();
-    const bool fused = e->step || asplit || kv8 || attention_fused_ok(e->hs);
-    const bool need_long = !e->step && !asplit && (!fused || e->max_t > e->g_switch);
+    // short contexts: one-kernel attention where the head size has it; the
+    // tolerance mode (L2Q_ENGINE_ATTN_SPLIT) switches to the split-context
+    // kernel from kAttnSplitFrom positions, where it overtakes the exact
+    // one (below, the exact kernel is the faster and the more exact)
+    e->g_switch = kv8 ? L2Q_KV8_SPLIT_FROM
+                      : asplit ? std::min(attention_fused_max(), kAttnSplitFrom) : attention_fused_max();
+    const bool fused = e->step || kv8 || attention_fused_ok(e->hs);
+    const bool need_long = !e->step && (!fused || e->max_t > e->g_switch);
     for (int a = 0; a < 2; a++) {
         if (fused && (rc = capture(e, a, true, &e->graph[a][0], &e->exec[a][0]))) return rc;
         if (need_long && (rc = capture(e, a, false, &e->graph[a][1], &e->exec[a][1]))) return rc;

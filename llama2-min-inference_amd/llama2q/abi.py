@@ -19,6 +19,7 @@ L2Q_ENGINE_KV_INT8 = 1
 L2Q_ENGINE_STEP_KERNEL = 2
 L2Q_ENGINE_ATTN_SPLIT = 4
 L2Q_KV8_SPLIT_FROM = 1024
+L2Q_ATTN_SPLIT_FROM = 320
 L2Q_ATTN_K_INTERLEAVED = 1
 L2Q_ATTN_ONE_KERNEL = 2
 L2Q_ATTN_TWO_KERNELS = 4

@@ -1,10 +1,12 @@
 """The engine's tolerance-mode attention (L2Q_ENGINE_ATTN_SPLIT).
 
-The decode attention then runs split over the context in one kernel
-(k_attn_flash: per-split softmax partials merged in split order by the
-last workgroup of each head) instead of in the reference's exact serial
-order (runq.c:367-391, softmax :307-318).  The kernel itself is within
-1e-5 of the exact order (test_gpu_ops.py::
+From L2Q_ATTN_SPLIT_FROM positions on, the decode attention then runs split
+over the context in one kernel (k_attn_flash: per-split softmax partials
+merged in split order by the last workgroup of each head) instead of in the
+reference's exact serial order (runq.c:367-391, softmax :307-318); below it
+the engine runs the exact one-kernel attention (faster there), so those
+positions are bit-identical to the default engine.  The split kernel itself
+is within 1e-5 of the exact order (test_gpu_ops.py::
 test_attention_split_context_tolerance).  Inside the engine that rounding
 difference does not stay at 1e-6: every matmul input is re-quantized to
 int8 per group (runq.c:117-139), and a difference of one ulp flips an int8
@@ -22,11 +24,11 @@ rms(e)):
   * the deeper layers and the logits stay within loose bounds, and the
     top-1 token agrees at a stated fraction of positions.
 
-Measured on MI355X: c1 first layer median 6.8e-7 (99% of positions <= 1e-4,
-max 1.5e-2), all layers <= 2.8e-2, top-1 agreement 253/256; c5 first layer
-median 7.6e-4 (max 4.2e-2), all layers <= 0.39, top-1 agreement 205/256.
-The exact order stays the engine default; its bit-exact tests are
-test_gpu_engine.py and test_gpu_c5.py.
+Measured on MI355X with the split at every position: c1 first layer median
+6.8e-7 (99% of positions <= 1e-4, max 1.5e-2), all layers <= 2.8e-2, top-1
+agreement 253/256; c5 first layer median 7.6e-4 (max 4.2e-2), all layers
+<= 0.39, top-1 agreement 205/256.  The exact order stays the engine default;
+its bit-exact tests are test_gpu_engine.py and test_gpu_c5.py.
 """
 import json
 import os
@@ -36,7 +38,7 @@ import numpy as np
 import pytest
 
 from conftest import GOLDEN
-from llama2q import host
+from llama2q import abi, host
 from llama2q.model import Engine
 import oracle_py as O
 
@@ -55,29 +57,35 @@ def rel(a, e) -> float:
 
 
 def test_attn_split_c1_teacher_forced(gpu_lib):
-    """c1 (stories15M shape, INT8 g32): 16 prompt ids, then the oracle's
-    greedy ids, 256 positions; every position's residual streams and logits
-    against the oracle's exact order."""
-    ck = host.synth_checkpoint(host.config_15m(), 8, 32, seed=1234)
+    """A c1-shaped model (stories15M dims, INT8 g32) with a 448-position
+    cache: 16 prompt ids, then the oracle's greedy ids; positions below
+    L2Q_ATTN_SPLIT_FROM bit-identical to the oracle (the exact attention),
+    the 128 beyond within the tolerance bars."""
+    n_pos, first_split = 448, abi.L2Q_ATTN_SPLIT_FROM
+    ck = host.synth_checkpoint(host.make_config(288, 768, 6, 6, 6, 32000, n_pos), 8, 32, seed=1234)
     prompt = [int(v) for v in host.uniform_ints(16, 1234, 100, 3, 32000)]
-    eng = Engine(ck, max_steps=256, attn_split=True)
-    orc = O.Oracle(ck.cfg.as_list(), ck.weights, 8, 32, max_t=256)
+    eng = Engine(ck, max_steps=n_pos, attn_split=True)
+    orc = O.Oracle(ck.cfg.as_list(), ck.weights, 8, 32, max_t=n_pos)
     token, first, deep, agree = prompt[0], [], [], 0
-    for pos in range(256):
+    for pos in range(n_pos):
         xg, lg = eng.forward_debug(token, pos)
         xo, lo = orc.forward(token, pos, layers=True)
-        np.testing.assert_array_equal(xg[0], xo[0])          # the embedding row
-        first.append(rel(xg[1], xo[1]))
-        deep.append(max([rel(xg[i], xo[i]) for i in range(2, xo.shape[0])] + [rel(lg, lo)]))
-        agree += int(np.argmax(lg)) == int(np.argmax(lo))
+        if pos + 1 <= first_split:
+            np.testing.assert_array_equal(xg, xo, err_msg=f"exact-attention position {pos}")
+            np.testing.assert_array_equal(lg, lo, err_msg=f"exact-attention position {pos}")
+        else:
+            np.testing.assert_array_equal(xg[0], xo[0])          # the embedding row
+            first.append(rel(xg[1], xo[1]))
+            deep.append(max([rel(xg[i], xo[i]) for i in range(2, xo.shape[0])] + [rel(lg, lo)]))
+            agree += int(np.argmax(lg)) == int(np.argmax(lo))
         token = prompt[pos + 1] if pos + 1 < len(prompt) else int(np.argmax(lo))
     eng.close()
     orc.close()
     first = np.array(first)
-    assert first.max() <= FIRST_MAX, f"first layer rel {first.max():.3g} at position {int(first.argmax())}"
+    assert first.max() <= FIRST_MAX, f"first layer rel {first.max():.3g} at position {int(first.argmax()) + first_split}"
     assert np.mean(first <= 1e-4) >= 0.95, f"first layer within 1e-4 at only {np.mean(first <= 1e-4):.3f}"
     assert max(deep) <= 0.1, f"deeper layers / logits rel {max(deep):.3g}"
-    assert agree >= 240, f"top-1 agreement {agree}/256"
+    assert agree >= 0.9 * len(first), f"top-1 agreement {agree}/{len(first)}"
 
 
 def test_attn_split_c5_teacher_forced(gpu_lib):
@@ -104,6 +112,9 @@ def test_attn_split_c5_teacher_forced(gpu_lib):
         agree += int(np.argmax(ls)) == int(np.argmax(le))
     split.close()
     exact.close()
+    # below L2Q_ATTN_SPLIT_FROM the tolerance mode runs the exact attention
+    n_exact = abi.L2Q_ATTN_SPLIT_FROM - len(prompt) + 1
+    assert max(first[:n_exact]) == 0.0 and max(deep[:n_exact]) == 0.0, "positions before the split point"
     first = np.array(first)
     assert first.max() <= FIRST_MAX, f"first layer rel {first.max():.3g} at position {int(first.argmax()) + 127}"
     assert np.median(first) <= 5e-3, f"first layer median rel {np.median(first):.3g}"
