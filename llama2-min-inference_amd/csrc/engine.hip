@@ -605,11 +605,11 @@ int prefill_chunk(l2q_engine* e, const int* tokens, int T, int pos0, bool want_l
         if ((rc = gemm(e->qkv_w + (size_t)l * qkv_rows * e->rowb_d, e->qkv_s + (size_t)l * qkv_rows * nbd, qkv_rows,
                        d, e->pf_qkv, &rp)))
             return rc;
-        if ((rc = launch_attention_exact(e->pf_qkv, kc, vc, e->pf_att, e->pf_scores, 0, nullptr, pos0, c.n_heads,
-                                         c.n_kv_heads, e->hs, e->max_t, st, T, qkv_rows, -1, 1)))
+        // attention, its output quantized into the wo operand
+        if ((rc = launch_attention_prefill(e->pf_qkv, kc, vc, e->pf_att, e->pf_scores, pos0, c.n_heads, c.n_kv_heads,
+                                           e->hs, e->max_t, st, T, qkv_rows, 1, G, &pod)))
             return rc;
         // wo
-        if ((rc = launch_quantize(e->pf_att, T * d, G, nullptr, nullptr, st, &pod))) return rc;
         if ((rc = gemm(e->wo_w + (size_t)l * d * e->rowb_d, e->wo_s + (size_t)l * d * nbd, d, d, e->pf_wo))) return rc;
         // x = xb + wo -> xa; RMSNorm; SwiGLU(w1 x, w3 x); w2
         if ((rc = launch_rmsnorm_quant(e->pf_xb, nullptr, nullptr, e->pf_wo, e->pf_xa, e->rms_ffn + (size_t)l * d, d,

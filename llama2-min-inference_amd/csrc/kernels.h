@@ -820,6 +820,135 @@ __global__ __launch_bounds__(kPvThreads) void k_attn_pv_b(const float* __restric
     }
 }
 
+// k_attn_pvq_b: softmax + p*V (+ the Q8 quantization of the output) of a
+// batch of queries whose context fits kPqMaxKeys, in one kernel: workgroup
+// (head, kPqQueries-query block) with HS/4 threads per query.  The query's
+// threads take the max of its score row, e_t = exp_runq(s_t - max) into LDS
+// (k_attn_softmax_b's operations), one thread sums e in position order
+// (serial_sum), p_t = e_t / sum in place; then thread (query, element quad)
+// runs the p*V chains over V staged in 64-key chunks (k_attn_pv_b's order).
+// With pf.xqp set the output goes straight to the wo GEMM operand: the
+// G/4 threads of a group take its max, Q8 scale and values (k_quantize's
+// operations) and write the permuted bytes and the record; else out [T][dim]
+// (fp32).  Same bits as k_attn_softmax_b + k_attn_pv_b (+ k_quantize).
+constexpr int kPqQueries = 32, kPqMaxKeys = 256, kPqKeys = 64;
+constexpr int kPqPitch = kPqMaxKeys + 4;   // e / p rows (16-byte aligned for serial_sum)
+template <int HS, int G>
+__global__ __launch_bounds__(kPqQueries * HS / 4) void k_attn_pvq_b(
+    const float* __restrict__ scores, const float* __restrict__ vcache, float* __restrict__ out, int pos0, int T,
+    int kv_mul, int n_heads, int max_t, PfOperand pf) {
+#pragma clang fp contract(off)
+    constexpr int TPQ = HS / 4;                  // threads per query = element quads
+    constexpr int NT = kPqQueries * TPQ;
+    static_assert(TPQ == 16 || TPQ == 32, "head size 64 or 128");
+    static_assert(HS % G == 0, "groups inside a head");
+    __shared__ __attribute__((aligned(16))) float ep[kPqQueries * kPqPitch + 4 * 8];   // + serial_sum's read-ahead
+    __shared__ float4 vt[kPqKeys][TPQ];
+    __shared__ float red[kPqQueries];
+    const int h = blockIdx.x, q0 = blockIdx.y * kPqQueries;
+    const int tid = threadIdx.x, ql = tid / TPQ, quad = tid % TPQ;
+    const int qi = q0 + ql;
+    const int n = qi < T ? pos0 + qi + 1 : 0;                 // keys of this thread's query
+    const int nblk = pos0 + min(q0 + kPqQueries, T);           // keys of the block's last query
+    float* e = ep + ql * kPqPitch;
+    // V rows in 64-key chunks for the p*V below, the next chunk in registers
+    // while the current one is folded; the first is requested before the
+    // softmax, which it does not depend on
+    const float* vb = vcache + (size_t)(h / kv_mul) * max_t * HS;
+    constexpr int VPT = kPqKeys * TPQ / NT;                   // float4 of V per thread per chunk
+    static_assert(VPT * NT == kPqKeys * TPQ, "V staging");
+    float4 rv0, rv1;
+    static_assert(VPT == 2, "two float4 of V per thread");
+    auto fetch = [&](int c) __attribute__((always_inline)) {
+        const int f0 = tid, f1 = tid + NT;
+        rv0 = *reinterpret_cast<const float4*>(vb + (size_t)min(c * kPqKeys + f0 / TPQ, nblk - 1) * HS + 4 * (f0 % TPQ));
+        rv1 = *reinterpret_cast<const float4*>(vb + (size_t)min(c * kPqKeys + f1 / TPQ, nblk - 1) * HS + 4 * (f1 % TPQ));
+    };
+    const int nchunks = (nblk + kPqKeys - 1) / kPqKeys;
+    if (nchunks > 0) fetch(0);
+    // softmax (k_attn_softmax_b): max, exp into LDS, serial sum, divide
+    const float* row = scores + ((size_t)min(qi, T - 1) * n_heads + h) * attn_b_pitch(max_t);
+    constexpr int KMAX = kPqMaxKeys / TPQ;                    // score loads per thread, all in flight at once
+    float sv[KMAX];
+#pragma unroll
+    for (int k = 0; k < KMAX; k++) sv[k] = row[min(quad + TPQ * k, max(n - 1, 0))];
+    float m = -INFINITY;
+#pragma unroll
+    for (int k = 0; k < KMAX; k++)
+        if (quad + TPQ * k < n) m = fmaxf(m, sv[k]);
+    m = group_max<TPQ>(m);
+#pragma unroll
+    for (int k = 0; k < KMAX; k++)
+        if (quad + TPQ * k < n) e[quad + TPQ * k] = exp_runq(sv[k] - m);
+    __syncthreads();
+    if (quad == 0 && n > 0) red[ql] = serial_sum(e, n);
+    __syncthreads();
+    const float sum = red[ql];
+    for (int t = quad; t < n; t += TPQ) e[t] = e[t] / sum;
+    float4 acc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    for (int c = 0; c < nchunks; c++) {
+        __syncthreads();   // the previous chunk's reads are done (and, first, the p rows written)
+        vt[tid / TPQ][tid % TPQ] = rv0;
+        vt[(tid + NT) / TPQ][(tid + NT) % TPQ] = rv1;
+        __syncthreads();
+        if (c + 1 < nchunks) fetch(c + 1);
+        const int tn = min(kPqKeys, n - c * kPqKeys);
+        const float* pr = e + c * kPqKeys;
+        int t = 0;
+        for (; t + 8 <= tn; t += 8) {
+            float pv[8];
+            float4 v[8];
+#pragma unroll
+            for (int k = 0; k < 8; k++) {
+                pv[k] = pr[t + k];
+                v[k] = vt[t + k][quad];
+            }
+#pragma unroll
+            for (int k = 0; k < 8; k++) {
+                acc.x = __builtin_fmaf(pv[k], v[k].x, acc.x);
+                acc.y = __builtin_fmaf(pv[k], v[k].y, acc.y);
+                acc.z = __builtin_fmaf(pv[k], v[k].z, acc.z);
+                acc.w = __builtin_fmaf(pv[k], v[k].w, acc.w);
+            }
+        }
+        for (; t < tn; t++) {
+            const float pv = pr[t];
+            const float4 v = vt[t][quad];
+            acc.x = __builtin_fmaf(pv, v.x, acc.x);
+            acc.y = __builtin_fmaf(pv, v.y, acc.y);
+            acc.z = __builtin_fmaf(pv, v.z, acc.z);
+            acc.w = __builtin_fmaf(pv, v.w, acc.w);
+        }
+    }
+    const bool in = qi < T;
+    const int dim = n_heads * HS, e0 = h * HS + 4 * quad;    // first of this thread's four elements
+    if (!pf.xqp) {
+        if (in) *reinterpret_cast<float4*>(out + (size_t)qi * dim + e0) = acc;
+        return;
+    }
+    // Q8 of the output (k_quantize): the G/4 threads of a group
+    const float a0 = in ? acc.x : 0.0f, a1 = in ? acc.y : 0.0f, a2 = in ? acc.z : 0.0f, a3 = in ? acc.w : 0.0f;
+    const float amax = fmaxf(fmaxf(fabsf(a0), fabsf(a1)), fmaxf(fabsf(a2), fabsf(a3)));
+    const float s = q8_scale(group_max<G / 4>(amax));
+    const float r = q8_recip(s);
+    const int qa = q8_value_fast(a0, s, r), qb = q8_value_fast(a1, s, r), qc = q8_value_fast(a2, s, r),
+              qd = q8_value_fast(a3, s, r);
+    const int sum_q = group_isum<G / 4>(qa + qb + qc + qd);
+    if (!in) return;
+    constexpr int CH = G / 4;
+    const int j0 = e0 % G;
+    int8_t* dst = pf.xqp + (size_t)qi * dim + (e0 - j0);
+    auto put = [&](int j, int qv) __attribute__((always_inline)) {
+        const int jj = j % CH;
+        dst[pf.bits == 4 ? j - jj + ((jj & 1) ? jj / 2 : CH / 2 + jj / 2) : j] = (int8_t)qv;
+    };
+    put(j0, qa);
+    put(j0 + 1, qb);
+    put(j0 + 2, qc);
+    put(j0 + 3, qd);
+    if (j0 == 0) pf.rec[(size_t)(e0 / G) * T + qi] = pf_record(s, sum_q, pf.bits);
+}
+
 // ---------------------------------------------------------------------------
 // Single-query attention in the reference's exact order in ONE kernel
 // (runq.c:367-391, softmax :307-318): the same operations as k_attn_scores

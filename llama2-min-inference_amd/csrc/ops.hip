@@ -378,6 +378,19 @@ int launch_attention_flash(const float* q, const float* kcache, const float* vca
     }
 }
 
+// The batched scores kernel (T > 1 queries at positions pos..pos+T-1).
+static int launch_attention_scores_b(const float* q, const float* kcache, float* scores, int pos, int T, int kv_mul,
+                                     int n_heads, int hs, int max_t, int q_stride, int k_il, hipStream_t st) {
+    const int nk = pos + T;
+    const size_t lds = attn_scores_b_lds_bytes(hs);
+    if (int rc = raise_lds_limit(reinterpret_cast<const void*>(&k_attn_scores_b), lds,
+                                 "attention: raising the LDS limit"))
+        return rc;
+    hipLaunchKernelGGL(k_attn_scores_b, dim3(n_heads, (nk + kSbKeys - 1) / kSbKeys, (T + kSbQueries - 1) / kSbQueries),
+                       dim3(kSbThreads), lds, st, q, kcache, scores, pos, T, kv_mul, n_heads, hs, max_t, q_stride, k_il);
+    return check_launch("attention_scores_b");
+}
+
 int launch_attention_exact(const float* q, const float* kcache, const float* vcache, float* out, float* scores,
                            int S, const int* meta, int pos, int n_heads, int n_kv_heads, int hs, int max_t,
                            hipStream_t st, int T, int q_stride, int fused, int k_il) {
@@ -401,15 +414,7 @@ int launch_attention_exact(const float* q, const float* kcache, const float* vca
     if (T > 1 && !meta) {
         // a batch of queries: K and V rows shared over the queries (same
         // operations, same order as the per-query kernels below)
-        const int nk = pos + T;
-        const size_t lds = attn_scores_b_lds_bytes(hs);
-        if (int rc = raise_lds_limit(reinterpret_cast<const void*>(&k_attn_scores_b), lds,
-                                     "attention: raising the LDS limit"))
-            return rc;
-        hipLaunchKernelGGL(k_attn_scores_b, dim3(n_heads, (nk + kSbKeys - 1) / kSbKeys, (T + kSbQueries - 1) / kSbQueries),
-                           dim3(kSbThreads), lds, st, q, kcache, scores, pos, T, kv_mul, n_heads, hs, max_t, q_stride,
-                           k_il);
-        int rc = check_launch("attention_scores_b");
+        int rc = launch_attention_scores_b(q, kcache, scores, pos, T, kv_mul, n_heads, hs, max_t, q_stride, k_il, st);
         if (rc) return rc;
         hipLaunchKernelGGL(k_attn_softmax_b, dim3(T, n_heads), dim3(kSmThreads), attn_softmax_b_lds_bytes(max_t), st,
                            scores, pos, n_heads, max_t);
@@ -429,6 +434,41 @@ int launch_attention_exact(const float* q, const float* kcache, const float* vca
     hipLaunchKernelGGL(k_attn_softmax_v, dim3(n_heads, (hs + kVDims - 1) / kVDims, T), dim3(kAttnThreads),
                        attn_v_lds_bytes(max_t), st, scores, vcache, out, meta, pos, kv_mul, hs, max_t);
     return check_launch("attention_softmax_v");
+}
+
+int launch_attention_prefill(const float* q, const float* kcache, const float* vcache, float* out, float* scores,
+                             int pos, int n_heads, int n_kv_heads, int hs, int max_t, hipStream_t st, int T,
+                             int q_stride, int k_il, int group, const PfOperand* pf) {
+    const bool fuse = T > 1 && (hs == 64 || hs == 128) && hs % group == 0 && pos + T <= kPqMaxKeys &&
+                      attention_shape_ok(n_heads, n_kv_heads, hs) && pos >= 0 && pos + T <= max_t &&
+                      attention_exact_ok(max_t) && (group == 32 || group == 64);
+    if (!fuse) {
+        int rc = launch_attention_exact(q, kcache, vcache, out, scores, 0, nullptr, pos, n_heads, n_kv_heads, hs,
+                                        max_t, st, T, q_stride, -1, k_il);
+        if (rc || !pf) return rc;
+        return launch_quantize(out, T * n_heads * hs, group, nullptr, nullptr, st, pf);
+    }
+    if (pf && (!pf->xqp || !pf->rec || (pf->bits != 4 && pf->bits != 8) || pf->K != n_heads * hs || pf->T != T)) {
+        set_error("attention prefill: bad GEMM operand");
+        return L2Q_ERR_ARG;
+    }
+    const int kv_mul = n_heads / n_kv_heads;
+    int rc = launch_attention_scores_b(q, kcache, scores, pos, T, kv_mul, n_heads, hs, max_t, q_stride, k_il, st);
+    if (rc) return rc;
+    const PfOperand po = pf ? *pf : PfOperand{nullptr, nullptr, 8, 1, 1};
+    const dim3 grid((unsigned)n_heads, (unsigned)((T + kPqQueries - 1) / kPqQueries));
+#define L2Q_PQ(HS_, G_)                                                                                              \
+    hipLaunchKernelGGL((k_attn_pvq_b<HS_, G_>), grid, dim3(kPqQueries * HS_ / 4), 0, st, scores, vcache, out, pos, T, \
+                       kv_mul, n_heads, max_t, po)
+    if (hs == 128) {
+        if (group == 64) L2Q_PQ(128, 64);
+        else L2Q_PQ(128, 32);
+    } else {
+        if (group == 64) L2Q_PQ(64, 64);
+        else L2Q_PQ(64, 32);
+    }
+#undef L2Q_PQ
+    return check_launch("attention_pvq_b");
 }
 
 bool kv8_shape_ok(int n_heads, int n_kv_heads, int hs, int max_t) {

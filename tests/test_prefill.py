@@ -116,6 +116,20 @@ def test_engine_prefill_7b_shape_int4_g64(gpu_lib):
     prefill_then_greedy(ck, prompt, 4, 64)
 
 
+@pytest.mark.parametrize("bits,group", [(4, 64), (8, 32)])
+@pytest.mark.parametrize("n_prompt,split", [(300, None), (200, 150)])
+def test_engine_prefill_fused_attention_chunks(gpu_lib, bits, group, n_prompt, split):
+    """Head size 128 (the fused softmax + p*V + quantize attention): a
+    300-position prompt prefills in chunks at positions 0, 128 (contexts of
+    up to 256: the fused kernel) and 256 (the three-kernel path); a second
+    call at pos0 = 150 mixes both; bit-exact against the oracle."""
+    print(f"prefill hs128 bits={bits} group={group} n={n_prompt} split={split}", flush=True)
+    cfg = host.make_config(512, 1024, 2, 4, 4, 32000, 512)
+    ck = host.synth_checkpoint(cfg, bits, group, seed=31 + bits, q4_divisor=7.0)
+    prompt = [int(v) for v in host.uniform_ints(n_prompt, 8, 100, 3, 32000)]
+    prefill_then_greedy(ck, prompt, 4, 512, split)
+
+
 def test_engine_prefill_rejects_bad_positions(gpu_lib, c1_q8):
     eng = Engine(c1_q8, max_steps=32)
     toks = np.arange(3, 13, dtype=np.int32)
