@@ -820,58 +820,150 @@ __global__ __launch_bounds__(kPvThreads) void k_attn_pv_b(const float* __restric
     }
 }
 
-// k_attn_pvq_b: softmax + p*V (+ the Q8 quantization of the output) of a
-// batch of queries whose context fits kPqMaxKeys, in one kernel: workgroup
-// (head, kPqQueries-query block) with HS/4 threads per query.  The query's
-// threads take the max of its score row, e_t = exp_runq(s_t - max) into LDS
-// (k_attn_softmax_b's operations), one thread sums e in position order
-// (serial_sum), p_t = e_t / sum in place; then thread (query, element quad)
-// runs the p*V chains over V staged in 64-key chunks (k_attn_pv_b's order).
-// With pf.xqp set the output goes straight to the wo GEMM operand: the
-// G/4 threads of a group take its max, Q8 scale and values (k_quantize's
-// operations) and write the permuted bytes and the record; else out [T][dim]
-// (fp32).  Same bits as k_attn_softmax_b + k_attn_pv_b (+ k_quantize).
-constexpr int kPqQueries = 32, kPqMaxKeys = 256, kPqKeys = 64;
+// k_attn_pf_b: the whole exact attention of a batch of queries whose
+// context fits kPqMaxKeys (+ the Q8 quantization of its output), in one
+// kernel: workgroup (head, kPqQueries-query block), HS/4 threads per query.
+//   scores   the block's q rows in LDS; K in 64-key chunks through LDS (the
+//            next chunk in registers while the current one is used); thread
+//            (key, query group) forms its 32*64/threads dots, each in
+//            k_attn_scores_b's order (products rounded and added in index
+//            order over hs & ~7 elements, the rest fused, / sqrtf(hs)),
+//            into the queries' LDS rows (causal pairs only);
+//   softmax  the query's threads: max, e_t = exp_runq(s_t - max); one thread
+//            sums e in position order (serial_sum); p_t = e_t / sum
+//            (k_attn_softmax_b's operations);
+//   p*V      thread (query, element quad), V staged in 64-key chunks, in
+//            position order (k_attn_pv_b's);
+//   out      with pf.xqp set, the wo GEMM operand: the G/4 threads of a
+//            group take its max, Q8 scale and values (k_quantize's) and
+//            write the permuted bytes and the record; else out [T][dim].
+// Same bits as k_attn_scores_b + k_attn_softmax_b + k_attn_pv_b (+
+// k_quantize), without three launches and the scores' round trip.
+constexpr int kPqQueries = 16, kPqMaxKeys = 256, kPqKeys = 64;
 constexpr int kPqPitch = kPqMaxKeys + 4;   // e / p rows (16-byte aligned for serial_sum)
 template <int HS, int G>
-__global__ __launch_bounds__(kPqQueries * HS / 4) void k_attn_pvq_b(
-    const float* __restrict__ scores, const float* __restrict__ vcache, float* __restrict__ out, int pos0, int T,
-    int kv_mul, int n_heads, int max_t, PfOperand pf) {
+__global__ __launch_bounds__(kPqQueries * HS / 4) void k_attn_pf_b(
+    const float* __restrict__ q, int q_stride, const float* __restrict__ kcache, int k_il,
+    const float* __restrict__ vcache, float* __restrict__ out, int pos0, int T, int kv_mul, int n_heads, int max_t,
+    PfOperand pf) {
 #pragma clang fp contract(off)
     constexpr int TPQ = HS / 4;                  // threads per query = element quads
     constexpr int NT = kPqQueries * TPQ;
+    constexpr int HSP = HS + 4;                  // LDS row pitch of q and K (floats)
+    constexpr int J = kPqQueries * kPqKeys / NT; // dot chains per thread
+    constexpr int KVP = kPqKeys * TPQ / NT;      // float4 of K / V per thread per chunk
     static_assert(TPQ == 16 || TPQ == 32, "head size 64 or 128");
     static_assert(HS % G == 0, "groups inside a head");
+    static_assert(KVP * NT == kPqKeys * TPQ && J * NT == kPqQueries * kPqKeys, "staging geometry");
     __shared__ __attribute__((aligned(16))) float ep[kPqQueries * kPqPitch + 4 * 8];   // + serial_sum's read-ahead
-    __shared__ float4 vt[kPqKeys][TPQ];
+    __shared__ __attribute__((aligned(16))) float qsm[kPqQueries * HSP];
+    __shared__ __attribute__((aligned(16))) float kvs[kPqKeys * HSP];                  // a K chunk, then V chunks
     __shared__ float red[kPqQueries];
-    const int h = blockIdx.x, q0 = blockIdx.y * kPqQueries;
+    const int h = blockIdx.x, q0 = blockIdx.y * kPqQueries, g = h / kv_mul;
     const int tid = threadIdx.x, ql = tid / TPQ, quad = tid % TPQ;
     const int qi = q0 + ql;
     const int n = qi < T ? pos0 + qi + 1 : 0;                 // keys of this thread's query
     const int nblk = pos0 + min(q0 + kPqQueries, T);           // keys of the block's last query
-    float* e = ep + ql * kPqPitch;
-    // V rows in 64-key chunks for the p*V below, the next chunk in registers
-    // while the current one is folded; the first is requested before the
-    // softmax, which it does not depend on
-    const float* vb = vcache + (size_t)(h / kv_mul) * max_t * HS;
-    constexpr int VPT = kPqKeys * TPQ / NT;                   // float4 of V per thread per chunk
-    static_assert(VPT * NT == kPqKeys * TPQ, "V staging");
-    float4 rv0, rv1;
-    static_assert(VPT == 2, "two float4 of V per thread");
-    auto fetch = [&](int c) __attribute__((always_inline)) {
-        const int f0 = tid, f1 = tid + NT;
-        rv0 = *reinterpret_cast<const float4*>(vb + (size_t)min(c * kPqKeys + f0 / TPQ, nblk - 1) * HS + 4 * (f0 % TPQ));
-        rv1 = *reinterpret_cast<const float4*>(vb + (size_t)min(c * kPqKeys + f1 / TPQ, nblk - 1) * HS + 4 * (f1 % TPQ));
-    };
     const int nchunks = (nblk + kPqKeys - 1) / kPqKeys;
-    if (nchunks > 0) fetch(0);
-    // softmax (k_attn_softmax_b): max, exp into LDS, serial sum, divide
-    const float* row = scores + ((size_t)min(qi, T - 1) * n_heads + h) * attn_b_pitch(max_t);
-    constexpr int KMAX = kPqMaxKeys / TPQ;                    // score loads per thread, all in flight at once
+    float* e = ep + ql * kPqPitch;
+    // K: float4 f of a chunk is (key r, column c4), consecutive lanes on
+    // consecutive keys with the interleaved layout (as k_attn_scores_b)
+    static_assert(KVP == 4, "four float4 of K / V per thread per chunk");
+    float4 kr0, kr1, kr2, kr3, vr0, vr1, vr2, vr3;   // (named: an indexed array of them went to scratch)
+    // K float4 f of a chunk: (key r, column c4)
+    auto kaddr = [&](int c, int f) __attribute__((always_inline)) {
+        int r, c4;
+        if (k_il) { c4 = f / kPqKeys; r = f - c4 * kPqKeys; }
+        else { r = f / TPQ; c4 = f - r * TPQ; }
+        return reinterpret_cast<const float4*>(kcache + k_index(k_il, g, min(c * kPqKeys + r, nblk - 1), 4 * c4, HS, max_t));
+    };
+    auto kslot = [&](int f) __attribute__((always_inline)) {
+        int r, c4;
+        if (k_il) { c4 = f / kPqKeys; r = f - c4 * kPqKeys; }
+        else { r = f / TPQ; c4 = f - r * TPQ; }
+        return reinterpret_cast<float4*>(kvs + r * HSP + 4 * c4);
+    };
+    auto kfetch = [&](int c) __attribute__((always_inline)) {
+        kr0 = *kaddr(c, tid);
+        kr1 = *kaddr(c, tid + NT);
+        kr2 = *kaddr(c, tid + 2 * NT);
+        kr3 = *kaddr(c, tid + 3 * NT);
+    };
+    auto kstore = [&]() __attribute__((always_inline)) {
+        *kslot(tid) = kr0;
+        *kslot(tid + NT) = kr1;
+        *kslot(tid + 2 * NT) = kr2;
+        *kslot(tid + 3 * NT) = kr3;
+    };
+    const float* vb = vcache + (size_t)g * max_t * HS;
+    auto vaddr = [&](int c, int f) __attribute__((always_inline)) {
+        return reinterpret_cast<const float4*>(vb + (size_t)min(c * kPqKeys + f / TPQ, nblk - 1) * HS + 4 * (f % TPQ));
+    };
+    auto vfetch = [&](int c) __attribute__((always_inline)) {
+        vr0 = *vaddr(c, tid);
+        vr1 = *vaddr(c, tid + NT);
+        vr2 = *vaddr(c, tid + 2 * NT);
+        vr3 = *vaddr(c, tid + 3 * NT);
+    };
+    kfetch(0);
+    {   // the block's q rows (one float4 per thread)
+        const float4 v = *reinterpret_cast<const float4*>(q + (size_t)min(qi, T - 1) * q_stride + (size_t)h * HS + 4 * quad);
+        *reinterpret_cast<float4*>(qsm + ql * HSP + 4 * quad) = v;
+    }
+    vfetch(0);   // the first V chunk rides behind the scores
+    // scores
+    const int tl = tid % kPqKeys, qg = tid / kPqKeys;
+    const float rs = sqrtf((float)HS);
+    constexpr int NV = (HS & ~7) >> 2;   // float4 blocks added unfused, then the fused rest
+    for (int c = 0; c < nchunks; c++) {
+        __syncthreads();   // the previous chunk's dots are done (and, first, the q rows stored)
+        kstore();
+        __syncthreads();
+        if (c + 1 < nchunks) kfetch(c + 1);
+        const float4* k4 = reinterpret_cast<const float4*>(kvs + tl * HSP);
+        const float4* qb = reinterpret_cast<const float4*>(qsm + qg * J * HSP);
+        float sc[J];
+#pragma unroll
+        for (int j = 0; j < J; j++) sc[j] = 0.0f;
+#pragma unroll 4
+        for (int cc = 0; cc < NV; cc++) {
+            const float4 kv = k4[cc];
+            float4 qv[J];
+#pragma unroll
+            for (int j = 0; j < J; j++) qv[j] = qb[j * (HSP / 4) + cc];
+#pragma unroll
+            for (int j = 0; j < J; j++) {
+                sc[j] = sc[j] + qv[j].x * kv.x;
+                sc[j] = sc[j] + qv[j].y * kv.y;
+                sc[j] = sc[j] + qv[j].z * kv.z;
+                sc[j] = sc[j] + qv[j].w * kv.w;
+            }
+        }
+#pragma unroll
+        for (int cc = NV; cc < TPQ; cc++) {
+            const float4 kv = k4[cc];
+#pragma unroll
+            for (int j = 0; j < J; j++) {
+                const float4 qv = qb[j * (HSP / 4) + cc];
+                sc[j] = __builtin_fmaf(qv.x, kv.x, sc[j]);
+                sc[j] = __builtin_fmaf(qv.y, kv.y, sc[j]);
+                sc[j] = __builtin_fmaf(qv.z, kv.z, sc[j]);
+                sc[j] = __builtin_fmaf(qv.w, kv.w, sc[j]);
+            }
+        }
+        const int t = c * kPqKeys + tl;
+#pragma unroll
+        for (int j = 0; j < J; j++) {
+            const int qj = q0 + qg * J + j;
+            if (qj < T && t <= pos0 + qj) ep[(qg * J + j) * kPqPitch + t] = sc[j] / rs;
+        }
+    }
+    __syncthreads();
+    // softmax (k_attn_softmax_b): max, exp, serial sum, divide
+    constexpr int KMAX = kPqMaxKeys / TPQ;
     float sv[KMAX];
 #pragma unroll
-    for (int k = 0; k < KMAX; k++) sv[k] = row[min(quad + TPQ * k, max(n - 1, 0))];
+    for (int k = 0; k < KMAX; k++) sv[k] = e[min(quad + TPQ * k, max(n - 1, 0))];
     float m = -INFINITY;
 #pragma unroll
     for (int k = 0; k < KMAX; k++)
@@ -885,13 +977,17 @@ __global__ __launch_bounds__(kPqQueries * HS / 4) void k_attn_pvq_b(
     __syncthreads();
     const float sum = red[ql];
     for (int t = quad; t < n; t += TPQ) e[t] = e[t] / sum;
+    // p*V (k_attn_pv_b's order)
+    float4* vt = reinterpret_cast<float4*>(kvs);   // [kPqKeys][TPQ]
     float4 acc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
     for (int c = 0; c < nchunks; c++) {
         __syncthreads();   // the previous chunk's reads are done (and, first, the p rows written)
-        vt[tid / TPQ][tid % TPQ] = rv0;
-        vt[(tid + NT) / TPQ][(tid + NT) % TPQ] = rv1;
+        vt[tid] = vr0;
+        vt[tid + NT] = vr1;
+        vt[tid + 2 * NT] = vr2;
+        vt[tid + 3 * NT] = vr3;
         __syncthreads();
-        if (c + 1 < nchunks) fetch(c + 1);
+        if (c + 1 < nchunks) vfetch(c + 1);
         const int tn = min(kPqKeys, n - c * kPqKeys);
         const float* pr = e + c * kPqKeys;
         int t = 0;
@@ -901,7 +997,7 @@ __global__ __launch_bounds__(kPqQueries * HS / 4) void k_attn_pvq_b(
 #pragma unroll
             for (int k = 0; k < 8; k++) {
                 pv[k] = pr[t + k];
-                v[k] = vt[t + k][quad];
+                v[k] = vt[(t + k) * TPQ + quad];
             }
 #pragma unroll
             for (int k = 0; k < 8; k++) {
@@ -913,7 +1009,7 @@ __global__ __launch_bounds__(kPqQueries * HS / 4) void k_attn_pvq_b(
         }
         for (; t < tn; t++) {
             const float pv = pr[t];
-            const float4 v = vt[t][quad];
+            const float4 v = vt[t * TPQ + quad];
             acc.x = __builtin_fmaf(pv, v.x, acc.x);
             acc.y = __builtin_fmaf(pv, v.y, acc.y);
             acc.z = __builtin_fmaf(pv, v.z, acc.z);

@@ -107,11 +107,11 @@ int launch_pf_prep(int bits, int group, const int8_t* xq, const float* xs, int K
 // rope (optional): the qkv form, q rotated to out, k and v appended to the caches (PfRope).
 int launch_pf_gemm(int bits, int group, const void* w, const float* ws, int rows, int cols, const int8_t* xqp,
                    const PfRecord* rec, int T, float* out, int ldo, hipStream_t st, const PfRope* rope = nullptr);
-// The prefill's attention of T > 1 queries (exact order): scores, then the
-// softmax, p*V and (pf set) the Q8 operand of the wo GEMM in one kernel
-// where the shape allows it (head size 64 / 128, groups inside a head, a
-// context of at most 256 positions), else the three-kernel batched path and
-// the quantize.  out [T][dim] is written only without pf.
+// The prefill's attention of T > 1 queries (exact order): scores, softmax,
+// p*V and (pf set) the Q8 operand of the wo GEMM in one kernel where the
+// shape allows it (head size 64 / 128, groups inside a head, a context of at
+// most 256 positions), else the three-kernel batched path and the quantize.
+// out [T][dim] is written only without pf.
 int launch_attention_prefill(const float* q, const float* kcache, const float* vcache, float* out, float* scores,
                              int pos, int n_heads, int n_kv_heads, int hs, int max_t, hipStream_t st, int T,
                              int q_stride, int k_il, int group, const PfOperand* pf);

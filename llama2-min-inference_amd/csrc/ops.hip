@@ -453,13 +453,11 @@ int launch_attention_prefill(const float* q, const float* kcache, const float* v
         return L2Q_ERR_ARG;
     }
     const int kv_mul = n_heads / n_kv_heads;
-    int rc = launch_attention_scores_b(q, kcache, scores, pos, T, kv_mul, n_heads, hs, max_t, q_stride, k_il, st);
-    if (rc) return rc;
     const PfOperand po = pf ? *pf : PfOperand{nullptr, nullptr, 8, 1, 1};
     const dim3 grid((unsigned)n_heads, (unsigned)((T + kPqQueries - 1) / kPqQueries));
-#define L2Q_PQ(HS_, G_)                                                                                              \
-    hipLaunchKernelGGL((k_attn_pvq_b<HS_, G_>), grid, dim3(kPqQueries * HS_ / 4), 0, st, scores, vcache, out, pos, T, \
-                       kv_mul, n_heads, max_t, po)
+#define L2Q_PQ(HS_, G_)                                                                                         \
+    hipLaunchKernelGGL((k_attn_pf_b<HS_, G_>), grid, dim3(kPqQueries * HS_ / 4), 0, st, q, q_stride, kcache, k_il, \
+                       vcache, out, pos, T, kv_mul, n_heads, max_t, po)
     if (hs == 128) {
         if (group == 64) L2Q_PQ(128, 64);
         else L2Q_PQ(128, 32);
@@ -468,7 +466,7 @@ int launch_attention_prefill(const float* q, const float* kcache, const float* v
         else L2Q_PQ(64, 32);
     }
 #undef L2Q_PQ
-    return check_launch("attention_pvq_b");
+    return check_launch("attention_pf_b");
 }
 
 bool kv8_shape_ok(int n_heads, int n_kv_heads, int hs, int max_t) {
