@@ -93,9 +93,9 @@ struct l2q_engine {
     // batched prefill (allocated at the first l2q_engine_prefill): T tokens per chunk
     char* pfarena = nullptr;
     int pf_T = 0;
-    float *pf_xa, *pf_xb, *pf_qkv, *pf_att, *pf_wo, *pf_h13, *pf_ffn, *pf_scores;
-    int8_t* pf_xqp;
-    l2q::PfRecord* pf_rec;
+    float *pf_xa, *pf_xb, *pf_qkv, *pf_att, *pf_wo, *pf_ffn, *pf_scores;
+    int8_t *pf_xqp, *pf_xqh;           // GEMM operands: d-wide, and w2's h-wide one (written by w1|w3)
+    l2q::PfRecord *pf_rec, *pf_rech;
     int* pf_tok;
 };
 
@@ -561,16 +561,18 @@ int prefill_alloc(l2q_engine* e) {
     const size_t kmax = d > h ? d : h, nbmax = kmax / e->G;
     Arena a;
     const size_t o_xa = a.take(T * d * 4), o_xb = a.take(T * d * 4), o_qkv = a.take(T * qkv * 4);
-    const size_t o_att = a.take(T * d * 4), o_wo = a.take(T * d * 4), o_h13 = a.take(T * 2 * h * 4);
+    const size_t o_att = a.take(T * d * 4), o_wo = a.take(T * d * 4);
     const size_t o_ffn = a.take(T * d * 4), o_sc = a.take(T * c.n_heads * (size_t)attn_b_pitch(e->max_t) * 4);
     const size_t o_xqp = a.take(T * kmax), o_rec = a.take(T * nbmax * sizeof(PfRecord));
+    const size_t o_xqh = a.take(T * h), o_rech = a.take(T * (h / e->G) * sizeof(PfRecord));
     const size_t o_tok = a.take(T * 4);
     HIPCHK(hipMalloc(&e->pfarena, align_up(a.used, 256)), "hipMalloc(prefill)");
     char* P = e->pfarena;
     e->pf_xa = (float*)(P + o_xa); e->pf_xb = (float*)(P + o_xb); e->pf_qkv = (float*)(P + o_qkv);
-    e->pf_att = (float*)(P + o_att); e->pf_wo = (float*)(P + o_wo); e->pf_h13 = (float*)(P + o_h13);
+    e->pf_att = (float*)(P + o_att); e->pf_wo = (float*)(P + o_wo);
     e->pf_ffn = (float*)(P + o_ffn); e->pf_scores = (float*)(P + o_sc);
     e->pf_xqp = (int8_t*)(P + o_xqp); e->pf_rec = (PfRecord*)(P + o_rec);
+    e->pf_xqh = (int8_t*)(P + o_xqh); e->pf_rech = (PfRecord*)(P + o_rech);
     e->pf_tok = (int*)(P + o_tok);
     e->pf_T = (int)T;
     return L2Q_OK;
@@ -589,9 +591,10 @@ int prefill_chunk(l2q_engine* e, const int* tokens, int T, int pos0, bool want_l
     HIPCHK(hipMemcpyAsync(e->pf_tok, tokens, T * sizeof(int), hipMemcpyHostToDevice, st), "upload tokens");
     if ((rc = launch_pf_embed(e->emb, e->pf_tok, e->pf_xa, d, T, st))) return rc;
     // every quantizing producer writes the GEMM operand (permuted q, records) itself
-    const PfOperand pod{e->pf_xqp, e->pf_rec, bits, d, T}, poh{e->pf_xqp, e->pf_rec, bits, h, T};
-    auto gemm = [&](const uint8_t* w, const float* ws, int rows, int cols, float* out, const PfRope* rp = nullptr) {
-        return launch_pf_gemm(bits, G, w, ws, rows, cols, e->pf_xqp, e->pf_rec, T, out, rows, st, rp);
+    const PfOperand pod{e->pf_xqp, e->pf_rec, bits, d, T}, poh{e->pf_xqh, e->pf_rech, bits, h, T};
+    auto gemm = [&](const uint8_t* w, const float* ws, int rows, const PfOperand& in, float* out,
+                    const PfRope* rp = nullptr, const PfOperand* sw = nullptr) {
+        return launch_pf_gemm(bits, G, w, ws, rows, in.K, in.xqp, in.rec, T, out, rows, st, rp, sw);
     };
     for (int l = 0; l < c.n_layers; l++) {
         float* kc = e->kcache + (size_t)l * kv * e->max_t;
@@ -603,23 +606,23 @@ int prefill_chunk(l2q_engine* e, const int* tokens, int T, int pos0, bool want_l
         // q, k, v rows with RoPE and the KV append fused into the GEMM's stores
         const PfRope rp{e->rope, kc, vc, pos0, d, kv, e->hs, e->max_t, 1};
         if ((rc = gemm(e->qkv_w + (size_t)l * qkv_rows * e->rowb_d, e->qkv_s + (size_t)l * qkv_rows * nbd, qkv_rows,
-                       d, e->pf_qkv, &rp)))
+                       pod, e->pf_qkv, &rp)))
             return rc;
         // attention, its output quantized into the wo operand
         if ((rc = launch_attention_prefill(e->pf_qkv, kc, vc, e->pf_att, e->pf_scores, pos0, c.n_heads, c.n_kv_heads,
                                            e->hs, e->max_t, st, T, qkv_rows, 1, G, &pod)))
             return rc;
         // wo
-        if ((rc = gemm(e->wo_w + (size_t)l * d * e->rowb_d, e->wo_s + (size_t)l * d * nbd, d, d, e->pf_wo))) return rc;
+        if ((rc = gemm(e->wo_w + (size_t)l * d * e->rowb_d, e->wo_s + (size_t)l * d * nbd, d, pod, e->pf_wo))) return rc;
         // x = xb + wo -> xa; RMSNorm; SwiGLU(w1 x, w3 x); w2
         if ((rc = launch_rmsnorm_quant(e->pf_xb, nullptr, nullptr, e->pf_wo, e->pf_xa, e->rms_ffn + (size_t)l * d, d,
                                        G, nullptr, nullptr, st, T, &pod)))
             return rc;
-        if ((rc = gemm(e->w13_w + (size_t)l * 2 * h * e->rowb_d, e->w13_s + (size_t)l * 2 * h * nbd, 2 * h, d,
-                       e->pf_h13)))
+        // w1|w3 with SwiGLU + Q8 in its stores: w2's operand, no h13 in HBM
+        if ((rc = gemm(e->w13_w + (size_t)l * 2 * h * e->rowb_d, e->w13_s + (size_t)l * 2 * h * nbd, 2 * h, pod,
+                       nullptr, nullptr, &poh)))
             return rc;
-        if ((rc = launch_pf_swiglu_quant(e->pf_h13, h, T, G, nullptr, nullptr, st, &poh))) return rc;
-        if ((rc = gemm(e->w2_w + (size_t)l * d * e->rowb_h, e->w2_s + (size_t)l * d * nbh, d, h, e->pf_ffn))) return rc;
+        if ((rc = gemm(e->w2_w + (size_t)l * d * e->rowb_h, e->w2_s + (size_t)l * d * nbh, d, poh, e->pf_ffn))) return rc;
     }
     if (!want_logits) return L2Q_OK;
     // the last position: final RMSNorm of xa + ffn, classifier

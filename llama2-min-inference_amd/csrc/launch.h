@@ -105,8 +105,10 @@ constexpr int kPfMaxTokens = 128;    // tokens per prefill chunk
 int launch_pf_prep(int bits, int group, const int8_t* xq, const float* xs, int K, int T, int8_t* xqp, PfRecord* rec,
                    hipStream_t st);
 // rope (optional): the qkv form, q rotated to out, k and v appended to the caches (PfRope).
+// swiglu (optional): the w1|w3 form, SwiGLU + Q8 straight into the w2 operand (out unused).
 int launch_pf_gemm(int bits, int group, const void* w, const float* ws, int rows, int cols, const int8_t* xqp,
-                   const PfRecord* rec, int T, float* out, int ldo, hipStream_t st, const PfRope* rope = nullptr);
+                   const PfRecord* rec, int T, float* out, int ldo, hipStream_t st, const PfRope* rope = nullptr,
+                   const PfOperand* swiglu = nullptr);
 // The prefill's attention of T > 1 queries (exact order): scores, softmax,
 // p*V and (pf set) the Q8 operand of the wo GEMM in one kernel where the
 // shape allows it (head size 64 / 128, groups inside a head, a context of at
@@ -116,8 +118,6 @@ int launch_attention_prefill(const float* q, const float* kcache, const float* v
                              int pos, int n_heads, int n_kv_heads, int hs, int max_t, hipStream_t st, int T,
                              int q_stride, int k_il, int group, const PfOperand* pf);
 int launch_pf_embed(const float* emb, const int* tokens, float* x, int dim, int T, hipStream_t st);
-int launch_pf_swiglu_quant(const float* h13, int n, int T, int group, int8_t* xq, float* xs, hipStream_t st,
-                           const PfOperand* pf = nullptr);
 
 int launch_argmax(const float* v, int n, int* out, hipStream_t st);
 

@@ -549,11 +549,24 @@ namespace {
 // 16x16 tiles, SC columns per step.
 template <int B_, int G_, int RTW, int TPW, int WR, int WT, int SC, int NST, bool PIPE, int EPI>
 void pf3_launch(const uint8_t* w, const float* ws, int rows, int cols, const int8_t* xqp, const PfRecord* rec, int T,
-                float* out, int ldo, const PfRope& rp, hipStream_t st) {
+                float* out, int ldo, const PfRope& rp, hipStream_t st, const PfOperand& so = PfOperand{}) {
     using P = Pf3<B_, G_, RTW, TPW, WR, WT, SC>;
     const dim3 grid((unsigned)((rows + P::RT - 1) / P::RT), (unsigned)((T + P::TT - 1) / P::TT));
     hipLaunchKernelGGL((k_pf_gemm3<B_, G_, RTW, TPW, WR, WT, SC, NST, PIPE, EPI>), grid, dim3(P::NT), 0, st, w, ws,
-                       rows, cols, xqp, rec, T, out, ldo, rp);
+                       rows, cols, xqp, rec, T, out, ldo, rp, so);
+}
+
+// The w1|w3 GEMM with the SwiGLU + Q8 stores (EPI 2): 2G-row workgroups,
+// one quantization group of the hidden vector each (8 waves: 4 x 2 of 32 x 16
+// for G64, 2 x 4 for G32; the 128-row tile measures as fast as the 64-row
+// one on w1|w3).
+template <int B_, int G_>
+void pf3_swiglu(const uint8_t* w, const float* ws, int rows, int cols, const int8_t* xqp, const PfRecord* rec, int T,
+                const PfOperand& so, hipStream_t st) {
+    if constexpr (G_ == 64)
+        pf3_launch<B_, G_, 2, 1, 4, 2, 2 * G_, 3, false, 2>(w, ws, rows, cols, xqp, rec, T, nullptr, rows, PfRope{}, st, so);
+    else
+        pf3_launch<B_, G_, 2, 1, 2, 4, 2 * G_, 3, false, 2>(w, ws, rows, cols, xqp, rec, T, nullptr, rows, PfRope{}, st, so);
 }
 
 // The two workgroup shapes of the batched GEMM (16x16 MFMA tiles; SC =
@@ -591,7 +604,8 @@ void pf3_bits(int bits, int group, PfShape shp, const uint8_t* w, const float* w
 }  // namespace
 
 int launch_pf_gemm(int bits, int group, const void* w, const float* ws, int rows, int cols, const int8_t* xqp,
-                   const PfRecord* rec, int T, float* out, int ldo, hipStream_t st, const PfRope* rope) {
+                   const PfRecord* rec, int T, float* out, int ldo, hipStream_t st, const PfRope* rope,
+                   const PfOperand* swiglu) {
     if (T < 1 || rows < 1 || cols <= 0 || (group != 32 && group != 64) || cols % group || (bits != 4 && bits != 8) ||
         cols % 32 || ldo < rows) {
         set_error("prefill gemm: bad rows=%d cols=%d T=%d group=%d bits=%d", rows, cols, T, group, bits);
@@ -610,6 +624,19 @@ int launch_pf_gemm(int bits, int group, const void* w, const float* ws, int rows
     const long long wg_wide = (long long)((rows + 63) / 64) * ((T + 63) / 64);
     const PfShape shp = wg_wide >= ncu ? kPfWide : kPfSmall;
     const uint8_t* wb = static_cast<const uint8_t*>(w);
+    if (swiglu) {
+        const PfOperand& so = *swiglu;
+        if (rope || !so.xqp || !so.rec || reinterpret_cast<uintptr_t>(so.rec) % 16 || (so.bits != 4 && so.bits != 8) ||
+            rows % (2 * group) || so.K != rows / 2 || so.T != T) {
+            set_error("prefill gemm: bad SwiGLU operand (rows=%d K=%d T=%d)", rows, so.K, so.T);
+            return L2Q_ERR_ARG;
+        }
+        if (bits == 4 && group == 64) pf3_swiglu<4, 64>(wb, ws, rows, cols, xqp, rec, T, so, st);
+        if (bits == 4 && group == 32) pf3_swiglu<4, 32>(wb, ws, rows, cols, xqp, rec, T, so, st);
+        if (bits == 8 && group == 64) pf3_swiglu<8, 64>(wb, ws, rows, cols, xqp, rec, T, so, st);
+        if (bits == 8 && group == 32) pf3_swiglu<8, 32>(wb, ws, rows, cols, xqp, rec, T, so, st);
+        return check_launch("prefill_gemm_swiglu");
+    }
     if (rope) {
         const PfRope& r = *rope;
         if (!r.rope || !r.kcache || !r.vcache || r.hs <= 0 || r.hs % 2 || r.dim % r.hs || r.kv_dim % r.hs ||
@@ -630,19 +657,6 @@ int launch_pf_embed(const float* emb, const int* tokens, float* x, int dim, int 
     return check_launch("prefill_embed");
 }
 
-int launch_pf_swiglu_quant(const float* h13, int n, int T, int group, int8_t* xq, float* xs, hipStream_t st,
-                           const PfOperand* pf) {
-    if (n <= 0 || n % group || (group != 32 && group != 64) || T < 1 || T > 65535) {
-        set_error("prefill swiglu: bad n=%d T=%d", n, T);
-        return L2Q_ERR_ARG;
-    }
-    PfOperand po;
-    if (int rc = pf_operand(pf, xq, xs, n, T, &po, "prefill swiglu")) return rc;
-    const dim3 grid((unsigned)((n + 255) / 256), (unsigned)T);   // groups never straddle a 256-element block
-    if (group == 32) hipLaunchKernelGGL(k_pf_swiglu_quant<32>, grid, dim3(256), 0, st, h13, n, T, xq, xs, po);
-    else hipLaunchKernelGGL(k_pf_swiglu_quant<64>, grid, dim3(256), 0, st, h13, n, T, xq, xs, po);
-    return check_launch("prefill_swiglu_quant");
-}
 
 int launch_argmax(const float* v, int n, int* out, hipStream_t st) {
     if (n <= 0 || !v || !out || reinterpret_cast<uintptr_t>(v) % 16) {

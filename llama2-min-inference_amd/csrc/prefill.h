@@ -136,7 +136,7 @@ template <int BITS, int G, int RTW, int TPW, int WR, int WT, int SC, int NST, bo
 __global__ __launch_bounds__(WR * WT * L2Q_WAVE) void k_pf_gemm3(
     const uint8_t* __restrict__ w, const float* __restrict__ ws, int rows, int cols,
     const int8_t* __restrict__ xqp, const PfRecord* __restrict__ rec, int T, float* __restrict__ out, int ldo,
-    PfRope rp) {
+    PfRope rp, PfOperand so) {
     using P = Pf3<BITS, G, RTW, TPW, WR, WT, SC>;
     constexpr int KS = P::KS;
     static_assert(NST >= 3 && NST <= 5, "pipeline depth");
@@ -395,6 +395,75 @@ __global__ __launch_bounds__(WR * WT * L2Q_WAVE) void k_pf_gemm3(
             }
     }
     if (PIPE && nj > 0) fold((nsteps - 1) % 2 == 0 ? pa : pb);
+    if constexpr (EPI == 2) {
+        // SwiGLU + Q8 into the w2 GEMM's operand (so): rows alternate w1 / w3
+        // of a hidden unit, the workgroup's RT = 2G rows are one quantization
+        // group of G units; g = (h1 * (1/(1+expf(-h1)))) * h3 (runq.c:
+        // 405-410, the operations of k_swiglu_quant), its group's max over
+        // the lanes of the token (xor 16 / 32) and the WR row-waves (LDS),
+        // Q8 as k_swiglu_quant quantizes (runq.c:117-139)
+        static_assert(TPW == 1 && P::RT == 2 * G, "one token tile per wave, one group per workgroup");
+        const int t = t0 + tw0 + l16;
+        const bool tin = nj > 0 && t < T;
+        float gv[RTW][2];
+        float amax = 0.0f;
+#pragma unroll
+        for (int i = 0; i < RTW; i++)
+#pragma unroll
+            for (int m = 0; m < 2; m++) {
+                float h = acc[0][i][2 * m];
+                h *= (1.0f / (1.0f + exp_runq(-h)));
+                gv[i][m] = tin ? h * acc[0][i][2 * m + 1] : 0.0f;
+                amax = fmaxf(amax, fabsf(gv[i][m]));
+            }
+        unsigned ua, ub;
+        xor16_pair(__float_as_uint(amax), ua, ub);
+        amax = fmaxf(__uint_as_float(ua), __uint_as_float(ub));
+        xor32_pair(__float_as_uint(amax), ua, ub);
+        amax = fmaxf(__uint_as_float(ua), __uint_as_float(ub));
+        const int wr = wv % WR, wt = wv / WR;
+        float* xm = reinterpret_cast<float*>(sb0);      // [WT][WR][16] row-wave maxima
+        int* xq = reinterpret_cast<int*>(xm + WT * WR * 16);   // [WT][WR][16] row-wave sums
+        barrier();   // every wave is past its last LDS read of the stages
+        if (c == 0) xm[(wt * WR + wr) * 16 + l16] = amax;
+        barrier();
+        float gm = 0.0f;
+#pragma unroll
+        for (int k = 0; k < WR; k++) gm = fmaxf(gm, xm[(wt * WR + k) * 16 + l16]);
+        const float s = q8_scale(gm);
+        const float r = q8_recip(s);
+        int qv[RTW][2];
+        int qs = 0;
+#pragma unroll
+        for (int i = 0; i < RTW; i++)
+#pragma unroll
+            for (int m = 0; m < 2; m++) {
+                qv[i][m] = q8_value_fast(gv[i][m], s, r);
+                qs += qv[i][m];
+            }
+        xor16_pair((unsigned)qs, ua, ub);
+        qs = (int)(ua + ub);
+        xor32_pair((unsigned)qs, ua, ub);
+        qs = (int)(ua + ub);
+        if (c == 0) xq[(wt * WR + wr) * 16 + l16] = qs;
+        barrier();
+        if (!tin) return;
+        int total = 0;
+#pragma unroll
+        for (int k = 0; k < WR; k++) total += xq[(wt * WR + k) * 16 + l16];
+        constexpr int CH = G / 4;
+        int8_t* dst = so.xqp + (size_t)t * so.K + r0 / 2;   // the group's G bytes of token t
+#pragma unroll
+        for (int i = 0; i < RTW; i++)
+#pragma unroll
+            for (int m = 0; m < 2; m++) {
+                const int j = 16 * RTW * wr / 2 + 8 * i + 2 * c + m;   // unit of the group
+                const int jj = j % CH;
+                dst[so.bits == 4 ? j - jj + ((jj & 1) ? jj / 2 : CH / 2 + jj / 2) : j] = (int8_t)qv[i][m];
+            }
+        if (wr == 0 && c == 0) so.rec[(size_t)(r0 / P::RT) * T + t] = pf_record(s, total, so.bits);
+        return;
+    }
     // out[t][r]: rows 16i + 4c + e of the wave's tile i, token 16j + l16
 #pragma unroll
     for (int j = 0; j < TPW; j++) {
@@ -453,33 +522,6 @@ __global__ void k_pf_embed(const float* __restrict__ emb, const int* __restrict_
     const int t = blockIdx.y;
     const int i = blockIdx.x * blockDim.x + threadIdx.x;
     if (i < dim) x[(size_t)t * dim + i] = emb[(size_t)tokens[t] * dim + i];
-}
-
-// SwiGLU + Q8 quantize of T tokens from interleaved (w1, w3) rows:
-// h13 [T][2n] -> xq [T][n], xs [T][n/G], as k_swiglu_quant per token
-// (pf.xqp set: also the GEMM operand, pf_emit; xq may then be null).
-template <int G>
-__global__ __launch_bounds__(256) void k_pf_swiglu_quant(const float* __restrict__ h13, int n, int T,
-                                                         int8_t* __restrict__ xq, float* __restrict__ xs,
-                                                         PfOperand pf) {
-    // workgroup (x, token): elements j of one token, no division
-    const int t = blockIdx.y, j = blockIdx.x * blockDim.x + threadIdx.x;
-    const bool in = j < n;
-    const size_t i = (size_t)t * n + j;   // element of the flattened [T][n]
-    float g = 0.0f;
-    if (in) {
-        const float2 hh = reinterpret_cast<const float2*>(h13 + (size_t)t * 2 * n)[j];   // (w1, w3) of unit j
-        float h = hh.x;   // (built with -ffp-contract=off, as k_swiglu_quant)
-        h *= (1.0f / (1.0f + exp_runq(-h)));
-        g = h * hh.y;
-    }
-    const float s = q8_scale(group_max<G>(fabsf(g)));
-    const int q = q8_value_fast(g, s, q8_recip(s));
-    if (pf.xqp) pf_emit<G>(pf, t, j, q, s, in);
-    if (in) {
-        if (xq) xq[i] = (int8_t)q;
-        if (xs && (i % G) == 0) xs[i / G] = s;
-    }
 }
 
 }  // namespace l2q
