@@ -242,6 +242,17 @@ int launch_rmsnorm_quant(const float* x, const float* emb, const int* meta, cons
     }
     PfOperand po;
     if (int rc = pf_operand(pf, xq, xs, n, T, &po, "rmsnorm_quant")) return rc;
+    if (pf && !emb && !xq && !xs && n % 4 == 0 && n <= kPfNormThreads * kPfNormMaxChunks * 4 &&
+        reinterpret_cast<uintptr_t>(x) % 16 == 0 && reinterpret_cast<uintptr_t>(resid) % 16 == 0 &&
+        reinterpret_cast<uintptr_t>(xout) % 16 == 0 && reinterpret_cast<uintptr_t>(w) % 16 == 0) {
+        // the GEMM operand alone (prefill): float4 chunks, each token on kPfNormSplit workgroups
+        const dim3 grid(kPfNormSplit, (unsigned)T);
+        if (group == 32)
+            hipLaunchKernelGGL(k_pf_rmsnorm_quant<32>, grid, dim3(kPfNormThreads), 0, st, x, resid, xout, w, n, po);
+        else
+            hipLaunchKernelGGL(k_pf_rmsnorm_quant<64>, grid, dim3(kPfNormThreads), 0, st, x, resid, xout, w, n, po);
+        return check_launch("prefill_rmsnorm_quant");
+    }
     if (group == 32)
         hipLaunchKernelGGL(k_rmsnorm_quant<32>, dim3(T), dim3(kNormThreads), 0, st, x, emb, meta, resid, xout, w, n, xq, xs, po);
     else

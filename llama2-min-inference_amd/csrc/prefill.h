@@ -424,9 +424,11 @@ __global__ __launch_bounds__(WR * WT * L2Q_WAVE) void k_pf_gemm3(
         const int wr = wv % WR, wt = wv / WR;
         float* xm = reinterpret_cast<float*>(sb0);      // [WT][WR][16] row-wave maxima
         int* xq = reinterpret_cast<int*>(xm + WT * WR * 16);   // [WT][WR][16] row-wave sums
-        barrier();   // every wave is past its last LDS read of the stages
+        // __syncthreads, not the loop's bare s_barrier: these LDS stores must
+        // land (lgkmcnt(0)) before other waves read them
+        __syncthreads();   // every wave is past its last LDS read of the stages
         if (c == 0) xm[(wt * WR + wr) * 16 + l16] = amax;
-        barrier();
+        __syncthreads();
         float gm = 0.0f;
 #pragma unroll
         for (int k = 0; k < WR; k++) gm = fmaxf(gm, xm[(wt * WR + k) * 16 + l16]);
@@ -446,7 +448,7 @@ __global__ __launch_bounds__(WR * WT * L2Q_WAVE) void k_pf_gemm3(
         xor32_pair((unsigned)qs, ua, ub);
         qs = (int)(ua + ub);
         if (c == 0) xq[(wt * WR + wr) * 16 + l16] = qs;
-        barrier();
+        __syncthreads();
         if (!tin) return;
         int total = 0;
 #pragma unroll
@@ -512,6 +514,100 @@ __global__ __launch_bounds__(WR * WT * L2Q_WAVE) void k_pf_gemm3(
                 for (int e = 0; e < 4; e++)
                     if (r + e < rows) o[e] = acc[j][i][e];
             }
+        }
+    }
+}
+
+// Residual add + RMSNorm + Q8 of T vectors into the GEMM operand
+// (runq.c:294-305 then :117-139), with the operations of the decode GEMV's
+// kNorm prologue (prologue_compute): v = x + resid, the sum of squares in
+// the reference's order (runq_sumsq_t over a transposed LDS copy), inv =
+// 1/sqrtf(ss/n + 1e-5), o = w * (inv * v), group maxima of |o| on the bit
+// patterns, q8 values.  Workgroup (split s, token t) of 256 threads, thread
+// i holding float4 chunks c = i + 256k: every split forms the token's whole
+// sum of squares (the chain is latency, not work), and quantizes, stores
+// and emits the chunks with k % kPfNormSplit == s, so a token's
+// quantization is spread over kPfNormSplit CUs.  A group is G/4
+// consecutive lanes.  xout receives v.
+constexpr int kPfNormThreads = 256, kPfNormSplit = 2, kPfNormMaxChunks = 8;   // n <= 8192
+template <int G>
+__global__ __launch_bounds__(kPfNormThreads) void k_pf_rmsnorm_quant(
+    const float* __restrict__ x, const float* __restrict__ resid, float* __restrict__ xout,
+    const float* __restrict__ w, int n, PfOperand pf) {
+#pragma clang fp contract(off)
+    __shared__ __attribute__((aligned(16))) float vt[16 * sumsq_stride(kPfNormThreads * kPfNormMaxChunks * 4)];
+    __shared__ float inv_s;
+    const int tid = threadIdx.x, sp = blockIdx.x, t = blockIdx.y;
+    const int nc = n / 4, st = sumsq_stride(n);
+    const size_t to = (size_t)t * n;
+    const float4* x4 = reinterpret_cast<const float4*>(x + to);
+    const float4* r4 = resid ? reinterpret_cast<const float4*>(resid + to) : nullptr;
+    const float4* w4 = reinterpret_cast<const float4*>(w);
+    float4 v[kPfNormMaxChunks], rv[kPfNormMaxChunks], wv[kPfNormMaxChunks];
+    // every load first: one round trip
+#pragma unroll
+    for (int k = 0; k < kPfNormMaxChunks; k++) {
+        const int c = tid + kPfNormThreads * k;
+        if (c < nc) {
+            v[k] = x4[c];
+            if (resid) rv[k] = r4[c];
+            if (k % kPfNormSplit == sp) wv[k] = w4[c];
+        }
+    }
+#pragma unroll
+    for (int k = 0; k < kPfNormMaxChunks; k++) {
+        const int c = tid + kPfNormThreads * k;
+        if (c < nc) {
+            if (resid) { v[k].x += rv[k].x; v[k].y += rv[k].y; v[k].z += rv[k].z; v[k].w += rv[k].w; }
+            const int e = 4 * c;   // elements e..e+3: accumulators e%16.., step e/16
+            vt[((e + 0) & 15) * st + (e >> 4)] = v[k].x;
+            vt[((e + 1) & 15) * st + (e >> 4)] = v[k].y;
+            vt[((e + 2) & 15) * st + (e >> 4)] = v[k].z;
+            vt[((e + 3) & 15) * st + (e >> 4)] = v[k].w;
+            if (xout && k % kPfNormSplit == sp) reinterpret_cast<float4*>(xout + to)[c] = v[k];
+        }
+    }
+    __syncthreads();
+    if (tid < L2Q_WAVE) {
+        const float ss = runq_sumsq_t(vt, n, st, tid);
+        if (tid == 0) inv_s = 1.0f / sqrtf(ss / (float)n + 1e-5f);
+    }
+    __syncthreads();
+    const float inv = inv_s;
+    constexpr int CH = G / 4;   // the INT4 operand's permutation unit (pf_emit)
+#pragma unroll
+    for (int k = 0; k < kPfNormMaxChunks; k++) {
+        if (kPfNormThreads * k >= nc) break;   // uniform across the workgroup
+        if (k % kPfNormSplit != sp) continue;
+        const int c = tid + kPfNormThreads * k;
+        const bool in = c < nc;
+        float4 o = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        if (in) {
+            o.x = wv[k].x * (inv * v[k].x); o.y = wv[k].y * (inv * v[k].y);
+            o.z = wv[k].z * (inv * v[k].z); o.w = wv[k].w * (inv * v[k].w);
+        }
+        unsigned mb = max(max(__float_as_uint(o.x) & 0x7fffffffu, __float_as_uint(o.y) & 0x7fffffffu),
+                          max(__float_as_uint(o.z) & 0x7fffffffu, __float_as_uint(o.w) & 0x7fffffffu));
+        mb = group_umax<G / 4>(mb);
+        const float sc = q8_scale(__uint_as_float(mb));
+        const float r = q8_recip(sc);
+        const int q0 = q8_value_fast(o.x, sc, r), q1 = q8_value_fast(o.y, sc, r);
+        const int q2 = q8_value_fast(o.z, sc, r), q3 = q8_value_fast(o.w, sc, r);
+        const int sum = group_isum<G / 4>(in ? q0 + q1 + q2 + q3 : 0);   // exact in any order
+        if (in) {
+            const int e = 4 * c;
+            int8_t* row = pf.xqp + (size_t)t * pf.K;
+            auto b2 = [](int a, int b) __attribute__((always_inline)) {
+                return (uint16_t)((a & 0xff) | ((b & 0xff) << 8));
+            };
+            if (pf.bits == 4) {   // chunk of CH: odd elements first, then even (pf_emit's order)
+                const int cb = e - e % CH, m = (e % CH) / 4;
+                *reinterpret_cast<uint16_t*>(row + cb + 2 * m) = b2(q1, q3);
+                *reinterpret_cast<uint16_t*>(row + cb + CH / 2 + 2 * m) = b2(q0, q2);
+            } else {
+                *reinterpret_cast<unsigned*>(row + e) = (unsigned)b2(q0, q1) | ((unsigned)b2(q2, q3) << 16);
+            }
+            if (c % (G / 4) == 0) pf.rec[(size_t)(e / G) * pf.T + t] = pf_record(sc, sum, pf.bits);
         }
     }
 }
