@@ -30,7 +30,7 @@ def dev(torch, a):
 @pytest.mark.parametrize("bits", [8, 4])
 @pytest.mark.parametrize("group", [32, 64])
 @pytest.mark.parametrize("rows,cols,T", [(288, 288, 1), (768, 288, 17), (4096, 4096, 128), (4096, 11008, 33),
-                                         (130, 4224, 20), (3, 64, 5), (32000, 4096, 16)])
+                                         (130, 4224, 20), (3, 64, 5), (32000, 4096, 16), (4128, 4096, 100)])
 def test_gemm_matches_oracle_per_token(gpu_lib, torch_cuda, bits, group, rows, cols, T):
     if cols % group:
         pytest.skip("group does not divide cols")
