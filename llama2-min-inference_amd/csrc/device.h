@@ -202,11 +202,13 @@ __device__ __forceinline__ float q8_bias_term(float s, int sumq) {
 // The batched-prefill GEMM operand of quantized activations [T][K]: xqp
 // holds q in the MFMA chunk order (INT4 weights: per chunk of G/4 columns,
 // the odd columns then the even ones; INT8: natural order) and rec [K/G][T]
-// one 32-byte record per (group, token), pf_record.  Producers that
+// one 16-byte record per (group, token), pf_record.  Producers that
 // quantize write it directly (xqp == nullptr: not wanted).
-struct PfRecord {
-    int4 c;     // the MFMA accumulator input, four copies
-    float4 s;   // xs, xt, 0, 0
+struct __attribute__((aligned(16))) PfRecord {
+    int c;       // the MFMA accumulator input (every row of the token's column)
+    float xs;    // the group's activation scale
+    float xt;    // its bias term
+    int pad;
 };
 
 struct PfOperand {
@@ -236,7 +238,7 @@ struct PfRope {
 // the dot.
 __device__ __forceinline__ PfRecord pf_record(float xs, int sumq, int bits) {
     const int c = sumq * (bits == 4 ? 2048 : 128);
-    return PfRecord{make_int4(c, c, c, c), make_float4(xs, q8_bias_term(xs, sumq), 0.0f, 0.0f)};
+    return PfRecord{c, xs, q8_bias_term(xs, sumq), 0};
 }
 
 // Emit element i of token t (i < K, K % G == 0) with value q and group scale

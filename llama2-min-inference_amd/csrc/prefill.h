@@ -85,7 +85,7 @@ __host__ __device__ constexpr int pf_swz(int units, int x) {
 // advance in steps of SC (KS groups).  A step's stage in LDS:
 //   A   [KS][RT][GB]   weight bytes of each row and group (GB = G*BITS/8)
 //   B   [KS][TT][G]    the tokens' permuted activations
-//   R   [KS][TT]       32-byte records (pf_record)
+//   R   [KS][TT]       16-byte records (pf_record)
 // with the 16-byte units of each row (token) and group permuted by pf_swz
 //   W   [KS][RT]       weight scales
 // each region filled by 64-lane DMA instructions (16-byte units; 4-byte
@@ -96,7 +96,7 @@ struct Pf3 {
     static constexpr int RT = 16 * RTW * WR, TT = 16 * TPW * WT;
     static constexpr int KS = SC / G;
     static constexpr int GB = G * BITS / 8;
-    static constexpr int AU = KS * RT * GB / 16, BU = KS * TT * G / 16, RU = 2 * KS * TT, WU = KS * RT;
+    static constexpr int AU = KS * RT * GB / 16, BU = KS * TT * G / 16, RU = KS * TT, WU = KS * RT;
     static constexpr int NA = (AU + 63) / 64, NB = (BU + 63) / 64, NR = (RU + 63) / 64, NWS = (WU + 63) / 64;
     static constexpr int N = NA + NB + NR + NWS;
     static constexpr int OB = NA * 1024, OR = OB + NB * 1024, OWS = OR + NR * 1024;
@@ -175,9 +175,8 @@ __global__ __launch_bounds__(WR * WT * L2Q_WAVE) void k_pf_gemm3(
         k -= P::NB;
         if (k < P::NR) {
             const int u = min(k * 64 + lane, P::RU - 1);
-            const int g = u / (2 * P::TT), t = (u / 2) % P::TT;
-            return reinterpret_cast<const uint8_t*>(rec + (size_t)min(s * KS + g, nb - 1) * T + min(t0 + t, T - 1)) +
-                   16 * ((u & 1) ^ pf_swz(2, t));
+            const int g = u / P::TT, t = u % P::TT;
+            return reinterpret_cast<const uint8_t*>(rec + (size_t)min(s * KS + g, nb - 1) * T + min(t0 + t, T - 1));
         }
         k -= P::NR;
         const int u = min(k * 64 + lane, P::WU - 1);
@@ -215,7 +214,7 @@ __global__ __launch_bounds__(WR * WT * L2Q_WAVE) void k_pf_gemm3(
                     if (full || lane < ng * (P::TT * G / 16) - 64 * kb) dma_lds<16>(a, buf + P::OB + kb * 1024);
                 } else if (k < P::NA + P::NB + P::NR) {
                     const int kr = k - P::NA - P::NB;
-                    if (full || lane < ng * (2 * P::TT) - 64 * kr) dma_lds<16>(a, buf + P::OR + kr * 1024);
+                    if (full || lane < ng * P::TT - 64 * kr) dma_lds<16>(a, buf + P::OR + kr * 1024);
                 } else {
                     const int kw = k - P::NA - P::NB - P::NR;
                     if (full || lane < ng * P::RT - 64 * kw) dma_lds<4>(a, buf + P::OWS + kw * 256);
@@ -230,7 +229,6 @@ __global__ __launch_bounds__(WR * WT * L2Q_WAVE) void k_pf_gemm3(
     // and tokens of a lane differ by multiples of 16, which leave the key)
     const int offa = 16 * ((c * CB / 16) ^ pf_swz(P::GB / 16, l16)) + c * CB % 16;
     const int offb = 16 * ((c * CX / 16) ^ pf_swz(G / 16, l16)) + c * CX % 16;
-    const int offr = 16 * pf_swz(2, l16);
     const int rw0 = (wv % WR) * 16 * RTW, tw0 = (wv / WR) * 16 * TPW;
     const int left = T - t0 - tw0;
     const int nj = left <= 0 ? 0 : min(TPW, (left + 15) / 16);   // token tiles with tokens (wave-uniform)
@@ -289,11 +287,10 @@ __global__ __launch_bounds__(WR * WT * L2Q_WAVE) void k_pf_gemm3(
                     const int2 v = *reinterpret_cast<const int2*>(pb);
                     o.bl[g][j] = (long)(unsigned)v.x | ((long)v.y << 32);
                 }
-                const uint8_t* pr = buf + P::OR + (g * P::TT + tl) * 32;
-                const int4 ci = *reinterpret_cast<const int4*>(pr + offr);
-                o.cin[g][j] = v4i32{ci.x, ci.y, ci.z, ci.w};
-                const float4 sv = *reinterpret_cast<const float4*>(pr + (16 ^ offr));
-                pn.sc[g][j] = make_float2(sv.x, sv.y);
+                // the record (c, xs, xt): c is the accumulator input of every row
+                const int4 ci = *reinterpret_cast<const int4*>(buf + P::OR + (g * P::TT + tl) * 16);
+                o.cin[g][j] = v4i32{ci.x, ci.x, ci.x, ci.x};
+                pn.sc[g][j] = make_float2(__int_as_float(ci.y), __int_as_float(ci.z));
             }
         }
     };
