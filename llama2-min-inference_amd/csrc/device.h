@@ -233,11 +233,10 @@ struct PfRope {
 
 // The record: xt = q8_bias_term(xs, sum(q)) (runq.c:137) and c =
 // 128*sum(q), the MFMA's accumulator input, so that D = d + 128*sum(q)
-// comes out of the MFMA.  INT4 weights enter the MFMA as 16x their value,
-// so there c is 16x as well and D >> 4 (exact: D is a multiple of 16) is
-// the dot.
+// comes out of the MFMA.  INT4 weights enter the MFMA in offset binary
+// (s4 + 8, see k_pf_gemm3), so there c = 120*sum(q) completes the same D.
 __device__ __forceinline__ PfRecord pf_record(float xs, int sumq, int bits) {
-    const int c = sumq * (bits == 4 ? 2048 : 128);
+    const int c = sumq * (bits == 4 ? 120 : 128);
     return PfRecord{c, xs, q8_bias_term(xs, sumq), 0};
 }
 

@@ -121,8 +121,8 @@ __device__ __forceinline__ void wait_stages(int wv) {
 // ws[r][b] * fma(xs[t][b], (float)(d + 128*sum(q)), -xt[t][b]), the decode
 // GEMV's fold (runq.c:150-156) for every (row, token), bit for bit.  Per
 // group: one MFMA per (row tile, token tile) with the record's accumulator
-// input, then 3 VALU operations per output (convert, two FMAs; INT4 adds
-// the shift).  Operands reach LDS by DMA, NST stages in rotation: stage
+// input, then 3 VALU operations per output (convert, two FMAs; INT4
+// weights enter in offset binary, so no shift).  Operands reach LDS by DMA, NST stages in rotation: stage
 // s + NST - 1 is requested while stage s is consumed, and one barrier per
 // step publishes stage s + 1.  The buffers are distinct LDS variables and
 // the loop is unrolled by NST, so the compiler sees which buffer every LDS
@@ -298,19 +298,20 @@ __global__ __launch_bounds__(WR * WT * L2Q_WAVE) void k_pf_gemm3(
 #pragma unroll
         for (int g = 0; g < KS; g++) {
             if (g < pn.ng) {
-                // INT4: 16x the odd / even nibbles in place (exact), matching the
-                // activations' [odd | even] order per chunk
+                // INT4: the odd / even nibbles as bytes in offset binary (n ^ 8 =
+                // s4(n) + 8, 0..15), matching the activations' [odd | even] order
+                // per chunk; the record's c adds the remaining 120*sum(q)
                 if constexpr (BITS == 4) {
+                    constexpr int kLo = 0x0F0F0F0F, kFlip = (int)0x88888888;
 #pragma unroll
                     for (int i = 0; i < RTW; i++) {
                         if constexpr (G == 64) {
-                            const int x = o.av[g][i][0], y = o.av[g][i][1];
-                            o.av[g][i] = v4i32{x & (int)0xF0F0F0F0, y & (int)0xF0F0F0F0, (x << 4) & (int)0xF0F0F0F0,
-                                               (y << 4) & (int)0xF0F0F0F0};
+                            const int x = o.av[g][i][0] ^ kFlip, y = o.av[g][i][1] ^ kFlip;
+                            o.av[g][i] = v4i32{(int)((unsigned)x >> 4) & kLo, (int)((unsigned)y >> 4) & kLo, x & kLo,
+                                               y & kLo};
                         } else {
-                            const int v = (int)o.al[g][i];
-                            o.al[g][i] = (long)(unsigned)(v & (int)0xF0F0F0F0) |
-                                         ((long)((v << 4) & (int)0xF0F0F0F0) << 32);
+                            const int v = (int)o.al[g][i] ^ kFlip;
+                            o.al[g][i] = (long)(unsigned)((int)((unsigned)v >> 4) & kLo) | ((long)(v & kLo) << 32);
                         }
                     }
                 }
@@ -343,7 +344,7 @@ __global__ __launch_bounds__(WR * WT * L2Q_WAVE) void k_pf_gemm3(
                             for (int e = 0; e < 4; e++) {
                                 const int dv = pn.d[g][j][i][e];
                                 acc[j][i][e] = __builtin_fmaf(
-                                    wr[e], __builtin_fmaf(pn.sc[g][j].x, (float)(BITS == 4 ? dv >> 4 : dv), -pn.sc[g][j].y),
+                                    wr[e], __builtin_fmaf(pn.sc[g][j].x, (float)dv, -pn.sc[g][j].y),
                                     acc[j][i][e]);
                             }
                         }
