@@ -401,6 +401,7 @@ __global__ __launch_bounds__(WR * WT * L2Q_WAVE) void k_pf_gemm3(
         // the lanes of the token (xor 16 / 32) and the WR row-waves (LDS),
         // Q8 as k_swiglu_quant quantizes (runq.c:117-139)
         static_assert(TPW == 1 && P::RT == 2 * G, "one token tile per wave, one group per workgroup");
+        static_assert(2 * WT * WR * 16 * sizeof(float) <= P::STAGE, "the exchange fits in stage buffer 0");
         const int t = t0 + tw0 + l16;
         const bool tin = nj > 0 && t < T;
         float gv[RTW][2];
