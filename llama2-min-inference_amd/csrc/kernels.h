@@ -53,7 +53,7 @@ template <int G>
 __global__ __launch_bounds__(kNormThreads) void k_rmsnorm_quant(
     const float* __restrict__ x, const float* __restrict__ emb, const int* __restrict__ meta,
     const float* __restrict__ resid, float* __restrict__ xout, const float* __restrict__ w, int n,
-    int8_t* __restrict__ xq, float* __restrict__ xs, PfOperand pf) {
+    int8_t* __restrict__ xq, float* __restrict__ xs) {
     __shared__ float vs[kNormThreads * kNormMaxPer];
     __shared__ float inv_s;
     const int tid = threadIdx.x;
@@ -63,8 +63,8 @@ __global__ __launch_bounds__(kNormThreads) void k_rmsnorm_quant(
         x += to;
         if (resid) resid += to;
         if (xout) xout += to;
-        if (xq) xq += to;
-        if (xs) xs += to / G;
+        xq += to;
+        xs += to / G;
     }
     const float* src = emb ? emb + (size_t)meta[0] * n : x;
     float v[kNormMaxPer], wv[kNormMaxPer];
@@ -95,11 +95,10 @@ __global__ __launch_bounds__(kNormThreads) void k_rmsnorm_quant(
         const float o = in ? wv[k] * (inv * v[k]) : 0.0f;
         const float s = q8_scale(group_max<G>(fabsf(o)));
         const int q = q8_value_fast(o, s, q8_recip(s));
-        if (pf.xqp) pf_emit<G>(pf, blockIdx.x, i, q, s, in);
         if (in) {
             if (xout) xout[i] = v[k];
-            if (xq) xq[i] = (int8_t)q;
-            if (xs && (i % G) == 0) xs[i / G] = s;
+            xq[i] = (int8_t)q;
+            if ((i % G) == 0) xs[i / G] = s;
         }
     }
 }

@@ -28,6 +28,8 @@ int launch_quantize(const float* x, int n, int group, int8_t* xq, float* xs, hip
 
 // emb/meta: layer-0 form (x = emb[meta[0]]); otherwise x.
 // T > 1: T consecutive vectors of n (x, resid, xout, xq rows of n; xs rows of n/group).
+// pf: the prefill GEMM operand form (k_pf_rmsnorm_quant): the operand is the
+// only quantized output (xq, xs, emb null), pointers 16-byte aligned.
 int launch_rmsnorm_quant(const float* x, const float* emb, const int* meta, const float* resid,
                          float* xout, const float* w, int n, int group, int8_t* xq, float* xs,
                          hipStream_t st, int T = 1, const PfOperand* pf = nullptr);

@@ -240,12 +240,15 @@ int launch_rmsnorm_quant(const float* x, const float* emb, const int* meta, cons
         set_error("rmsnorm_quant: bad n=%d group=%d T=%d", n, group, T);
         return L2Q_ERR_ARG;
     }
-    PfOperand po;
-    if (int rc = pf_operand(pf, xq, xs, n, T, &po, "rmsnorm_quant")) return rc;
-    if (pf && !emb && !xq && !xs && n % 4 == 0 && n <= kPfNormThreads * kPfNormMaxChunks * 4 &&
-        reinterpret_cast<uintptr_t>(x) % 16 == 0 && reinterpret_cast<uintptr_t>(resid) % 16 == 0 &&
-        reinterpret_cast<uintptr_t>(xout) % 16 == 0 && reinterpret_cast<uintptr_t>(w) % 16 == 0) {
-        // the GEMM operand alone (prefill): float4 chunks, each token on kPfNormSplit workgroups
+    if (pf) {
+        // the GEMM operand of a prefill batch: float4 chunks, each token on kPfNormSplit workgroups
+        PfOperand po;
+        if (int rc = pf_operand(pf, nullptr, nullptr, n, T, &po, "rmsnorm_quant")) return rc;
+        if (emb || xq || xs || reinterpret_cast<uintptr_t>(x) % 16 || reinterpret_cast<uintptr_t>(resid) % 16 ||
+            reinterpret_cast<uintptr_t>(xout) % 16 || reinterpret_cast<uintptr_t>(w) % 16) {
+            set_error("rmsnorm_quant: the GEMM operand form takes 16-byte aligned x, resid, xout, w and no other output");
+            return L2Q_ERR_ARG;
+        }
         const dim3 grid(kPfNormSplit, (unsigned)T);
         if (group == 32)
             hipLaunchKernelGGL(k_pf_rmsnorm_quant<32>, grid, dim3(kPfNormThreads), 0, st, x, resid, xout, w, n, po);
@@ -253,10 +256,11 @@ int launch_rmsnorm_quant(const float* x, const float* emb, const int* meta, cons
             hipLaunchKernelGGL(k_pf_rmsnorm_quant<64>, grid, dim3(kPfNormThreads), 0, st, x, resid, xout, w, n, po);
         return check_launch("prefill_rmsnorm_quant");
     }
+    if (!xq || !xs) { set_error("rmsnorm_quant: no output"); return L2Q_ERR_ARG; }
     if (group == 32)
-        hipLaunchKernelGGL(k_rmsnorm_quant<32>, dim3(T), dim3(kNormThreads), 0, st, x, emb, meta, resid, xout, w, n, xq, xs, po);
+        hipLaunchKernelGGL(k_rmsnorm_quant<32>, dim3(T), dim3(kNormThreads), 0, st, x, emb, meta, resid, xout, w, n, xq, xs);
     else
-        hipLaunchKernelGGL(k_rmsnorm_quant<64>, dim3(T), dim3(kNormThreads), 0, st, x, emb, meta, resid, xout, w, n, xq, xs, po);
+        hipLaunchKernelGGL(k_rmsnorm_quant<64>, dim3(T), dim3(kNormThreads), 0, st, x, emb, meta, resid, xout, w, n, xq, xs);
     return check_launch("rmsnorm_quant");
 }
 
