@@ -596,16 +596,21 @@ void pf3_swiglu(const uint8_t* w, const float* ws, int rows, int cols, const int
 // shapes, T = 127: qkv and w1|w3 wide, wo and w2 small (other shapes
 // tried: 64 x 64 with 4 waves of 32 x 32, 32 x 64 with 16 x 32, 8-wave
 // 64 x 128 and 128 x 64, one to eight groups per step, 3 to 5 stages).
-// Workgroup tiles (rows x tokens): wide 64 x 64 (8 waves), mid 64 x 32 (8
-// waves), small 32 x 32 (4 waves); the largest that still gives every CU a
-// workgroup (fewer re-reads of the activations and weights).
-enum PfShape { kPfWide, kPfMid, kPfSmall };
+// Workgroup tiles (rows x tokens): wide 64 x 64 (8 waves of 32 x 16) when
+// its grid gives every CU two workgroups; narrow 64 x 32 (4 waves of 16 x 32:
+// a wave's unpacked weights serve two token tiles, and the finer grid fills
+// the CUs more evenly: the 7B qkv at 127 tokens 32.8 vs 35.3 us); then mid
+// 64 x 32 (8 waves of 16 x 16) and small 32 x 32 (4 waves), the largest that
+// still gives every CU a workgroup (fewer re-reads of activations and weights).
+enum PfShape { kPfWide, kPfNarrow, kPfMid, kPfSmall };
 
 template <int B_, int G_, int EPI>
 void pf3_shape(PfShape shp, const uint8_t* w, const float* ws, int rows, int cols, const int8_t* xqp,
                const PfRecord* rec, int T, float* out, int ldo, const PfRope& rp, hipStream_t st) {
     if (shp == kPfWide)
         pf3_launch<B_, G_, 2, 1, 2, 4, 2 * G_, 3, false, EPI>(w, ws, rows, cols, xqp, rec, T, out, ldo, rp, st);
+    else if (shp == kPfNarrow)
+        pf3_launch<B_, G_, 1, 2, 4, 1, 2 * G_, 3, false, EPI>(w, ws, rows, cols, xqp, rec, T, out, ldo, rp, st);
     else if (shp == kPfMid)
         pf3_launch<B_, G_, 1, 1, 4, 2, 4 * G_, 4, false, EPI>(w, ws, rows, cols, xqp, rec, T, out, ldo, rp, st);
     else
@@ -636,14 +641,14 @@ int launch_pf_gemm(int bits, int group, const void* w, const float* ws, int rows
         set_error("prefill gemm: weights, activations and records must be 16-byte aligned (rows of 16n bytes)");
         return L2Q_ERR_ARG;
     }
-    // the largest tile that gives every CU a workgroup
+    // the tile by how many workgroups its grid gives each CU (see PfShape)
     int ncu = 0, dev = 0;
     if (hipGetDevice(&dev) != hipSuccess ||
         hipDeviceGetAttribute(&ncu, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || ncu <= 0)
         ncu = 256;
     const long long wg_wide = (long long)((rows + 63) / 64) * ((T + 63) / 64);
     const long long wg_mid = (long long)((rows + 63) / 64) * ((T + 31) / 32);
-    const PfShape shp = wg_wide >= ncu ? kPfWide : wg_mid >= ncu ? kPfMid : kPfSmall;
+    const PfShape shp = wg_wide >= 2 * ncu ? kPfWide : wg_wide >= ncu ? kPfNarrow : wg_mid >= ncu ? kPfMid : kPfSmall;
     const uint8_t* wb = static_cast<const uint8_t*>(w);
     if (swiglu) {
         const PfOperand& so = *swiglu;
