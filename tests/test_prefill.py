@@ -116,13 +116,15 @@ def test_engine_prefill_7b_shape_int4_g64(gpu_lib):
     prefill_then_greedy(ck, prompt, 4, 64)
 
 
-@pytest.mark.parametrize("bits,group", [(4, 64), (8, 32)])
+@pytest.mark.parametrize("bits,group", [(4, 64), (8, 32), (8, 64), (4, 32)])
 @pytest.mark.parametrize("n_prompt,split", [(300, None), (200, 150)])
 def test_engine_prefill_fused_attention_chunks(gpu_lib, bits, group, n_prompt, split):
     """Head size 128 (the fused softmax + p*V + quantize attention): a
     300-position prompt prefills in chunks at positions 0, 128 (contexts of
     up to 256: the fused kernel) and 256 (the three-kernel path); a second
-    call at pos0 = 150 mixes both; bit-exact against the oracle."""
+    call at pos0 = 150 mixes both; bit-exact against the oracle.  The four
+    bit widths x group sizes also cover every form of the w1|w3 GEMM's
+    SwiGLU + Q8 stores."""
     print(f"prefill hs128 bits={bits} group={group} n={n_prompt} split={split}", flush=True)
     cfg = host.make_config(512, 1024, 2, 4, 4, 32000, 512)
     ck = host.synth_checkpoint(cfg, bits, group, seed=31 + bits, q4_divisor=7.0)
