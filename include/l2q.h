@@ -111,9 +111,11 @@ int l2q_engine_create(const l2q_config* cfg, const void* weights,
  * layer together (chunks of up to 128 tokens; the weights stream once per
  * chunk, group dots on int8 MFMA), leaving the KV cache exactly as n calls
  * of l2q_engine_forward would; if logits is not NULL it receives the logits
- * of the last position, bit-identical to l2q_engine_forward's.  Replaces the
- * prompt-forcing loop of generate() (runq.c:695-700, v5-cuda-fused/run.cu:
- * 969-974) and the batched forward of v2-cuda/run.cu:347-394. */
+ * of the last position, bit-identical to l2q_engine_forward's (also with
+ * L2Q_ENGINE_KV_INT8: the rows are appended and each query attends as its
+ * decode step would).  Replaces the prompt-forcing loop of generate()
+ * (runq.c:695-700, v5-cuda-fused/run.cu:969-974) and the batched forward of
+ * v2-cuda/run.cu:347-394. */
 int l2q_engine_prefill(l2q_engine* e, const int* tokens, int n, int pos0,
                        float* logits);
 

@@ -223,12 +223,14 @@ struct PfOperand {
 // kv_dim) k and the rest v of token t at position pos0 + t; q and k pairs
 // (2i, 2i + 1) are rotated as k_rope_kv_append rotates them (runq.c:
 // 351-365) — q stored to out, k and v appended to the caches — so no
-// separate RoPE / append launch follows.
+// separate RoPE / append launch follows.  Token t is rotated for position
+// pos0 + t and stored to cache row row0 + t (row0 = pos0 for the KV cache;
+// 0 for a staging buffer of the chunk's rows).
 struct PfRope {
     const float* rope;
     float* kcache;
     float* vcache;
-    int pos0, dim, kv_dim, hs, max_t, k_il;
+    int pos0, dim, kv_dim, hs, max_t, k_il, row0;
 };
 
 // The record: xt = q8_bias_term(xs, sum(q)) (runq.c:137) and c =

@@ -95,6 +95,7 @@ struct l2q_engine {
     int pf_T = 0;
     float *pf_xa, *pf_xb, *pf_qkv, *pf_att, *pf_wo, *pf_ffn, *pf_scores;
     int8_t *pf_xqp, *pf_xqh;           // GEMM operands: d-wide, and w2's h-wide one (written by w1|w3)
+    float* pf_kvst;                    // int8 KV cache: the chunk's rotated k, v rows [2][n_kv][pf_T][hs]
     l2q::PfRecord *pf_rec, *pf_rech;
     int* pf_tok;
 };
@@ -566,6 +567,7 @@ int prefill_alloc(l2q_engine* e) {
     const size_t o_xqp = a.take(T * kmax), o_rec = a.take(T * nbmax * sizeof(PfRecord));
     const size_t o_xqh = a.take(T * h), o_rech = a.take(T * (h / e->G) * sizeof(PfRecord));
     const size_t o_tok = a.take(T * 4);
+    const size_t o_kvst = a.take((e->flags & L2Q_ENGINE_KV_INT8) ? 2 * T * kv * 4 : 0);
     HIPCHK(hipMalloc(&e->pfarena, align_up(a.used, 256)), "hipMalloc(prefill)");
     char* P = e->pfarena;
     e->pf_xa = (float*)(P + o_xa); e->pf_xb = (float*)(P + o_xb); e->pf_qkv = (float*)(P + o_qkv);
@@ -574,6 +576,7 @@ int prefill_alloc(l2q_engine* e) {
     e->pf_xqp = (int8_t*)(P + o_xqp); e->pf_rec = (PfRecord*)(P + o_rec);
     e->pf_xqh = (int8_t*)(P + o_xqh); e->pf_rech = (PfRecord*)(P + o_rech);
     e->pf_tok = (int*)(P + o_tok);
+    e->pf_kvst = (e->flags & L2Q_ENGINE_KV_INT8) ? (float*)(P + o_kvst) : nullptr;
     e->pf_T = (int)T;
     return L2Q_OK;
 }
@@ -596,22 +599,54 @@ int prefill_chunk(l2q_engine* e, const int* tokens, int T, int pos0, bool want_l
                     const PfRope* rp = nullptr, const PfOperand* sw = nullptr) {
         return launch_pf_gemm(bits, G, w, ws, rows, in.K, in.xqp, in.rec, T, out, rows, st, rp, sw);
     };
+    const bool kv8 = e->flags & L2Q_ENGINE_KV_INT8;
+    // int8 KV cache: queries whose decode step runs the one-workgroup-per-
+    // head kernel (positions up to the engine's switch), the rest split
+    int nfused = 0;
+    if (kv8)
+        while (nfused < T && step_graph(e, false, pos0 + nfused) == e->exec[0][0]) nfused++;
     for (int l = 0; l < c.n_layers; l++) {
-        float* kc = e->kcache + (size_t)l * kv * e->max_t;
-        float* vc = e->vcache + (size_t)l * kv * e->max_t;
         // x = (l == 0 ? emb rows : xa + ffn) -> xb; RMSNorm; q, k, v; RoPE + append; attention
         if ((rc = launch_rmsnorm_quant(e->pf_xa, nullptr, nullptr, l == 0 ? nullptr : e->pf_ffn, e->pf_xb,
                                        e->rms_att + (size_t)l * d, d, G, nullptr, nullptr, st, T, &pod)))
             return rc;
-        // q, k, v rows with RoPE and the KV append fused into the GEMM's stores
-        const PfRope rp{e->rope, kc, vc, pos0, d, kv, e->hs, e->max_t, 1};
-        if ((rc = gemm(e->qkv_w + (size_t)l * qkv_rows * e->rowb_d, e->qkv_s + (size_t)l * qkv_rows * nbd, qkv_rows,
-                       pod, e->pf_qkv, &rp)))
-            return rc;
-        // attention, its output quantized into the wo operand
-        if ((rc = launch_attention_prefill(e->pf_qkv, kc, vc, e->pf_att, e->pf_scores, pos0, c.n_heads, c.n_kv_heads,
-                                           e->hs, e->max_t, st, T, qkv_rows, 1, G, &pod)))
-            return rc;
+        const uint8_t* wqkv = e->qkv_w + (size_t)l * qkv_rows * e->rowb_d;
+        const float* sqkv = e->qkv_s + (size_t)l * qkv_rows * nbd;
+        if (kv8) {
+            // q, and the rotated k, v rows to the chunk's staging; the decode
+            // step's int8 append (k_kv8_append) of every row; then each query's
+            // attention as its decode step runs it (the appended rows read back)
+            const size_t co = (size_t)l * kv * e->max_t, so = (size_t)l * c.n_kv_heads * e->max_t;
+            float* stk = e->pf_kvst;
+            float* stv = e->pf_kvst + (size_t)e->pf_T * kv;
+            const PfRope rp{e->rope, stk, stv, pos0, d, kv, e->hs, e->pf_T, 0, 0};
+            if ((rc = gemm(wqkv, sqkv, qkv_rows, pod, e->pf_qkv, &rp))) return rc;
+            if ((rc = launch_kv8_append(stk, stv, e->k8 + co, e->v8 + co, e->ks + so, e->vs + so, nullptr, nullptr,
+                                        pos0, c.n_kv_heads, e->hs, e->max_t, st, T, e->pf_T)))
+                return rc;
+            if (nfused &&
+                (rc = launch_attention_kv8(e->pf_qkv, e->k8 + co, e->v8 + co, e->ks + so, e->vs + so, e->pf_att,
+                                           nullptr, nullptr, pos0, c.n_heads, c.n_kv_heads, e->hs, e->max_t, st,
+                                           nullptr, nullptr, nfused, qkv_rows, d)))
+                return rc;
+            for (int t = nfused; t < T; t++)
+                if ((rc = launch_attention_kv8_split(e->pf_qkv + (size_t)t * qkv_rows, nullptr, nullptr, e->k8 + co,
+                                                     e->v8 + co, e->ks + so, e->vs + so, e->pf_att + (size_t)t * d,
+                                                     e->apart, e->acnt, e->aS, nullptr, pos0 + t, c.n_heads,
+                                                     c.n_kv_heads, e->hs, e->max_t, st)))
+                    return rc;
+            if ((rc = launch_quantize(e->pf_att, T * d, G, nullptr, nullptr, st, &pod))) return rc;
+        } else {
+            float* kc = e->kcache + (size_t)l * kv * e->max_t;
+            float* vc = e->vcache + (size_t)l * kv * e->max_t;
+            // q, k, v rows with RoPE and the KV append fused into the GEMM's stores
+            const PfRope rp{e->rope, kc, vc, pos0, d, kv, e->hs, e->max_t, 1, pos0};
+            if ((rc = gemm(wqkv, sqkv, qkv_rows, pod, e->pf_qkv, &rp))) return rc;
+            // attention, its output quantized into the wo operand
+            if ((rc = launch_attention_prefill(e->pf_qkv, kc, vc, e->pf_att, e->pf_scores, pos0, c.n_heads,
+                                               c.n_kv_heads, e->hs, e->max_t, st, T, qkv_rows, 1, G, &pod)))
+                return rc;
+        }
         // wo
         if ((rc = gemm(e->wo_w + (size_t)l * d * e->rowb_d, e->wo_s + (size_t)l * d * nbd, d, pod, e->pf_wo))) return rc;
         // x = xb + wo -> xa; RMSNorm; SwiGLU(w1 x, w3 x); w2
@@ -653,11 +688,6 @@ int l2q_engine_prefill(l2q_engine* e, const int* tokens, int n, int pos0, float*
     for (int i = 0; i < n; i++)
         if (tokens[i] < 0 || tokens[i] >= e->cfg.vocab_size) { set_error("engine: token %d out of range", tokens[i]); return L2Q_ERR_ARG; }
     int rc;
-    if (e->flags & L2Q_ENGINE_KV_INT8) {   // int8 KV cache: the decode step per token (same results)
-        for (int i = 0; i < n; i++)
-            if ((rc = l2q_engine_forward(e, tokens[i], pos0 + i, i == n - 1 ? logits : nullptr))) return rc;
-        return L2Q_OK;
-    }
     if ((rc = prefill_alloc(e))) return rc;
     for (int i0 = 0; i0 < n; i0 += e->pf_T) {
         const int T = n - i0 < e->pf_T ? n - i0 : e->pf_T;

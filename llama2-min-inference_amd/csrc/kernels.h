@@ -1271,11 +1271,14 @@ __device__ __forceinline__ void kv8_quant_row(const float* __restrict__ src, con
 __global__ __launch_bounds__(L2Q_WAVE) void k_kv8_append(
     const float* __restrict__ k, const float* __restrict__ v, int8_t* __restrict__ k8, int8_t* __restrict__ v8,
     float* __restrict__ ks, float* __restrict__ vs, const float* __restrict__ rope, const int* __restrict__ meta,
-    int pos_arg, int hs, int max_t) {
+    int pos_arg, int hs, int max_t, int src_rows) {
+    // row blockIdx.z of k / v ([n_kv][src_rows][hs]; a decode step: one row)
+    // to cache position pos + blockIdx.z
     const int g = blockIdx.x, isv = blockIdx.y, lane = threadIdx.x;
-    const int pos = meta_pos(meta, pos_arg);
+    const int pos = meta_pos(meta, pos_arg) + blockIdx.z;
     const size_t row = (size_t)g * max_t + pos;
-    kv8_quant_row<false>((isv ? v : k) + (size_t)g * hs, isv ? nullptr : rope, pos, hs, lane, (isv ? v8 : k8) + row * hs,
+    const size_t src = ((size_t)g * src_rows + blockIdx.z) * hs;
+    kv8_quant_row<false>((isv ? v : k) + src, isv ? nullptr : rope, pos, hs, lane, (isv ? v8 : k8) + row * hs,
                   (isv ? vs : ks) + row, nullptr, nullptr);
 }
 
@@ -1314,7 +1317,8 @@ __host__ __device__ constexpr size_t attn8_fused_lds_bytes(int max_t) {
 __global__ __launch_bounds__(kA8Threads) void k_attn8_fused(
     const float* __restrict__ q, const float* __restrict__ kst, const float* __restrict__ vst,
     int8_t* __restrict__ k8, int8_t* __restrict__ v8, float* __restrict__ ks, float* __restrict__ vs,
-    float* __restrict__ out, const int* __restrict__ meta, int pos_arg, int kv_mul, int hs, int max_t) {
+    float* __restrict__ out, const int* __restrict__ meta, int pos_arg, int kv_mul, int hs, int max_t,
+    int q_stride, int out_stride) {
     extern __shared__ __attribute__((aligned(16))) float smf[];
     float* sc = smf;                                   // [max_t] scores, then e_t * vs_t
     float* part = sc + (max_t + 3) / 4 * 4;            // [slices][hs] partial sums
@@ -1324,7 +1328,11 @@ __global__ __launch_bounds__(kA8Threads) void k_attn8_fused(
     uint64_t* etab = reinterpret_cast<uint64_t*>(vrow + kAttnMaxHs);   // [32] exp table
     const int h = blockIdx.x, hk = h / kv_mul;
     const int tid = threadIdx.x, lane = tid & (L2Q_WAVE - 1), wv = tid / L2Q_WAVE, sub = tid & 3;
-    const int pos = meta_pos(meta, pos_arg);
+    // query blockIdx.y of a batch (prefill): position pos + blockIdx.y, its q
+    // row and output row at the given strides (a decode step: one query)
+    const int pos = meta_pos(meta, pos_arg) + blockIdx.y;
+    q += (size_t)blockIdx.y * q_stride;
+    out += (size_t)blockIdx.y * out_stride;
     const int n = pos + 1;
     const bool append = kst != nullptr;
     const size_t prow = (size_t)hk * max_t + pos;

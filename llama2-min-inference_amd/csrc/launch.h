@@ -86,15 +86,18 @@ int attention_fused_max();
 
 // int8 KV cache: append one position / attention over positions 0..pos.
 bool kv8_shape_ok(int n_heads, int n_kv_heads, int hs, int max_t);
+// nrows > 1: rows [n_kv][src_rows][hs] of k / v (the first nrows of each
+// head) to positions pos.. (no meta).
 int launch_kv8_append(const float* k, const float* v, int8_t* k8, int8_t* v8, float* ks, float* vs,
                       const float* rope, const int* meta, int pos, int n_kv_heads, int hs, int max_t,
-                      hipStream_t st);
+                      hipStream_t st, int nrows = 1, int src_rows = 1);
 // The one-kernel int8-cache attention (k_attn8_fused).  With kst / vst (the
 // step's rotated k and v rows, [n_kv][hs]) it first appends position pos to
 // the caches (the k_kv8_append operations); without them it only reads.
 int launch_attention_kv8(const float* q, int8_t* k8, int8_t* v8, float* ks, float* vs, float* out, float* scores,
                          const int* meta, int pos, int n_heads, int n_kv_heads, int hs, int max_t, hipStream_t st,
-                         const float* kst = nullptr, const float* vst = nullptr);
+                         const float* kst = nullptr, const float* vst = nullptr, int nq = 1, int q_stride = 0,
+                         int out_stride = 0);
 
 // Score workgroups for n positions: ~128 positions each, at most 64.
 inline int score_splits(int n) {

@@ -490,22 +490,24 @@ bool kv8_shape_ok(int n_heads, int n_kv_heads, int hs, int max_t) {
 
 int launch_kv8_append(const float* k, const float* v, int8_t* k8, int8_t* v8, float* ks, float* vs,
                       const float* rope, const int* meta, int pos, int n_kv_heads, int hs, int max_t,
-                      hipStream_t st) {
+                      hipStream_t st, int nrows, int src_rows) {
     if (!kv8_shape_ok(n_kv_heads, n_kv_heads, hs, max_t) || (!meta && (pos < 0 || pos >= max_t)) || !k || !v ||
-        !k8 || !v8 || !ks || !vs) {
-        set_error("kv8 append: bad arguments kv_heads=%d hs=%d pos=%d max_t=%d", n_kv_heads, hs, pos, max_t);
+        !k8 || !v8 || !ks || !vs || nrows < 1 || nrows > 65535 || src_rows < nrows ||
+        (nrows > 1 && (meta || pos + nrows > max_t))) {
+        set_error("kv8 append: bad arguments kv_heads=%d hs=%d pos=%d max_t=%d rows=%d", n_kv_heads, hs, pos, max_t,
+                  nrows);
         return L2Q_ERR_ARG;
     }
-    hipLaunchKernelGGL(k_kv8_append, dim3(n_kv_heads, 2), dim3(L2Q_WAVE), 0, st, k, v, k8, v8, ks, vs, rope, meta,
-                       pos, hs, max_t);
+    hipLaunchKernelGGL(k_kv8_append, dim3(n_kv_heads, 2, nrows), dim3(L2Q_WAVE), 0, st, k, v, k8, v8, ks, vs, rope,
+                       meta, pos, hs, max_t, src_rows);
     return check_launch("kv8_append");
 }
 
 int launch_attention_kv8(const float* q, int8_t* k8, int8_t* v8, float* ks, float* vs, float* out, float* scores,
                          const int* meta, int pos, int n_heads, int n_kv_heads, int hs, int max_t, hipStream_t st,
-                         const float* kst, const float* vst) {
+                         const float* kst, const float* vst, int nq, int q_stride, int out_stride) {
     if (!kv8_shape_ok(n_heads, n_kv_heads, hs, max_t) || (!meta && (pos < 0 || pos >= max_t)) ||
-        (!kst != !vst)) {
+        (!kst != !vst) || nq < 1 || nq > 65535 || (nq > 1 && (kst || meta || pos + nq > max_t))) {
         set_error("attention kv8: bad shape heads=%d kv_heads=%d hs=%d pos=%d max_t=%d", n_heads, n_kv_heads, hs,
                   pos, max_t);
         return L2Q_ERR_ARG;
@@ -516,8 +518,8 @@ int launch_attention_kv8(const float* q, int8_t* k8, int8_t* v8, float* ks, floa
     if (int rc = raise_lds_limit(reinterpret_cast<const void*>(&k_attn8_fused), lds,
                                  "attention kv8: raising the LDS limit"))
         return rc;
-    hipLaunchKernelGGL(k_attn8_fused, dim3(n_heads), dim3(kA8Threads), lds, st, q, kst, vst, k8, v8, ks, vs, out,
-                       meta, pos, kv_mul, hs, max_t);
+    hipLaunchKernelGGL(k_attn8_fused, dim3(n_heads, nq), dim3(kA8Threads), lds, st, q, kst, vst, k8, v8, ks, vs, out,
+                       meta, pos, kv_mul, hs, max_t, q_stride, out_stride);
     return check_launch("attention_kv8");
 }
 
@@ -666,7 +668,7 @@ int launch_pf_gemm(int bits, int group, const void* w, const float* ws, int rows
     if (rope) {
         const PfRope& r = *rope;
         if (!r.rope || !r.kcache || !r.vcache || r.hs <= 0 || r.hs % 2 || r.dim % r.hs || r.kv_dim % r.hs ||
-            r.kv_dim > r.dim || rows != r.dim + 2 * r.kv_dim || r.pos0 < 0 || r.pos0 + T > r.max_t ||
+            r.kv_dim > r.dim || rows != r.dim + 2 * r.kv_dim || r.pos0 < 0 || r.row0 < 0 || r.row0 + T > r.max_t ||
             (r.k_il && r.hs % 4)) {
             set_error("prefill gemm: bad RoPE/KV epilogue arguments");
             return L2Q_ERR_ARG;

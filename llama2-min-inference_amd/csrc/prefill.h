@@ -476,7 +476,7 @@ __global__ __launch_bounds__(WR * WT * L2Q_WAVE) void k_pf_gemm3(
             float* o = out + (size_t)t * ldo + r;
             if constexpr (EPI == 1) {
                 // pairs (r, r + 1), (r + 2, r + 3): r is a multiple of 4
-                const int pos = rp.pos0 + t;
+                const int pos = rp.pos0 + t, crow = rp.row0 + t;
 #pragma unroll
                 for (int m = 0; m < 2; m++) {
                     const int rr = r + 2 * m;
@@ -493,13 +493,13 @@ __global__ __launch_bounds__(WR * WT * L2Q_WAVE) void k_pf_gemm3(
                             o[2 * m] = a0;
                             o[2 * m + 1] = a1;
                         } else {
-                            const size_t ko = k_index(rp.k_il, e / rp.hs, pos, hd, rp.hs, rp.max_t);
+                            const size_t ko = k_index(rp.k_il, e / rp.hs, crow, hd, rp.hs, rp.max_t);
                             rp.kcache[ko] = a0;
                             rp.kcache[ko + 1] = a1;
                         }
                     } else {
                         const int e = rr - rp.dim - rp.kv_dim;
-                        const size_t vo = ((size_t)(e / rp.hs) * rp.max_t + pos) * rp.hs + e % rp.hs;
+                        const size_t vo = ((size_t)(e / rp.hs) * rp.max_t + crow) * rp.hs + e % rp.hs;
                         rp.vcache[vo] = v0;
                         rp.vcache[vo + 1] = v1;
                     }

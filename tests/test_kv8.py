@@ -324,3 +324,54 @@ def test_gpu_engine_kv8_follows_oracle(gpu_lib, torch_cuda, shape):
         token = int(np.argmax(lo))
     eng.close()
     orc.close()
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("shape", ["c1_q8_g32", "7b2_q4_g64", "gqa_hs64_q4_g32", "c1_q8_g32_long"])
+def test_gpu_engine_kv8_prefill_follows_oracle(gpu_lib, torch_cuda, shape):
+    """The batched prefill with the int8 KV cache: the qkv GEMM stages the
+    rotated k, v rows, the decode step's int8 quantizer appends them, and
+    each query's attention is the kernel its decode step would run (one
+    workgroup per head up to L2Q_KV8_SPLIT_FROM positions, split beyond).
+    The prompt's last logits and the greedy steps after it equal the
+    oracle's int8-KV forward bit for bit; the long case prefills 1060
+    positions in two calls, the second chunk straddling the switch."""
+    from llama2q.model import Engine
+    split = None
+    if shape == "c1_q8_g32":
+        ck = host.synth_checkpoint(host.config_15m(), 8, 32, seed=21)
+        n_prompt, steps = 40, 64
+    elif shape == "c1_q8_g32_long":
+        cfg = host.make_config(288, 768, 2, 6, 6, 512, 2048)
+        ck = host.synth_checkpoint(cfg, 8, 32, seed=25)
+        n_prompt, steps, split = 1060, 1080, 1000
+    elif shape == "gqa_hs64_q4_g32":
+        cfg = host.make_config(256, 512, 2, 4, 2, 512, 64)
+        ck = host.synth_checkpoint(cfg, 4, 32, seed=24, q4_divisor=7.0)
+        n_prompt, steps = 30, 40
+    else:
+        cfg = host.make_config(4096, 11008, 2, 32, 32, 32000, 4096)
+        ck = host.synth_checkpoint(cfg, 4, 64, seed=22, q4_divisor=7.0)
+        n_prompt, steps = 9, 12
+    print(f"engine kv8 prefill {shape}", flush=True)
+    vocab = ck.cfg.as_list()[5]
+    prompt = [int(v) for v in host.uniform_ints(n_prompt, 27, 100, 3, vocab)]
+    eng = Engine(ck, max_steps=steps, kv8=True)
+    orc = O.Oracle(ck.cfg.as_list(), ck.weights, ck.wbits, ck.group, max_t=steps, kv8=True,
+                   kv8_splits=eng.attention_splits, kv8_split_from=abi.L2Q_KV8_SPLIT_FROM)
+    for pos, tok in enumerate(prompt):
+        lo = orc.forward(tok, pos)
+    if split:
+        eng.prefill(prompt[:split], 0, logits=False)
+        lg = eng.prefill(prompt[split:], split)
+    else:
+        lg = eng.prefill(prompt, 0)
+    np.testing.assert_array_equal(lg, lo, err_msg="last prompt position")
+    token = int(np.argmax(lo))
+    for pos in range(n_prompt, steps):
+        lo = orc.forward(token, pos)
+        lg = eng.forward(token, pos)
+        np.testing.assert_array_equal(lg, lo, err_msg=f"pos {pos}")
+        token = int(np.argmax(lo))
+    eng.close()
+    orc.close()
