@@ -699,11 +699,13 @@ __host__ __device__ constexpr size_t attn_softmax_b_lds_bytes(int max_t) {
     return ((size_t)(max_t + 3) / 4 * 4 + kRingSlack + 4) * sizeof(float);
 }
 __global__ __launch_bounds__(kSmThreads) void k_attn_softmax_b(float* __restrict__ scores, int pos0, int n_heads,
-                                                               int max_t) {
+                                                               int max_t, int nmax) {
 #pragma clang fp contract(off)
+    // LDS sized for the launch's longest row, nmax = pos0 + T (not the
+    // cache's max_t): more of these one-wave workgroups fit on a CU
     extern __shared__ __attribute__((aligned(16))) float sm[];
     float* p = sm;                                         // [n] e_t
-    float* red = sm + (max_t + 3) / 4 * 4 + kRingSlack;    // [1] sum
+    float* red = sm + (nmax + 3) / 4 * 4 + kRingSlack;     // [1] sum
     const int qi = blockIdx.x, h = blockIdx.y, lane = threadIdx.x;
     const int n = pos0 + qi + 1;
     float* row = scores + ((size_t)qi * n_heads + h) * attn_b_pitch(max_t);

@@ -431,8 +431,8 @@ int launch_attention_exact(const float* q, const float* kcache, const float* vca
         // operations, same order as the per-query kernels below)
         int rc = launch_attention_scores_b(q, kcache, scores, pos, T, kv_mul, n_heads, hs, max_t, q_stride, k_il, st);
         if (rc) return rc;
-        hipLaunchKernelGGL(k_attn_softmax_b, dim3(T, n_heads), dim3(kSmThreads), attn_softmax_b_lds_bytes(max_t), st,
-                           scores, pos, n_heads, max_t);
+        hipLaunchKernelGGL(k_attn_softmax_b, dim3(T, n_heads), dim3(kSmThreads), attn_softmax_b_lds_bytes(pos + T), st,
+                           scores, pos, n_heads, max_t, pos + T);
         if ((rc = check_launch("attention_softmax_b"))) return rc;
         hipLaunchKernelGGL(k_attn_pv_b, dim3(n_heads, (hs + kVDims - 1) / kVDims, (T + kPvQueries - 1) / kPvQueries),
                            dim3(kPvThreads), 0, st, scores, vcache, out, pos, T, kv_mul, n_heads, hs, max_t);
