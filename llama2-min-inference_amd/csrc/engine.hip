@@ -96,6 +96,8 @@ struct l2q_engine {
     float *pf_xa, *pf_xb, *pf_qkv, *pf_att, *pf_wo, *pf_ffn, *pf_scores;
     int8_t *pf_xqp, *pf_xqh;           // GEMM operands: d-wide, and w2's h-wide one (written by w1|w3)
     float* pf_kvst;                    // int8 KV cache: the chunk's rotated k, v rows [2][n_kv][pf_T][hs]
+    float* pf_apart;                   //   and its split attention's partials, per query of a chunk
+    unsigned* pf_acnt;                 //   and merge counters (zeroed; the kernel leaves them zeroed)
     l2q::PfRecord *pf_rec, *pf_rech;
     int* pf_tok;
 };
@@ -567,7 +569,10 @@ int prefill_alloc(l2q_engine* e) {
     const size_t o_xqp = a.take(T * kmax), o_rec = a.take(T * nbmax * sizeof(PfRecord));
     const size_t o_xqh = a.take(T * h), o_rech = a.take(T * (h / e->G) * sizeof(PfRecord));
     const size_t o_tok = a.take(T * 4);
-    const size_t o_kvst = a.take((e->flags & L2Q_ENGINE_KV_INT8) ? 2 * T * kv * 4 : 0);
+    const bool kv8 = e->flags & L2Q_ENGINE_KV_INT8;
+    const size_t o_kvst = a.take(kv8 ? 2 * T * kv * 4 : 0);
+    const size_t o_apart = a.take(kv8 && e->aS ? T * attention_flash_part_floats(c.n_heads, e->aS, e->hs) * 4 : 0);
+    const size_t o_acnt = a.take(kv8 && e->aS ? T * c.n_heads * sizeof(unsigned) : 0);
     HIPCHK(hipMalloc(&e->pfarena, align_up(a.used, 256)), "hipMalloc(prefill)");
     char* P = e->pfarena;
     e->pf_xa = (float*)(P + o_xa); e->pf_xb = (float*)(P + o_xb); e->pf_qkv = (float*)(P + o_qkv);
@@ -576,7 +581,10 @@ int prefill_alloc(l2q_engine* e) {
     e->pf_xqp = (int8_t*)(P + o_xqp); e->pf_rec = (PfRecord*)(P + o_rec);
     e->pf_xqh = (int8_t*)(P + o_xqh); e->pf_rech = (PfRecord*)(P + o_rech);
     e->pf_tok = (int*)(P + o_tok);
-    e->pf_kvst = (e->flags & L2Q_ENGINE_KV_INT8) ? (float*)(P + o_kvst) : nullptr;
+    e->pf_kvst = kv8 ? (float*)(P + o_kvst) : nullptr;
+    e->pf_apart = kv8 && e->aS ? (float*)(P + o_apart) : nullptr;
+    e->pf_acnt = kv8 && e->aS ? (unsigned*)(P + o_acnt) : nullptr;
+    if (e->pf_acnt) HIPCHK(hipMemset(e->pf_acnt, 0, T * c.n_heads * sizeof(unsigned)), "hipMemset(prefill counters)");
     e->pf_T = (int)T;
     return L2Q_OK;
 }
@@ -629,12 +637,12 @@ int prefill_chunk(l2q_engine* e, const int* tokens, int T, int pos0, bool want_l
                                            nullptr, nullptr, pos0, c.n_heads, c.n_kv_heads, e->hs, e->max_t, st,
                                            nullptr, nullptr, nfused, qkv_rows, d)))
                 return rc;
-            for (int t = nfused; t < T; t++)
-                if ((rc = launch_attention_kv8_split(e->pf_qkv + (size_t)t * qkv_rows, nullptr, nullptr, e->k8 + co,
-                                                     e->v8 + co, e->ks + so, e->vs + so, e->pf_att + (size_t)t * d,
-                                                     e->apart, e->acnt, e->aS, nullptr, pos0 + t, c.n_heads,
-                                                     c.n_kv_heads, e->hs, e->max_t, st)))
-                    return rc;
+            if (nfused < T &&
+                (rc = launch_attention_kv8_split(e->pf_qkv + (size_t)nfused * qkv_rows, nullptr, nullptr, e->k8 + co,
+                                                 e->v8 + co, e->ks + so, e->vs + so, e->pf_att + (size_t)nfused * d,
+                                                 e->pf_apart, e->pf_acnt, e->aS, nullptr, pos0 + nfused, c.n_heads,
+                                                 c.n_kv_heads, e->hs, e->max_t, st, T - nfused, qkv_rows, d)))
+                return rc;
             if ((rc = launch_quantize(e->pf_att, T * d, G, nullptr, nullptr, st, &pod))) return rc;
         } else {
             float* kc = e->kcache + (size_t)l * kv * e->max_t;

@@ -1482,7 +1482,7 @@ __global__ __launch_bounds__(kA8sThreads) void k_attn8_split(
     const float* __restrict__ q, const float* __restrict__ kst, const float* __restrict__ vst,
     int8_t* __restrict__ k8, int8_t* __restrict__ v8, float* __restrict__ ks, float* __restrict__ vs,
     float* __restrict__ out, float* __restrict__ part, unsigned* __restrict__ cnt, const int* __restrict__ meta,
-    int pos_arg, int kv_mul, int hs, int max_t) {
+    int pos_arg, int kv_mul, int hs, int max_t, int q_stride, int out_stride) {
     extern __shared__ __attribute__((aligned(16))) float smf[];
     float* sc = smf;                                   // [C] scores, then e_t * vs_t
     float* psl = sc + kA8sMaxC;                        // [slices][hs] p*V partials, then the partial
@@ -1494,7 +1494,14 @@ __global__ __launch_bounds__(kA8sThreads) void k_attn8_split(
     __shared__ int is_last;
     const int h = blockIdx.x, s = blockIdx.y, S = gridDim.y, hk = h / kv_mul;
     const int tid = threadIdx.x, lane = tid & (L2Q_WAVE - 1), wv = tid / L2Q_WAVE, sub = tid & 3;
-    const int pos = meta_pos(meta, pos_arg);
+    // query blockIdx.z of a batch (prefill): position pos + blockIdx.z, its
+    // q / output rows at the given strides, its own partials and counters
+    // (a decode step: one query)
+    const int pos = meta_pos(meta, pos_arg) + blockIdx.z;
+    q += (size_t)blockIdx.z * q_stride;
+    out += (size_t)blockIdx.z * out_stride;
+    part += (size_t)blockIdx.z * gridDim.x * S * (hs + 2);
+    cnt += (size_t)blockIdx.z * gridDim.x;
     const int n = pos + 1;
     const int C = (n + S - 1) / S;
     const int t0 = min(s * C, n), t1 = min(n, t0 + C), mn = t1 - t0;

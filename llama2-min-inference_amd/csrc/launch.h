@@ -55,9 +55,12 @@ int launch_attention_split(const float* q, const float* kcache, const float* vca
 // int8-KV attention split over the context (S splits, partials and zeroed
 // counters as launch_attention_flash); kst/vst: the step's staged rows to
 // append at pos (or both null).
+// nq > 1: queries pos.. of a batch (q, out rows at the given strides), each
+// with its own attention_flash_part_floats partials and n_heads counters.
 int launch_attention_kv8_split(const float* q, const float* kst, const float* vst, int8_t* k8, int8_t* v8,
                                float* ks, float* vs, float* out, float* part, unsigned* cnt, int S, const int* meta,
-                               int pos, int n_heads, int n_kv_heads, int hs, int max_t, hipStream_t st);
+                               int pos, int n_heads, int n_kv_heads, int hs, int max_t, hipStream_t st, int nq = 1,
+                               int q_stride = 0, int out_stride = 0);
 bool attention_flash_ok(int hs);
 int attention_flash_splits(int n_heads, int max_t, int ncu);
 size_t attention_flash_part_floats(int n_heads, int S, int hs);

@@ -525,11 +525,13 @@ int launch_attention_kv8(const float* q, int8_t* k8, int8_t* v8, float* ks, floa
 
 int launch_attention_kv8_split(const float* q, const float* kst, const float* vst, int8_t* k8, int8_t* v8,
                                float* ks, float* vs, float* out, float* part, unsigned* cnt, int S, const int* meta,
-                               int pos, int n_heads, int n_kv_heads, int hs, int max_t, hipStream_t st) {
+                               int pos, int n_heads, int n_kv_heads, int hs, int max_t, hipStream_t st, int nq,
+                               int q_stride, int out_stride) {
     // positions a launch may cover: any of the cache's under a captured graph
-    const int nmax = meta ? max_t : pos + 1;
+    const int nmax = meta ? max_t : pos + nq;
     if (!kv8_shape_ok(n_heads, n_kv_heads, hs, max_t) || (!meta && (pos < 0 || pos >= max_t)) || (!kst != !vst) ||
-        S < 1 || S > kFlMaxSplits || (nmax + S - 1) / S > kA8sMaxC || !part || !cnt) {
+        S < 1 || S > kFlMaxSplits || (nmax + S - 1) / S > kA8sMaxC || !part || !cnt || nq < 1 || nq > 65535 ||
+        (nq > 1 && (kst || meta || pos + nq > max_t))) {
         set_error("attention kv8 split: bad shape heads=%d kv_heads=%d hs=%d pos=%d max_t=%d S=%d", n_heads,
                   n_kv_heads, hs, pos, max_t, S);
         return L2Q_ERR_ARG;
@@ -538,8 +540,8 @@ int launch_attention_kv8_split(const float* q, const float* kst, const float* vs
     if (int rc = raise_lds_limit(reinterpret_cast<const void*>(&k_attn8_split), lds,
                                  "attention kv8 split: raising the LDS limit"))
         return rc;
-    hipLaunchKernelGGL(k_attn8_split, dim3(n_heads, S), dim3(kA8sThreads), lds, st, q, kst, vst, k8, v8, ks, vs, out,
-                       part, cnt, meta, pos, n_heads / n_kv_heads, hs, max_t);
+    hipLaunchKernelGGL(k_attn8_split, dim3(n_heads, S, nq), dim3(kA8sThreads), lds, st, q, kst, vst, k8, v8, ks, vs,
+                       out, part, cnt, meta, pos, n_heads / n_kv_heads, hs, max_t, q_stride, out_stride);
     return check_launch("attention_kv8_split");
 }
 
